@@ -1,0 +1,297 @@
+"""Benchmark of the HYDRA hot path on one MI355X.
+
+Headline (the JSON `value`): CCGQA attention forward tokens/s at config 3 --
+dim 1024, 4x compression to latent 256, 4 query heads / 1 KV head (hd 64),
+causal conv k=3, QK-mean, QK L2-norm with temperature 1.0, B4 x S4096, bf16,
+random-init N(0, 0.02) weights, N(0,1) activations (seed 0).  A step is one
+full module forward: qkv GEMM -> fused prep kernel -> attention kernel ->
+o_proj GEMM, inputs resident in HBM.
+
+Also reported on the same line:
+  roofline      the attention kernel (dominant), algorithmic FLOPs / its
+                average duration from HIP events over the timed steps;
+  stages        per-stage average durations of the step;
+  fused_ops     config 2 RMSNorm / RoPE / SwiGLU in HBM GB/s and % of peak
+                (buffers rotated over > 512 MB so the 256 MB MALL cannot
+                serve repeats);
+  mod           config 4 top-k / gather / residual scatter;
+  cpu_baseline  the oracle (the reference's PyTorch CPU path restated) on a
+                bounded sample of the same workload, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "CCGQA block fwd tokens/s + fused-op HBM GB/s (% peak), 1xMI355X"
+
+
+def _events(n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+# ----------------------------------------------------------------- config 3
+class C3Step:
+    """One CCGQA attention forward at config 3, stage by stage."""
+
+    def __init__(self, dev, B=4, S=4096, dim=1024, n_heads=4, n_kv_heads=1, comp=4, seed=0):
+        from hydra_amd.attention import CCGQAAttention
+
+        g = torch.Generator().manual_seed(seed)
+        self.B, self.S, self.dim = B, S, dim
+        m = CCGQAAttention(dim=dim, n_heads=n_heads, n_kv_heads=n_kv_heads,
+                           compression_factor=comp, max_seq_len=S)
+        with torch.no_grad():
+            x = torch.randn(B, S, dim, generator=g)
+            for name, p in m.named_parameters():
+                if name == "key_temperature":
+                    p.fill_(1.0)
+                else:
+                    p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+        self.m = m.to(dev, torch.bfloat16).eval()
+        self.x = x.to(dev, torch.bfloat16)
+        from hydra_amd.attention.backends.ccgqa.ops import prep_flags
+
+        self.flags = prep_flags(True, True, True, True, True)
+        mm = self.m
+        self.convw = (mm.q_conv.conv1.weight.detach(), mm.q_conv.conv2.weight.detach(),
+                      mm.k_conv.conv1.weight.detach(), mm.k_conv.conv2.weight.detach())
+        self.cos = mm.cos_cached[0, 0, :S].float().contiguous()
+        self.sin = mm.sin_cached[0, 0, :S].float().contiguous()
+        self.out = torch.empty(B, S, mm.latent_dim, dtype=torch.bfloat16, device=dev)
+
+    @torch.no_grad()
+    def __call__(self, ev=None):
+        from hydra_amd.attention.backends.ccgqa.ops import attention_forward, ccgqa_prep
+
+        m = self.m
+        if ev:
+            ev[0].record()
+        qkv = F.linear(self.x, m.qkv_proj.weight)
+        if ev:
+            ev[1].record()
+        q, k, v = ccgqa_prep(qkv, m.n_heads, m.n_kv_heads, m.head_dim, self.flags, *self.convw,
+                             temperature=m.key_temperature, cos=self.cos, sin=self.sin)
+        if ev:
+            ev[2].record()
+        o_view = self.out.view(self.B, self.S, m.n_heads, m.head_dim).transpose(1, 2)
+        attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view)
+        if ev:
+            ev[3].record()
+        y = F.linear(self.out, m.o_proj.weight)
+        if ev:
+            ev[4].record()
+        return y
+
+
+def c3_flops(B=4, S=4096, dim=1024, Hq=4, Hkv=1, comp=4):
+    from oracle.ccgqa import CCGQAConfig, flops
+
+    return flops(CCGQAConfig(dim=dim, n_heads=Hq, n_kv_heads=Hkv, compression_factor=comp), B, S)
+
+
+def bench_c3(dev, steps, warmup):
+    step = C3Step(dev)
+    check = step()  # also warms the GEMM heuristics
+    del check
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [_events(5) for _ in range(steps)]
+    t0, t1 = _events(2)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        step(evs[i])
+    t1.record()
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    names = ["qkv_gemm", "prep", "attention", "o_proj_gemm"]
+    stages = {n: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, n in enumerate(names)}
+    return step, total_ms / steps, stages
+
+
+# ----------------------------------------------------------------- config 2
+def _time_rotating(fn, sets, iters, warmup=3):
+    for i in range(warmup):
+        fn(*sets[i % len(sets)])
+    torch.cuda.synchronize()
+    a, b = _events(2)
+    a.record()
+    for i in range(iters):
+        fn(*sets[i % len(sets)])
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def bench_fused_ops(dev, iters=60):
+    from hydra_amd.kernels import fused_rms_norm, fused_rope, fused_swiglu
+    from oracle.fused_ops import rope_cache
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    res = {}
+    N, D, H = 8 * 2048, 768, 2048
+    bf = torch.bfloat16
+    # RMSNorm [8,2048,768]: 12 x (25 MB in + 25 MB out) rotating sets
+    w = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(bf)
+    sets = [(torch.randn(8, 2048, D, device=dev, generator=g).to(bf), w) for _ in range(12)]
+    ms = _time_rotating(lambda x, w: fused_rms_norm(x, w, 1e-6), sets, iters)
+    nbytes = 2 * N * D * 2 + 2 * D
+    res["rms_norm"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
+    del sets
+    # RoPE [8,12,2048,64] with fp32 [2048,32] cos/sin
+    cos, sin = rope_cache(64, 2048)
+    cos, sin = cos[0, 0].to(dev), sin[0, 0].to(dev)
+    sets = [(torch.randn(8, 12, 2048, 64, device=dev, generator=g).to(bf),) for _ in range(12)]
+    ms = _time_rotating(lambda x: fused_rope(x, cos, sin), sets, iters)
+    nbytes = 2 * 8 * 12 * 2048 * 64 * 2 + 2 * 2048 * 32 * 4
+    res["rope"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
+    del sets
+    # SwiGLU: halves of gate_up [8,2048,4096] -> [8,2048,2048]; 4 rotating sets
+    sets = []
+    for _ in range(4):
+        gu = torch.randn(8, 2048, 2 * H, device=dev, generator=g).to(bf)
+        sets.append(tuple(gu.chunk(2, -1)))
+    ms = _time_rotating(lambda a, b: fused_swiglu(a, b), sets, iters)
+    nbytes = 3 * N * H * 2
+    res["swiglu"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
+    del sets
+    for v in res.values():
+        v["pct_peak"] = 100.0 * v["GBs"] / HBM_PEAK_GBS
+    return res
+
+
+# ----------------------------------------------------------------- config 4
+def bench_mod(dev, iters=50):
+    from hydra_amd.routing import gather_by_indices, mod_topk, weighted_residual_scatter
+    from oracle.mod import make_tied_logits
+
+    g = torch.Generator().manual_seed(0)
+    B, L, D, k = 8, 4096, 1280, 3072
+    scores = make_tied_logits(B, L, 0.05, g).to(dev)
+    res = {}
+    ms = _time_rotating(lambda s: mod_topk(s, k), [(scores,)], iters)
+    res["topk"] = {"ms": ms, "bytes": B * L * 4 + 2 * B * k * 8, "us": ms * 1e3}
+    _, idx, _ = mod_topk(scores, k)
+    gd = torch.Generator(device=dev).manual_seed(1)
+    xs = [torch.randn(B, L, D, device=dev, generator=gd).to(torch.bfloat16) for _ in range(4)]
+    ys = [torch.randn(B, k, D, device=dev, generator=gd).to(torch.bfloat16) for _ in range(4)]
+    ms = _time_rotating(lambda x: gather_by_indices(x, idx), [(x,) for x in xs], iters)
+    nb = 2 * B * k * D * 2
+    res["gather"] = {"ms": ms, "bytes": nb, "GBs": nb / ms / 1e6, "pct_peak": 100 * nb / ms / 1e6 / HBM_PEAK_GBS}
+    ms = _time_rotating(lambda h, y: weighted_residual_scatter(h, y, idx), list(zip(xs, ys)), iters)
+    nb = 3 * B * k * D * 2
+    res["scatter"] = {"ms": ms, "bytes": nb, "GBs": nb / ms / 1e6, "pct_peak": 100 * nb / ms / 1e6 / HBM_PEAK_GBS}
+    return res
+
+
+# ------------------------------------------------------------- CPU baseline
+def cpu_baseline(budget_s=12.0):
+    """The oracle (reference PyTorch CPU path restated) on the config 3
+    workload (B=4 x S=4096, bf16): tokens/s on this host, median over repeats
+    bounded by budget_s seconds."""
+    from oracle import ccgqa as occ
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cfg = occ.CCGQAConfig(dim=1024, n_heads=4, n_kv_heads=1, compression_factor=4, max_seq_len=4096)
+    g = torch.Generator().manual_seed(0)
+    params = {k: v.to(torch.bfloat16) for k, v in occ.init_params(cfg, g, temperature=1.0).items()}
+    B, S = 4, 4096
+    x = torch.randn(B, S, 1024, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        for _ in range(2):
+            occ.forward(params, x, cfg)  # warmup
+        times = []
+        start = time.perf_counter()
+        while len(times) < 5 or ((time.perf_counter() - start) < budget_s and len(times) < 200):
+            t = time.perf_counter()
+            occ.forward(params, x, cfg)
+            times.append(time.perf_counter() - t)
+    med = sorted(times)[len(times) // 2]
+    cpu_name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": B * S / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle CCGQA forward (attention.py:201-331 restated on torch CPU ops), "
+                      f"full config 3 (B=4 x S=4096, bf16); median of {len(times)} runs in "
+                      f"{time.perf_counter() - start:.1f} s, {threads} threads on '{cpu_name}', "
+                      f"torch {torch.__version__}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-c3", action="store_true", help="skip the fused-op and MoD sections")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the hot path has no multi-GPU "
+              "component); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU", file=sys.stderr)
+        sys.exit(1)
+    from hydra_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    step, ms_step, stages = bench_c3(dev, args.steps, args.warmup)
+    fl = c3_flops()
+    attn_ms = stages["attention"]
+    achieved = fl["core"] / (attn_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": step.B * step.S / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 0, N(0,1) activations, N(0,0.02) weights)",
+        "config": {"workload": "config 3: CCGQA attention forward, dim 1024, latent 256, 4q/1kv heads "
+                               "x hd 64, causal conv k=3, QK-mean, QK-norm tau 1.0, B4 x S4096, bf16",
+                   "global_batch": step.B, "seq_len": step.S, "parallelism": "none (1 GPU)"},
+        "roofline": {"kernel": "attn_fwd_mfma_kernel<64,causal>", "bound": "mfma",
+                     "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                     "flops_per_launch": fl["core"], "avg_ms": attn_ms},
+        "stages_ms": stages,
+        "module_tflops": fl["total"] / (ms_step * 1e-3) / 1e12,
+    }
+    if not args.only_c3:
+        line["fused_ops"] = bench_fused_ops(dev)
+        line["mod"] = bench_mod(dev)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

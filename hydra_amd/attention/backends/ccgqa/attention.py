@@ -1,0 +1,161 @@
+"""CCGQAAttention on MI355X: drop-in for
+hydra/attention/backends/ccgqa/attention.py:67-383.
+
+Same constructor, attributes, parameters and state_dict keys
+(qkv_proj.weight, o_proj.weight, q_conv.conv1.weight, q_conv.conv2.weight,
+k_conv.conv1.weight, k_conv.conv2.weight, key_temperature) and the same
+non-persistent RoPE buffers (cos_cached, sin_cached).  The forward is
+
+    qkv  = x @ W_qkv^T                              torch GEMM (hipBLASLt)
+    q,k,v = hydra_ccgqa_prep_fwd(qkv, ...)          one HIP kernel: split, value
+                                                    shift, convs, QK-mean,
+                                                    L2-norm * temperature, RoPE
+    o    = hydra_attn_fwd(q, k, v, causal)          one HIP kernel (bf16 MFMA),
+                                                    written as [B, S, L]
+    out  = o @ W_o^T * output_scale                 torch GEMM
+
+The reference's precomputed [max_seq_len, max_seq_len] causal mask buffer is
+not kept: the kernel derives causality from indices.
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ...._autograd import track
+from ...._lib import MASK_KEY_PADDING, MASK_REFERENCE_SDPA
+from .kernels.fused_conv import OptimizedConvSequence
+from .ops import attention_forward, ccgqa_prep, prep_flags
+
+# Kept for callers that probe these names (attention.py:13-28).
+FUSED_KERNELS_AVAILABLE = True
+TRITON_ATTENTION_AVAILABLE = True
+
+
+def _mask_mode() -> int:
+    """How a padding mask passed to forward() is applied.
+
+    "reference" (default) reproduces attention.py:268-299 literally, including
+    its hand-off of a "True = masked" boolean to SDPA (which reads True as
+    "attend"); "key_padding" applies the mask as a key-padding mask on top of
+    causality."""
+    v = os.environ.get("HYDRA_CCGQA_MASK_SEMANTICS", "reference").strip().lower()
+    return MASK_KEY_PADDING if v in {"key_padding", "padding"} else MASK_REFERENCE_SDPA
+
+
+class CCGQAAttention(nn.Module):
+    """Compressed Convolutional Grouped Query Attention (forward on gfx950)."""
+
+    def __init__(self, dim: int, n_heads: int = 16, n_kv_heads: int = 4,
+                 compression_factor: int = 4, max_seq_len: int = 8192, use_rope: bool = True,
+                 use_qk_norm: bool = True, use_convs: bool = True, use_qk_mean: bool = True,
+                 use_value_shift: bool = True, conv_kernel_size: int = 3,
+                 use_fused_kernel: bool = True):
+        super().__init__()
+        self.dim = dim
+        self.n_heads = n_heads
+        self.n_kv_heads = n_kv_heads
+        self.n_groups = n_heads // n_kv_heads
+        self.compression_factor = compression_factor
+        self.use_rope = use_rope
+        self.use_qk_norm = use_qk_norm
+        self.use_convs = use_convs
+        self.use_qk_mean = use_qk_mean
+        self.use_value_shift = use_value_shift
+        self.use_fused_kernel = use_fused_kernel
+        self.conv_kernel_size = conv_kernel_size
+
+        self.latent_dim = dim // compression_factor
+        self.head_dim = self.latent_dim // n_heads
+        self.kv_dim = n_kv_heads * self.head_dim
+        assert self.latent_dim % n_heads == 0, (
+            f"latent_dim {self.latent_dim} must be divisible by n_heads {n_heads}")
+        assert self.head_dim % 2 == 0, (
+            f"head_dim {self.head_dim} must be even for RoPE (splits into pairs)")
+
+        # q | k | v_curr | v_prev  (or q | k | v without the value shift)
+        self.qkv_proj = nn.Linear(dim, self.latent_dim + 2 * self.kv_dim, bias=False)
+        self.o_proj = nn.Linear(self.latent_dim, dim, bias=False)
+        self.output_scale = float(os.environ.get("HYDRA_CCGQA_OUTPUT_SCALE", "1.0"))
+        if use_convs:
+            self.q_conv = OptimizedConvSequence(self.latent_dim, n_heads, 1, conv_kernel_size)
+            self.k_conv = OptimizedConvSequence(self.kv_dim, n_kv_heads, 1, conv_kernel_size)
+        self.key_temperature = nn.Parameter(torch.full((1,), float(self.head_dim ** 0.5)))
+        if use_rope:
+            self._init_rope(max_seq_len)
+        self.scale = self.head_dim ** -0.5
+        self.max_seq_len = max_seq_len
+
+    def _init_rope(self, max_seq_len: int) -> None:
+        """attention.py:160-185 (theta 1e4, fp32 unless HYDRA_ROPE_CACHE_DTYPE)."""
+        hd = self.head_dim
+        freqs = 1.0 / (10000.0 ** (torch.arange(0, hd, 2).float() / hd))
+        ang = torch.outer(torch.arange(max_seq_len, dtype=torch.float32), freqs)
+        env = os.environ.get("HYDRA_ROPE_CACHE_DTYPE", "").strip().lower()
+        cdt = {"bf16": torch.bfloat16, "bfloat16": torch.bfloat16, "fp16": torch.float16,
+               "float16": torch.float16, "half": torch.float16}.get(env, torch.float32)
+        self.register_buffer("cos_cached", ang.cos().to(cdt)[None, None], persistent=False)
+        self.register_buffer("sin_cached", ang.sin().to(cdt)[None, None], persistent=False)
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, S, _ = x.shape
+        if self.use_convs and self.conv_kernel_size != 3:
+            raise NotImplementedError("CCGQAAttention: the HIP prep kernel implements conv_kernel_size=3")
+        if self.use_rope and S > self.cos_cached.shape[2]:
+            raise ValueError(f"CCGQAAttention: sequence length {S} exceeds the RoPE cache "
+                             f"({self.cos_cached.shape[2]})")
+        qkv = F.linear(x, self.qkv_proj.weight)
+        flags = prep_flags(self.use_convs, self.use_qk_mean, self.use_value_shift,
+                           self.use_qk_norm, self.use_rope)
+        convw = ((self.q_conv.conv1.weight, self.q_conv.conv2.weight,
+                  self.k_conv.conv1.weight, self.k_conv.conv2.weight)
+                 if self.use_convs else (None, None, None, None))
+        with torch.no_grad():
+            q, k, v = ccgqa_prep(
+                qkv.detach(), self.n_heads, self.n_kv_heads, self.head_dim, flags, *[
+                    None if w is None else w.detach() for w in convw],
+                temperature=self.key_temperature.detach() if self.use_qk_norm else None,
+                cos=self.cos_cached if self.use_rope else None,
+                sin=self.sin_cached if self.use_rope else None)
+            out = torch.empty((B, S, self.latent_dim), dtype=x.dtype, device=x.device)
+            o_view = out.view(B, S, self.n_heads, self.head_dim).transpose(1, 2)
+            attention_forward(q, k, v, causal=True, scale=self.scale,
+                              key_mask=mask, mask_mode=_mask_mode() if mask is not None else 0,
+                              out=o_view)
+        out = track(out, x, self.qkv_proj.weight, self.key_temperature, *[w for w in convw if w is not None])
+        out = F.linear(out, self.o_proj.weight)
+        if self.output_scale != 1.0:
+            out = out * self.output_scale
+        return out
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        """Legacy checkpoint migration (attention.py:333-383): q_conv1/q_conv2/
+        k_conv1/k_conv2 -> q_conv.conv1/... and separate q/k/v(/v_shift)_down
+        projections concatenated into qkv_proj."""
+        has_q = hasattr(self, "q_conv")
+        has_k = hasattr(self, "k_conv")
+        for suffix in ("weight", "bias"):
+            for old, new, has in (("q_conv1", "q_conv.conv1", has_q), ("q_conv2", "q_conv.conv2", has_q),
+                                  ("k_conv1", "k_conv.conv1", has_k), ("k_conv2", "k_conv.conv2", has_k)):
+                ok, nk = prefix + f"{old}.{suffix}", prefix + f"{new}.{suffix}"
+                if ok not in state_dict:
+                    continue
+                if has and nk not in state_dict:
+                    state_dict[nk] = state_dict.pop(ok)
+                else:
+                    state_dict.pop(ok, None)
+        qk, kk, vk, vsk = (prefix + n for n in ("q_down.weight", "k_down.weight", "v_down.weight",
+                                                "v_shift_down.weight"))
+        fused = prefix + "qkv_proj.weight"
+        if qk in state_dict and fused not in state_dict:
+            parts = [state_dict.pop(qk), state_dict.pop(kk), state_dict.pop(vk)]
+            if self.use_value_shift and vsk in state_dict:
+                parts.append(state_dict.pop(vsk))
+            state_dict[fused] = torch.cat(parts, dim=0)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)

@@ -1,0 +1,116 @@
+"""Thin tensor-level wrappers over the CCGQA entry points of the C ABI
+(hydra_ccgqa_prep_fwd, hydra_attn_fwd).  Shapes and dtypes are checked
+here; strides, pointers and the current stream go to the library."""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ...._lib import (CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_QK_NORM, CCGQA_ROPE,
+                      CCGQA_VALUE_SHIFT, MASK_KEY_PADDING, MASK_NONE,
+                      MASK_REFERENCE_SDPA)
+from .... import _lib
+
+
+def prep_flags(use_convs: bool, use_qk_mean: bool, use_value_shift: bool,
+               use_qk_norm: bool, use_rope: bool) -> int:
+    return ((CCGQA_CONVS if use_convs else 0) | (CCGQA_QK_MEAN if use_qk_mean else 0)
+            | (CCGQA_VALUE_SHIFT if use_value_shift else 0)
+            | (CCGQA_QK_NORM if use_qk_norm else 0) | (CCGQA_ROPE if use_rope else 0))
+
+
+def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, flags: int,
+               wq1=None, wq2=None, wk1=None, wk2=None, temperature=None, cos=None, sin=None):
+    """q [B,Hq,S,hd], k/v [B,Hkv,S,hd] from the fused projection qkv [B,S,L+2K]
+    (CCGQAAttention.forward, attention.py:205-266)."""
+    _lib.require_gpu("ccgqa_prep", qkv, wq1, wq2, wk1, wk2, temperature, cos, sin)
+    B, S, W = qkv.shape
+    L, K = n_heads * head_dim, n_kv_heads * head_dim
+    if W != L + 2 * K:
+        raise ValueError(f"ccgqa_prep: qkv width {W} != L + 2K = {L + 2 * K}")
+    if qkv.stride(-1) != 1 or (B > 1 and qkv.stride(0) != S * qkv.stride(1)):
+        qkv = qkv.contiguous()
+    dt = qkv.dtype
+
+    def _w(t):
+        return None if t is None else t.to(dt).contiguous()
+
+    wq1, wq2, wk1, wk2, temp = map(_w, (wq1, wq2, wk1, wk2, temperature))
+    if flags & CCGQA_ROPE:
+        if cos.dim() == 4:
+            cos, sin = cos[0, 0], sin[0, 0]
+        if cos.shape[0] < S:
+            raise ValueError(f"ccgqa_prep: RoPE cache covers {cos.shape[0]} positions < S={S}")
+        cos = cos[:S].float().contiguous()
+        sin = sin[:S].float().contiguous()
+    q = torch.empty((B, n_heads, S, head_dim), dtype=dt, device=qkv.device)
+    k = torch.empty((B, n_kv_heads, S, head_dim), dtype=dt, device=qkv.device)
+    v = torch.empty((B, n_kv_heads, S, head_dim), dtype=dt, device=qkv.device)
+    with torch.cuda.device(qkv.device):
+        _lib.call("hydra_ccgqa_prep_fwd", qkv.data_ptr(), qkv.stride(1), _lib.ptr(wq1),
+                  _lib.ptr(wq2), _lib.ptr(wk1), _lib.ptr(wk2), _lib.ptr(temp), _lib.ptr(cos),
+                  _lib.ptr(sin), head_dim // 2 if cos is None else cos.stride(0),
+                  q.data_ptr(), k.data_ptr(), v.data_ptr(), B, S, n_heads, n_kv_heads,
+                  head_dim, flags, _lib.dtype_code(qkv), _lib.stream(qkv))
+    return q, k, v
+
+
+def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool,
+                      scale: Optional[float] = None, key_mask: Optional[torch.Tensor] = None,
+                      mask_mode: int = MASK_NONE, out: Optional[torch.Tensor] = None,
+                      want_lse: bool = False):
+    """Softmax attention over [B,H,S,hd] q and [B,Hkv,S,hd] k/v.  `out` may be
+    any [B,Hq,S,hd]-indexed view (e.g. a [B,S,Hq,hd] buffer transposed).
+    Returns (out, lse or None)."""
+    _lib.require_gpu("attention_forward", q, k, v, key_mask, out)
+    B, Hq, S, hd = q.shape
+    Hkv = k.shape[1]
+    if k.shape != (B, Hkv, S, hd) or v.shape != (B, Hkv, S, hd):
+        raise ValueError(f"attention_forward: k/v shapes {tuple(k.shape)}, {tuple(v.shape)} "
+                         f"do not match q {tuple(q.shape)}")
+    if Hq % Hkv != 0:
+        raise ValueError("attention_forward: n_heads must be a multiple of n_kv_heads")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("attention_forward: q, k, v must share a dtype")
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    if out is None:
+        out = torch.empty((B, Hq, S, hd), dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.stride(-1) != 1:
+        raise ValueError("attention_forward: out must be a [B,Hq,S,hd] view with unit last stride")
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device) if want_lse else None
+    km = None
+    if mask_mode != MASK_NONE:
+        if key_mask is None or key_mask.shape != (B, S):
+            raise ValueError(f"attention_forward: key mask must be [B,S] = [{B},{S}]")
+        km = (key_mask != 0).to(torch.uint8).contiguous()
+    sc = float(hd ** -0.5) if scale is None else float(scale)
+    with torch.cuda.device(q.device):
+        _lib.call("hydra_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                  _lib.ptr(lse), _lib.ptr(km), mask_mode, B, Hq, Hkv, S, hd,
+                  _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
+                  1 if causal else 0, sc, _lib.dtype_code(q), _lib.stream(q))
+    return out, lse
+
+
+def conv_sequence(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, groups1: int,
+                  groups2: int) -> torch.Tensor:
+    """Standalone OptimizedConvSequence forward ([B,N,C] -> [B,N,C]) through
+    the prep kernel's conv stage: x is laid out as the q block of a qkv
+    buffer whose k block is zero, with every other prep feature off."""
+    if groups2 != 1:
+        raise NotImplementedError("conv_sequence: the HIP conv stage implements a dense conv2 (groups2 == 1)")
+    if w1.shape[-1] != 3:
+        raise NotImplementedError("conv_sequence: the HIP conv stage implements kernel_size 3")
+    _lib.require_gpu("conv_sequence", x, w1, w2)
+    B, N, C = x.shape
+    hd = C // groups1
+    qkv = torch.zeros((B, N, C + 2 * hd), dtype=x.dtype, device=x.device)
+    qkv[..., :C] = x
+    zk = torch.zeros((hd, hd, 3), dtype=x.dtype, device=x.device)
+    q, _, _ = ccgqa_prep(qkv, groups1, 1, hd, CCGQA_CONVS, w1, w2, zk, zk)
+    return q.transpose(1, 2).reshape(B, N, C)
+
+
+__all__ = ["prep_flags", "ccgqa_prep", "attention_forward", "conv_sequence",
+           "MASK_NONE", "MASK_KEY_PADDING", "MASK_REFERENCE_SDPA"]

@@ -1,0 +1,410 @@
+// CCGQA attention core on gfx950: causal (or full) GQA softmax attention
+// forward, o = softmax(scale * q k^T + mask) v, with K/V heads shared by
+// G = Hq/Hkv query heads in repeat_interleave order.
+// Reference semantics: SDPA call of CCGQAAttention.forward
+// (hydra/attention/backends/ccgqa/attention.py:268-327) and the Triton
+// kernels _fwd_gqa_kernel / _fwd_kernel (kernels/fused_attention.py:14-110,
+// 341-429).
+//
+// bf16 path (attn_fwd_mfma_kernel): v_mfma_f32_32x32x16_bf16.
+//  * A workgroup is 4 waves that share one (batch, kv-head) and one staged
+//    K/V tile in LDS; wave w takes task 4*wg+w, task t -> (32-row query block
+//    t/G, query head kvh*G + t%G), so GQA heads reuse the same K/V tile.
+//  * Scores are computed transposed, S^T = K Q^T, so lane l owns query
+//    (l%32) and the online softmax needs no cross-lane traffic except one
+//    swap between the two half-waves.
+//  * O^T = V^T P^T: the bf16 P fragment is taken straight from the score
+//    accumulator registers; V is transposed while it is staged into LDS.
+//  * Causal: the grid runs the longest query blocks first, blocks above the
+//    diagonal are skipped, and only diagonal tiles evaluate the mask.
+//  * Softmax runs in the exp2 domain with fp32 statistics.
+// Generic path (attn_fwd_generic_kernel): one thread per query row, fp32
+// math, any element type, even head_dim <= 256.
+#include "common.h"
+
+namespace hydra {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(from_f32<bf16>(lo).bits) |
+         (static_cast<uint32_t>(from_f32<bf16>(hi).bits) << 16);
+}
+
+template <int HD, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
+    int S, int Hq, int Hkv, int G, int ntasks,
+    int64_t qs0, int64_t qs1, int64_t qs2,
+    int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2,
+    int64_t os0, int64_t os1, int64_t os2, float scale_log2) {
+  constexpr int BN = 64;                // keys per tile
+  constexpr int KSTEPS = HD / 16;       // k-steps of S^T = K Q^T
+  constexpr int DT = (HD + 31) / 32;    // 32-row d tiles of O^T
+  constexpr int KROW = HD + 8;          // padded LDS row of K (elements)
+  constexpr int VROW = BN + 4;          // padded LDS row of V^T (elements)
+  constexpr int DC = HD / 8;            // 16-byte chunks per K/V row
+  constexpr int KCH = (BN * DC + 255) / 256;        // K chunks per thread
+  constexpr int VCH = ((BN / 2) * DC + 255) / 256;  // V key-pair units per thread
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[DT * 32 * VROW];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int n = lane & 31, hf = lane >> 5;
+  const int bk = blockIdx.y;
+  const int b = bk / Hkv, kvh = bk - b * Hkv;
+  const int wg = gridDim.x - 1 - blockIdx.x;  // longest query blocks first
+  const int task = wg * 4 + wave;
+  const bool active = task < ntasks;
+  const int qb = task / G;
+  const int h = kvh * G + (task - qb * G);
+  const int q0 = qb * 32;
+  const int qi = q0 + n;
+  const int last_task = min(wg * 4 + 3, ntasks - 1);
+  const int wg_qmax = (last_task / G) * 32 + 31;
+  const int kend = CAUSAL ? min(S, wg_qmax + 1) : S;
+  const int nkb = (kend + BN - 1) / BN;
+
+  const bf16* kbase = k + b * ks0 + kvh * ks1;
+  const bf16* vbase = v + b * vs0 + kvh * vs1;
+
+  if (DT * 32 > HD) {  // zero the padding rows of V^T once
+    for (int i = tid; i < (DT * 32 - HD) * VROW; i += 256) Vt[HD * VROW + i] = 0;
+  }
+
+  // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7].
+  bf16x8_t qf[KSTEPS];
+  {
+    const bf16* qrow = q + b * qs0 + h * qs1 + static_cast<int64_t>(qi) * qs2;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (active && qi < S) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
+      qf[s] = as_bf16x8(raw);
+    }
+  }
+
+  uint4 kreg[KCH];
+  uint4 vreg[VCH][2];
+  auto fetch = [&](int key0) {
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int c = tid + 256 * j;
+      const int key = c / DC, dc = c - key * DC;
+      kreg[j] = make_uint4(0, 0, 0, 0);
+      if (c < BN * DC && key0 + key < S)
+        kreg[j] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key0 + key) * ks2 + dc * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+      const int u = tid + 256 * j;
+      const int kp = u / DC, dc = u - kp * DC;
+      const int key = key0 + 2 * kp;
+      vreg[j][0] = make_uint4(0, 0, 0, 0);
+      vreg[j][1] = make_uint4(0, 0, 0, 0);
+      if (u < (BN / 2) * DC) {
+        if (key < S) vreg[j][0] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * vs2 + dc * 8);
+        if (key + 1 < S) vreg[j][1] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key + 1) * vs2 + dc * 8);
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int c = tid + 256 * j;
+      const int key = c / DC, dc = c - key * DC;
+      if (c < BN * DC) *reinterpret_cast<uint4*>(&Ks[key * KROW + dc * 8]) = kreg[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+      const int u = tid + 256 * j;
+      const int kp = u / DC, dc = u - kp * DC;
+      if (u < (BN / 2) * DC) {
+        const uint32_t a[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
+        const uint32_t c2[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
+          const uint32_t lo = (a[e] & 0xffffu) | (c2[e] << 16);
+          const uint32_t hi = (a[e] >> 16) | (c2[e] & 0xffff0000u);
+          *reinterpret_cast<uint32_t*>(&Vt[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
+          *reinterpret_cast<uint32_t*>(&Vt[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
+        }
+      }
+    }
+  };
+
+  float m_i = -INFINITY, l_i = 0.f;
+  f32x16_t acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+
+  if (nkb > 0) fetch(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    stage();
+    __syncthreads();
+    if (kb + 1 < nkb) fetch((kb + 1) * BN);
+    const int key0 = kb * BN;
+    const bool live = active && !(CAUSAL && key0 > q0 + 31);
+    if (live) {
+      f32x16_t st[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const uint4 a = *reinterpret_cast<const uint4*>(&Ks[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
+          st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
+        }
+      }
+      const bool need_mask = MASK != 0 || key0 + BN > S || (CAUSAL && key0 + BN - 1 > q0);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = st[mt][r] * scale_log2;
+          if (need_mask) {
+            const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
+            bool ok = key < S;
+            if (CAUSAL) ok = ok && key <= qi;
+            if (MASK != 0) {
+              const bool keep = kmask[static_cast<int64_t>(b) * S + min(key, S - 1)] != 0;
+              ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
+            }
+            x = ok ? x : -INFINITY;
+          }
+          st[mt][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_i, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
+      float rs = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(st[mt][r] - m_use);
+          st[mt][r] = p;
+          rs += p;
+        }
+      rs += __shfl_xor(rs, 32);
+      l_i = l_i * alpha + rs;
+      m_i = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+      // O^T += V^T P^T over 4 k-steps of 16 keys.
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int mt = s2 >> 1, rb = 8 * (s2 & 1);
+        uint4 praw;
+        praw.x = pack_bf16x2(st[mt][rb + 0], st[mt][rb + 1]);
+        praw.y = pack_bf16x2(st[mt][rb + 2], st[mt][rb + 3]);
+        praw.z = pack_bf16x2(st[mt][rb + 4], st[mt][rb + 5]);
+        praw.w = pack_bf16x2(st[mt][rb + 6], st[mt][rb + 7]);
+        const bf16x8_t pf = as_bf16x8(praw);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint16_t* vr = &Vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+          const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (!active || qi >= S) return;
+  const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
+  bf16* orow = o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * dt + 8 * g4 + 4 * hf;
+      if (d < HD) {
+        uint2 w;
+        w.x = pack_bf16x2(acc[dt][4 * g4 + 0] * inv, acc[dt][4 * g4 + 1] * inv);
+        w.y = pack_bf16x2(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d) = w;
+      }
+    }
+  if (lse && hf == 0) {
+    lse[(static_cast<int64_t>(b) * Hq + h) * S + qi] =
+        l_i > 0.f ? (m_i + __log2f(l_i)) * kLn2 : -INFINITY;
+  }
+}
+
+// ---- generic path ---------------------------------------------------------
+template <typename T, int MAXHD>
+__global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    T* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
+    int B, int S, int Hq, int Hkv, int hd, int causal, int mask_mode,
+    int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t os0, int64_t os1, int64_t os2,
+    float scale) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= static_cast<int64_t>(B) * Hq * S) return;
+  const int s = static_cast<int>(gid % S);
+  const int bh = static_cast<int>(gid / S);
+  const int b = bh / Hq, h = bh - b * Hq;
+  const int j = h / (Hq / Hkv);
+  float qv[MAXHD], acc[MAXHD];
+  const T* qr = q + b * qs0 + h * qs1 + static_cast<int64_t>(s) * qs2;
+  for (int d = 0; d < hd; ++d) {
+    qv[d] = to_f32(qr[d]);
+    acc[d] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int tend = (causal && mask_mode != 2) ? s + 1 : S;
+  const T* kb = k + b * ks0 + j * ks1;
+  const T* vb = v + b * vs0 + j * vs1;
+  for (int t = 0; t < tend; ++t) {
+    if (mask_mode == 1 && kmask[static_cast<int64_t>(b) * S + t] == 0) continue;
+    if (mask_mode == 2 && t <= s && kmask[static_cast<int64_t>(b) * S + t] != 0) continue;
+    const T* kr = kb + static_cast<int64_t>(t) * ks2;
+    float dot = 0.f;
+    for (int d = 0; d < hd; ++d) dot = fmaf(qv[d], to_f32(kr[d]), dot);
+    const float x = dot * scale;
+    if (x > m) {
+      const float alpha = expf(m - x);
+      for (int d = 0; d < hd; ++d) acc[d] *= alpha;
+      l *= alpha;
+      m = x;
+    }
+    const float p = expf(x - m);
+    l += p;
+    const T* vr = vb + static_cast<int64_t>(t) * vs2;
+    for (int d = 0; d < hd; ++d) acc[d] = fmaf(p, to_f32(vr[d]), acc[d]);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = o + b * os0 + h * os1 + static_cast<int64_t>(s) * os2;
+  for (int d = 0; d < hd; ++d) orow[d] = from_f32<T>(acc[d] * inv);
+  if (lse) lse[gid] = l > 0.f ? m + logf(l) : -INFINITY;
+}
+
+template <int HD>
+static int launch_mfma(const void* q, const void* k, const void* v, void* o, float* lse,
+                       const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
+                       int64_t Hkv, int64_t S, const int64_t* qs, const int64_t* ks,
+                       const int64_t* vs, const int64_t* os, bool causal, float scale,
+                       hipStream_t st) {
+  const int G = static_cast<int>(Hq / Hkv);
+  const int nqb = static_cast<int>((S + 31) / 32);
+  const int ntasks = G * nqb;
+  const dim3 grid(static_cast<unsigned>((ntasks + 3) / 4), static_cast<unsigned>(B * Hkv));
+  const float sl2 = scale * kLog2e;
+  auto Q = static_cast<const bf16*>(q);
+  auto K = static_cast<const bf16*>(k);
+  auto V = static_cast<const bf16*>(v);
+  auto O = static_cast<bf16*>(o);
+#define HYDRA_ATTN_LAUNCH(C, M)                                                      \
+  attn_fwd_mfma_kernel<HD, C, M><<<grid, 256, 0, st>>>(                              \
+      Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, qs[0], qs[1],   \
+      qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], sl2)
+  // The reference-SDPA mask mode opens keys above the diagonal, so it walks
+  // every key tile (no causal tile skipping).
+  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) HYDRA_ATTN_LAUNCH(false, 2);
+  else if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) HYDRA_ATTN_LAUNCH(true, 1);
+  else if (causal) HYDRA_ATTN_LAUNCH(true, 0);
+  else if (mask_mode == HYDRA_MASK_KEY_PADDING) HYDRA_ATTN_LAUNCH(false, 1);
+  else HYDRA_ATTN_LAUNCH(false, 0);
+#undef HYDRA_ATTN_LAUNCH
+  return check_launch("attn_fwd_mfma_kernel");
+}
+
+template <typename T>
+static int launch_generic(const void* q, const void* k, const void* v, void* o, float* lse,
+                          const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
+                          int64_t Hkv, int64_t S, int64_t hd, const int64_t* qs,
+                          const int64_t* ks, const int64_t* vs, const int64_t* os,
+                          bool causal, float scale, hipStream_t st) {
+  const int64_t total = B * Hq * S;
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  auto Q = static_cast<const T*>(q);
+  auto K = static_cast<const T*>(k);
+  auto V = static_cast<const T*>(v);
+  auto O = static_cast<T*>(o);
+#define HYDRA_GEN_LAUNCH(MAXHD)                                                       \
+  attn_fwd_generic_kernel<T, MAXHD><<<grid, 256, 0, st>>>(                            \
+      Q, K, V, O, lse, kmask, (int)B, (int)S, (int)Hq, (int)Hkv, (int)hd, causal ? 1 : 0, \
+      mask_mode, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],  \
+      os[1], os[2], scale)
+  if (hd <= 32) HYDRA_GEN_LAUNCH(32);
+  else if (hd <= 64) HYDRA_GEN_LAUNCH(64);
+  else if (hd <= 128) HYDRA_GEN_LAUNCH(128);
+  else HYDRA_GEN_LAUNCH(256);
+#undef HYDRA_GEN_LAUNCH
+  return check_launch("attn_fwd_generic_kernel");
+}
+
+}  // namespace hydra
+
+using namespace hydra;
+
+extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                              float* lse, const uint8_t* key_mask, int mask_mode,
+                              int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                              const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                              const int64_t* os, int causal, float scale, int dtype,
+                              void* stream) {
+  HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_fwd: bad size");
+  HYDRA_REQUIRE(Hq % Hkv == 0, "attn_fwd: n_heads must be a multiple of n_kv_heads");
+  HYDRA_REQUIRE(qs && ks && vs && os, "attn_fwd: null stride array");
+  HYDRA_REQUIRE(qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1,
+                "attn_fwd: head_dim must have unit stride");
+  HYDRA_REQUIRE(hd <= 256, "attn_fwd: head_dim must be <= 256");
+  HYDRA_REQUIRE(mask_mode >= HYDRA_MASK_NONE && mask_mode <= HYDRA_MASK_REFERENCE_SDPA,
+                "attn_fwd: unknown mask mode");
+  HYDRA_REQUIRE(mask_mode == HYDRA_MASK_NONE || key_mask != nullptr,
+                "attn_fwd: mask mode needs key_mask");
+  HYDRA_REQUIRE(mask_mode != HYDRA_MASK_REFERENCE_SDPA || causal,
+                "attn_fwd: the reference-SDPA mask mode is defined with causal=1");
+  if (B * S == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(q && k && v && o, "attn_fwd: null pointer");
+  HYDRA_REQUIRE(S < (int64_t(1) << 30), "attn_fwd: sequence too long");
+  HYDRA_REQUIRE(B * Hkv <= 65535, "attn_fwd: B*n_kv_heads must be <= 65535");
+  const uint8_t* km = mask_mode == HYDRA_MASK_NONE ? nullptr : key_mask;
+  auto st = static_cast<hipStream_t>(stream);
+  const bool mfma_shape = (hd == 16 || hd == 32 || hd == 64 || hd == 128);
+  bool strides8 = true;
+  for (int i = 0; i < 3; ++i)
+    strides8 = strides8 && qs[i] % 8 == 0 && ks[i] % 8 == 0 && vs[i] % 8 == 0 && os[i] % 4 == 0;
+  if (dtype == HYDRA_BF16 && mfma_shape && strides8 && aligned16(q) && aligned16(k) &&
+      aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0) {
+    switch (hd) {
+      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
+      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
+      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
+      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
+    }
+  }
+  HYDRA_REQUIRE(B * Hq * S / 256 < (int64_t(1) << 31), "attn_fwd: too many rows");
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_generic<T>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, hd, qs, ks, vs,
+                             os, causal != 0, scale, st);
+  });
+}

@@ -1,0 +1,124 @@
+// Shared device/host helpers of the gfx950 kernels: element types, 16-byte
+// vector I/O, wave64 reductions and the error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/hydra_amd.h"
+
+namespace hydra {
+
+// ---- element types ------------------------------------------------------
+// bf16 and fp16 are carried as raw 16-bit patterns; every kernel converts to
+// fp32, computes in fp32 and rounds once (round-to-nearest-even) on store.
+struct bf16 { uint16_t bits; };
+struct f16 { uint16_t bits; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) {
+  return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+__device__ __forceinline__ float to_f32(f16 v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, v.bits));
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
+  uint32_t u = __float_as_uint(v);
+  bf16 r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN: keep it quiet
+    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
+    r.bits = static_cast<uint16_t>(u >> 16);
+  }
+  return r;
+}
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) {
+  f16 r;
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  return r;
+}
+
+// Elements of T in one 16-byte vector.
+template <typename T> struct Vec { static constexpr int N = 16 / sizeof(T); };
+
+// 16-byte load / store of N elements of T, converted to / from fp32.
+template <typename T>
+__device__ __forceinline__ void load16(const T* p, float* out) {
+  const uint4 raw = *reinterpret_cast<const uint4*>(p);
+  if constexpr (sizeof(T) == 4) {
+    out[0] = __uint_as_float(raw.x); out[1] = __uint_as_float(raw.y);
+    out[2] = __uint_as_float(raw.z); out[3] = __uint_as_float(raw.w);
+  } else {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T lo, hi;
+      lo.bits = static_cast<uint16_t>(w[i] & 0xffffu);
+      hi.bits = static_cast<uint16_t>(w[i] >> 16);
+      out[2 * i] = to_f32(lo);
+      out[2 * i + 1] = to_f32(hi);
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store16(T* p, const float* in) {
+  uint4 raw;
+  if constexpr (sizeof(T) == 4) {
+    raw.x = __float_as_uint(in[0]); raw.y = __float_as_uint(in[1]);
+    raw.z = __float_as_uint(in[2]); raw.w = __float_as_uint(in[3]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = static_cast<uint32_t>(from_f32<T>(in[2 * i]).bits) |
+             (static_cast<uint32_t>(from_f32<T>(in[2 * i + 1]).bits) << 16);
+    }
+    raw.x = w[0]; raw.y = w[1]; raw.z = w[2]; raw.w = w[3];
+  }
+  *reinterpret_cast<uint4*>(p) = raw;
+}
+
+// ---- wave64 reductions ---------------------------------------------------
+template <int WIDTH = 64>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WIDTH);
+  return v;
+}
+template <int WIDTH = 64>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WIDTH));
+  return v;
+}
+
+// ---- host-side error plumbing -------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+bool aligned16(const void* p);
+int dtype_size(int dtype);
+
+}  // namespace hydra
+
+#define HYDRA_REQUIRE(cond, msg)                                 \
+  do {                                                           \
+    if (!(cond)) return ::hydra::fail(HYDRA_ERR_ARG, (msg));     \
+  } while (0)
+
+// Dispatch a templated launcher over the three element types.
+#define HYDRA_DISPATCH_DTYPE(dtype, T, ...)                                   \
+  [&]() -> int {                                                             \
+    switch (dtype) {                                                         \
+      case HYDRA_F32: { using T = float; return __VA_ARGS__(); }            \
+      case HYDRA_BF16: { using T = ::hydra::bf16; return __VA_ARGS__(); }   \
+      case HYDRA_F16: { using T = ::hydra::f16; return __VA_ARGS__(); }     \
+      default: return ::hydra::fail(HYDRA_ERR_ARG, "unknown dtype code");    \
+    }                                                                        \
+  }()

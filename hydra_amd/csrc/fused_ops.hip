@@ -1,0 +1,422 @@
+// Memory-bound fused element ops of hydra/kernels/fused_ops.py, written for
+// gfx950: RMSNorm, RoPE, SwiGLU and QK L2-norm.  Each has a 16-byte vector
+// path (128-bit global loads/stores, fp32 math, one rounding on store) and a
+// scalar path for shapes, strides or alignments the vector path cannot take.
+#include "common.h"
+
+namespace hydra {
+
+constexpr int kBlock = 256;  // 4 waves
+
+// ===========================================================================
+// RMSNorm   (reference: _fused_rms_norm_kernel, fused_ops.py:969-1007)
+// One wave per row.  The row stays in registers as raw 16-byte vectors, so
+// HBM sees exactly one read of x and one write of y.
+// ===========================================================================
+template <typename T, int VPL>
+__global__ __launch_bounds__(kBlock) void rms_norm_vec_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
+    int64_t rows, int nvec, int dim, int64_t x_rs, int64_t y_rs, float eps) {
+  constexpr int E = Vec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * x_rs;
+  uint4 raw[VPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int vi = lane + 64 * v;
+    if (vi < nvec) {
+      raw[v] = *reinterpret_cast<const uint4*>(xr + vi * E);
+      float f[E];
+      load16<T>(reinterpret_cast<const T*>(&raw[v]), f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) ss = fmaf(f[e], f[e], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float rinv = rsqrtf(ss / static_cast<float>(dim) + eps);
+  T* yr = y + row * y_rs;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int vi = lane + 64 * v;
+    if (vi < nvec) {
+      float f[E], g[E];
+      load16<T>(reinterpret_cast<const T*>(&raw[v]), f);
+      load16<T>(w + vi * E, g);
+#pragma unroll
+      for (int e = 0; e < E; ++e) f[e] = f[e] * rinv * g[e];
+      store16<T>(yr + vi * E, f);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rms_norm_scalar_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
+    int64_t rows, int dim, int64_t x_rs, int64_t y_rs, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * x_rs;
+  float ss = 0.f;
+  for (int i = lane; i < dim; i += 64) {
+    const float f = to_f32(xr[i]);
+    ss = fmaf(f, f, ss);
+  }
+  ss = wave_sum(ss);
+  const float rinv = rsqrtf(ss / static_cast<float>(dim) + eps);
+  T* yr = y + row * y_rs;
+  for (int i = lane; i < dim; i += 64) {
+    yr[i] = from_f32<T>(to_f32(xr[i]) * rinv * to_f32(w[i]));
+  }
+}
+
+template <typename T>
+static int launch_rms_norm(const void* x, const void* w, void* y, int64_t rows,
+                           int64_t dim, int64_t x_rs, int64_t y_rs, float eps,
+                           hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const bool vec_ok = dim % E == 0 && x_rs % E == 0 && y_rs % E == 0 &&
+                      aligned16(x) && aligned16(w) && aligned16(y);
+  const int nvec = static_cast<int>(dim / E);
+  const int vpl = (nvec + 63) / 64;
+  auto X = static_cast<const T*>(x);
+  auto W = static_cast<const T*>(w);
+  auto Y = static_cast<T*>(y);
+  if (vec_ok && vpl <= 16) {
+#define HYDRA_RMS_CASE(V)                                                      \
+  if (vpl <= V) {                                                              \
+    rms_norm_vec_kernel<T, V><<<grid, kBlock, 0, st>>>(X, W, Y, rows, nvec,    \
+                                                       (int)dim, x_rs, y_rs, eps); \
+    return check_launch("rms_norm_vec_kernel");                                \
+  }
+    HYDRA_RMS_CASE(1) HYDRA_RMS_CASE(2) HYDRA_RMS_CASE(3) HYDRA_RMS_CASE(4)
+    HYDRA_RMS_CASE(8) HYDRA_RMS_CASE(16)
+#undef HYDRA_RMS_CASE
+  }
+  rms_norm_scalar_kernel<T><<<grid, kBlock, 0, st>>>(X, W, Y, rows, (int)dim,
+                                                     x_rs, y_rs, eps);
+  return check_launch("rms_norm_scalar_kernel");
+}
+
+// ===========================================================================
+// RoPE   (reference: _fused_rope_kernel, fused_ops.py:185-237)
+// blockIdx.y = b*H + h; each thread rotates one 16-byte chunk (E/2 pairs).
+// Output is the contiguous [B,H,S,D] tensor; x may be any strided view.
+// ===========================================================================
+template <typename T, typename C>
+__global__ __launch_bounds__(kBlock) void rope_vec_kernel(
+    const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
+    T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
+    int64_t cs_rs) {
+  constexpr int E = Vec<T>::N;
+  const int cpr = D / E;  // chunks per row
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const int t = blockIdx.x * kBlock + threadIdx.x;
+  const int s = t / cpr;
+  if (s >= S) return;
+  const int c = t - s * cpr;
+  float f[E];
+  load16<T>(x + b * xb + h * xh + static_cast<int64_t>(s) * xsr + c * E, f);
+  const C* cr = cs + static_cast<int64_t>(s) * cs_rs + c * (E / 2);
+  const C* sr = sn + static_cast<int64_t>(s) * cs_rs + c * (E / 2);
+  float o[E];
+#pragma unroll
+  for (int p = 0; p < E / 2; ++p) {
+    const float cv = to_f32(cr[p]), sv = to_f32(sr[p]);
+    const float x1 = f[2 * p], x2 = f[2 * p + 1];
+    o[2 * p] = x1 * cv - x2 * sv;
+    o[2 * p + 1] = x1 * sv + x2 * cv;
+  }
+  store16<T>(out + (static_cast<int64_t>(bh) * S + s) * D + c * E, o);
+}
+
+template <typename T, typename C>
+__global__ __launch_bounds__(kBlock) void rope_scalar_kernel(
+    const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
+    T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
+    int64_t xd, int64_t cs_rs) {
+  const int half = D / 2;
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const int t = blockIdx.x * kBlock + threadIdx.x;
+  const int s = t / half;
+  if (s >= S) return;
+  const int p = t - s * half;
+  const T* xr = x + b * xb + h * xh + static_cast<int64_t>(s) * xsr;
+  const float x1 = to_f32(xr[(2 * p) * xd]), x2 = to_f32(xr[(2 * p + 1) * xd]);
+  const float cv = to_f32(cs[static_cast<int64_t>(s) * cs_rs + p]);
+  const float sv = to_f32(sn[static_cast<int64_t>(s) * cs_rs + p]);
+  T* o = out + (static_cast<int64_t>(bh) * S + s) * D;
+  o[2 * p] = from_f32<T>(x1 * cv - x2 * sv);
+  o[2 * p + 1] = from_f32<T>(x1 * sv + x2 * cv);
+}
+
+template <typename T, typename C>
+static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
+                       int64_t B, int64_t H, int64_t S, int64_t D,
+                       const int64_t* xs, int64_t cs_rs, hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  auto X = static_cast<const T*>(x);
+  auto CS = static_cast<const C*>(cs);
+  auto SN = static_cast<const C*>(sn);
+  auto O = static_cast<T*>(out);
+  const bool vec_ok = xs[3] == 1 && D % E == 0 && xs[0] % E == 0 &&
+                      xs[1] % E == 0 && xs[2] % E == 0 && aligned16(x) &&
+                      aligned16(out);
+  if (vec_ok) {
+    const int64_t threads = S * (D / E);
+    const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock),
+                    static_cast<unsigned>(B * H));
+    rope_vec_kernel<T, C><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S,
+                                                   (int)D, xs[0], xs[1], xs[2], cs_rs);
+    return check_launch("rope_vec_kernel");
+  }
+  const int64_t threads = S * (D / 2);
+  const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock),
+                  static_cast<unsigned>(B * H));
+  rope_scalar_kernel<T, C><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S,
+                                                    (int)D, xs[0], xs[1], xs[2],
+                                                    xs[3], cs_rs);
+  return check_launch("rope_scalar_kernel");
+}
+
+// ===========================================================================
+// SwiGLU   (reference: _fused_swiglu_kernel, fused_ops.py:703-725)
+// gate/up are read straight from the two halves of the gate_up GEMM output,
+// so no contiguous copies are made.  silu(g) = g / (1 + exp(-g)).
+// ===========================================================================
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.f + __expf(-g)); }
+
+template <typename T, int U>
+__global__ __launch_bounds__(kBlock) void swiglu_vec_kernel(
+    const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ o,
+    uint32_t total, uint32_t cpr, int64_t g_rs, int64_t u_rs, int64_t o_rs) {
+  constexpr int E = Vec<T>::N;
+  const uint32_t base = (blockIdx.x * U) * kBlock + threadIdx.x;
+  float gf[U][E], uf[U][E];
+  uint32_t rr[U], cc[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t idx = base + j * kBlock;
+    rr[j] = idx / cpr;
+    cc[j] = idx - rr[j] * cpr;
+    if (idx < total) {
+      load16<T>(g + rr[j] * g_rs + cc[j] * E, gf[j]);
+      load16<T>(u + rr[j] * u_rs + cc[j] * E, uf[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t idx = base + j * kBlock;
+    if (idx < total) {
+      float of[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) of[e] = silu_f32(gf[j][e]) * uf[j][e];
+      store16<T>(o + rr[j] * o_rs + cc[j] * E, of);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_scalar_kernel(
+    const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ o,
+    int64_t total, int64_t hidden, int64_t g_rs, int64_t u_rs, int64_t o_rs) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t r = idx / hidden, c = idx - r * hidden;
+  o[r * o_rs + c] = from_f32<T>(silu_f32(to_f32(g[r * g_rs + c])) * to_f32(u[r * u_rs + c]));
+}
+
+template <typename T>
+static int launch_swiglu(const void* g, const void* u, void* o, int64_t rows,
+                         int64_t hidden, int64_t g_rs, int64_t u_rs, int64_t o_rs,
+                         hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  constexpr int U = 2;
+  auto G = static_cast<const T*>(g);
+  auto Up = static_cast<const T*>(u);
+  auto O = static_cast<T*>(o);
+  const int64_t cpr = hidden / E;
+  const int64_t total_vec = rows * cpr;
+  const bool vec_ok = hidden % E == 0 && g_rs % E == 0 && u_rs % E == 0 &&
+                      o_rs % E == 0 && aligned16(g) && aligned16(u) && aligned16(o) &&
+                      total_vec < (int64_t(1) << 31);
+  if (vec_ok) {
+    const dim3 grid(static_cast<unsigned>((total_vec + U * kBlock - 1) / (U * kBlock)));
+    swiglu_vec_kernel<T, U><<<grid, kBlock, 0, st>>>(G, Up, O, (uint32_t)total_vec,
+                                                     (uint32_t)cpr, g_rs, u_rs, o_rs);
+    return check_launch("swiglu_vec_kernel");
+  }
+  const int64_t total = rows * hidden;
+  const dim3 grid(static_cast<unsigned>((total + kBlock - 1) / kBlock));
+  swiglu_scalar_kernel<T><<<grid, kBlock, 0, st>>>(G, Up, O, total, hidden, g_rs,
+                                                   u_rs, o_rs);
+  return check_launch("swiglu_scalar_kernel");
+}
+
+// ===========================================================================
+// QK L2-norm   (reference: _fused_qk_norm_kernel, fused_ops.py:323-369)
+// LPR lanes per row, one 16-byte chunk each; rows of q then rows of k.
+// ===========================================================================
+template <typename T, int LPR>
+__global__ __launch_bounds__(kBlock) void qk_norm_vec_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo,
+    T* __restrict__ ko, int64_t q_rows, int64_t k_rows, float scale, float temp) {
+  constexpr int E = Vec<T>::N;
+  constexpr int HD = LPR * E;
+  const int64_t gt = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  int64_t row = gt / LPR;
+  const int c = static_cast<int>(gt % LPR);
+  const bool is_k = row >= q_rows;
+  if (is_k) row -= q_rows;
+  const bool live = is_k ? row < k_rows : true;
+  const T* src = is_k ? k : q;
+  T* dst = is_k ? ko : qo;
+  float f[E];
+  float ss = 0.f;
+  if (live) {
+    load16<T>(src + row * HD + c * E, f);
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss = fmaf(f[e], f[e], ss);
+  }
+  ss = wave_sum<LPR>(ss);
+  if (!live) return;
+  float fac = rsqrtf(ss + 1e-8f) * scale;
+  if (is_k) fac *= temp;
+#pragma unroll
+  for (int e = 0; e < E; ++e) f[e] *= fac;
+  store16<T>(dst + row * HD + c * E, f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void qk_norm_scalar_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo,
+    T* __restrict__ ko, int64_t q_rows, int64_t k_rows, int hd, float scale,
+    float temp) {
+  int64_t row = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const bool is_k = row >= q_rows;
+  if (is_k) row -= q_rows;
+  if (is_k && row >= k_rows) return;
+  const T* src = (is_k ? k : q) + row * hd;
+  T* dst = (is_k ? ko : qo) + row * hd;
+  float ss = 0.f;
+  for (int i = 0; i < hd; ++i) {
+    const float f = to_f32(src[i]);
+    ss = fmaf(f, f, ss);
+  }
+  float fac = rsqrtf(ss + 1e-8f) * scale;
+  if (is_k) fac *= temp;
+  for (int i = 0; i < hd; ++i) dst[i] = from_f32<T>(to_f32(src[i]) * fac);
+}
+
+template <typename T>
+static int launch_qk_norm(const void* q, const void* k, void* qo, void* ko,
+                          int64_t q_rows, int64_t k_rows, int64_t hd, float scale,
+                          float temp, hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  auto Q = static_cast<const T*>(q);
+  auto K = static_cast<const T*>(k);
+  auto QO = static_cast<T*>(qo);
+  auto KO = static_cast<T*>(ko);
+  const int64_t lpr = hd / E;
+  const bool vec_ok = hd % E == 0 && lpr >= 1 && lpr <= 64 && (lpr & (lpr - 1)) == 0 &&
+                      aligned16(q) && aligned16(k) && aligned16(qo) && aligned16(ko);
+  if (vec_ok) {
+    const int64_t threads = (q_rows + k_rows) * lpr;
+    const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock));
+#define HYDRA_QKN_CASE(L)                                                      \
+  case L:                                                                      \
+    qk_norm_vec_kernel<T, L><<<grid, kBlock, 0, st>>>(Q, K, QO, KO, q_rows,    \
+                                                      k_rows, scale, temp);    \
+    return check_launch("qk_norm_vec_kernel");
+    switch (lpr) {
+      HYDRA_QKN_CASE(1) HYDRA_QKN_CASE(2) HYDRA_QKN_CASE(4) HYDRA_QKN_CASE(8)
+      HYDRA_QKN_CASE(16) HYDRA_QKN_CASE(32) HYDRA_QKN_CASE(64)
+      default: break;
+    }
+#undef HYDRA_QKN_CASE
+  }
+  const dim3 grid(static_cast<unsigned>((q_rows + k_rows + kBlock - 1) / kBlock));
+  qk_norm_scalar_kernel<T><<<grid, kBlock, 0, st>>>(Q, K, QO, KO, q_rows, k_rows,
+                                                    (int)hd, scale, temp);
+  return check_launch("qk_norm_scalar_kernel");
+}
+
+}  // namespace hydra
+
+using namespace hydra;
+
+extern "C" int hydra_rms_norm_fwd(const void* x, const void* w, void* y,
+                                  int64_t rows, int64_t dim, int64_t x_rs,
+                                  int64_t y_rs, float eps, int dtype, void* stream) {
+  HYDRA_REQUIRE(rows >= 0 && dim >= 1, "rms_norm: rows must be >= 0 and dim >= 1");
+  HYDRA_REQUIRE(dim <= (int64_t(1) << 30), "rms_norm: dim too large");
+  HYDRA_REQUIRE(x_rs >= dim && y_rs >= dim, "rms_norm: row stride smaller than dim");
+  if (rows == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(x && w && y, "rms_norm: null pointer");
+  HYDRA_REQUIRE((rows + 3) / 4 < (int64_t(1) << 31), "rms_norm: too many rows");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_rms_norm<T>(x, w, y, rows, dim, x_rs, y_rs, eps, st);
+  });
+}
+
+extern "C" int hydra_rope_fwd(const void* x, const void* cos, const void* sin,
+                              void* out, int64_t B, int64_t H, int64_t S, int64_t D,
+                              const int64_t* xs, int64_t cs_rs, int dtype,
+                              int cs_dtype, void* stream) {
+  HYDRA_REQUIRE(B >= 0 && H >= 0 && S >= 0 && D >= 0, "rope: negative size");
+  HYDRA_REQUIRE(D % 2 == 0, "rope: head_dim must be even");
+  HYDRA_REQUIRE(xs != nullptr, "rope: null stride array");
+  if (B * H * S * D == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(x && cos && sin && out, "rope: null pointer");
+  HYDRA_REQUIRE(cs_rs >= D / 2, "rope: cos/sin row stride smaller than head_dim/2");
+  HYDRA_REQUIRE(B * H <= 65535, "rope: B*H must be <= 65535");
+  HYDRA_REQUIRE(S * D < (int64_t(1) << 31), "rope: S*D too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    switch (cs_dtype) {
+      case HYDRA_F32: return launch_rope<T, float>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
+      case HYDRA_BF16: return launch_rope<T, bf16>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
+      case HYDRA_F16: return launch_rope<T, f16>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
+      default: return fail(HYDRA_ERR_ARG, "rope: unknown cos/sin dtype code");
+    }
+  });
+}
+
+extern "C" int hydra_swiglu_fwd(const void* gate, const void* up, void* out,
+                                int64_t rows, int64_t hidden, int64_t g_rs,
+                                int64_t u_rs, int64_t o_rs, int dtype, void* stream) {
+  HYDRA_REQUIRE(rows >= 0 && hidden >= 0, "swiglu: negative size");
+  if (rows * hidden == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(gate && up && out, "swiglu: null pointer");
+  HYDRA_REQUIRE(g_rs >= hidden && u_rs >= hidden && o_rs >= hidden,
+                "swiglu: row stride smaller than hidden");
+  HYDRA_REQUIRE((rows * hidden + kBlock - 1) / kBlock < (int64_t(1) << 31),
+                "swiglu: tensor too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_swiglu<T>(gate, up, out, rows, hidden, g_rs, u_rs, o_rs, st);
+  });
+}
+
+extern "C" int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out,
+                                 void* k_out, int64_t q_rows, int64_t k_rows,
+                                 int64_t hd, float scale, float temperature,
+                                 int dtype, void* stream) {
+  HYDRA_REQUIRE(q_rows >= 0 && k_rows >= 0 && hd >= 1, "qk_norm: bad size");
+  if (q_rows + k_rows == 0) return HYDRA_OK;
+  HYDRA_REQUIRE((q_rows == 0 || (q && q_out)) && (k_rows == 0 || (k && k_out)),
+                "qk_norm: null pointer");
+  HYDRA_REQUIRE((q_rows + k_rows) * hd < (int64_t(1) << 40), "qk_norm: tensor too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_qk_norm<T>(q, k, q_out, k_out, q_rows, k_rows, hd, scale,
+                             temperature, st);
+  });
+}

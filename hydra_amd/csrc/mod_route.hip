@@ -1,0 +1,346 @@
+// Mixture-of-Depths hard routing on gfx950: per-row top-k select with
+// lowest-index tie-breaking, row gather, and in-place weighted residual
+// scatter (hydra/routing/mixture_of_depths.py:159-216,
+// hydra/model/framework/blocks.py:243-269).
+//
+// Top-k: one workgroup per row.  Each score becomes a 64-bit composite key
+//   (~order_preserving_u32(score) << 32) | index
+// so that an ascending sort gives value-descending order with ties resolved
+// by ascending index, i.e. the order of a stable descending sort.  The keys
+// are bitonic-sorted in LDS; the first k are the selection.  The ascending
+// index list comes from a bitmap of the selection and a block prefix count.
+#include "common.h"
+
+namespace hydra {
+
+constexpr int kTopkThreads = 1024;
+
+// Order-preserving map of a float to u32 (ascending), with -0.0 folded into
+// +0.0 and every NaN mapped above +inf (torch.topk treats NaN as largest).
+__device__ __forceinline__ uint32_t score_key_asc(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN
+  if (u == 0x80000000u) u = 0u;                               // -0.0 -> +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <typename S>
+__global__ __launch_bounds__(kTopkThreads) void mod_topk_kernel(
+    const S* __restrict__ scores, int L, int64_t s_rs, int k, int P,
+    int64_t* __restrict__ idx_desc, int64_t* __restrict__ idx_sorted,
+    void* __restrict__ mask, int mask_dtype) {
+  extern __shared__ unsigned char smem[];
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
+  uint32_t* bits = reinterpret_cast<uint32_t*>(smem + sizeof(uint64_t) * P);
+  __shared__ int wave_tot[kTopkThreads / 64];
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const S* sr = scores + static_cast<int64_t>(row) * s_rs;
+
+  for (int i = tid; i < P; i += kTopkThreads) {
+    uint64_t key = ~uint64_t(0);
+    if (i < L) {
+      const uint32_t desc = ~score_key_asc(to_f32(sr[i]));
+      key = (static_cast<uint64_t>(desc) << 32) | static_cast<uint32_t>(i);
+    }
+    keys[i] = key;
+  }
+  const int nwords = (L + 31) / 32;
+  for (int i = tid; i < nwords; i += kTopkThreads) bits[i] = 0u;
+  __syncthreads();
+
+  // Bitonic sort, ascending, P a power of two.
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < P / 2; t += kTopkThreads) {
+        const int lo = 2 * t - (t & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = keys[lo], b = keys[hi];
+        if ((a > b) == up) {
+          keys[lo] = b;
+          keys[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  int64_t* drow = idx_desc ? idx_desc + static_cast<int64_t>(row) * k : nullptr;
+  for (int j = tid; j < k; j += kTopkThreads) {
+    const uint32_t i = static_cast<uint32_t>(keys[j] & 0xffffffffu);
+    if (drow) drow[j] = static_cast<int64_t>(i);
+    atomicOr(&bits[i >> 5], 1u << (i & 31));
+  }
+  __syncthreads();
+
+  if (mask) {
+    const int64_t mrow = static_cast<int64_t>(row) * L;
+    for (int i = tid; i < L; i += kTopkThreads) {
+      const float v = (bits[i >> 5] >> (i & 31)) & 1u ? 1.f : 0.f;
+      switch (mask_dtype) {
+        case HYDRA_F32: static_cast<float*>(mask)[mrow + i] = v; break;
+        case HYDRA_BF16: static_cast<bf16*>(mask)[mrow + i] = from_f32<bf16>(v); break;
+        default: static_cast<f16*>(mask)[mrow + i] = from_f32<f16>(v); break;
+      }
+    }
+  }
+  if (!idx_sorted) return;
+
+  // Ascending indices: thread t owns words [t*wpt, (t+1)*wpt) of the bitmap;
+  // an exclusive prefix over the per-thread popcounts gives each thread its
+  // output offset.
+  const int wpt = (nwords + kTopkThreads - 1) / kTopkThreads;
+  const int w0 = tid * wpt;
+  int cnt = 0;
+  for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(bits[w]);
+  const int lane = tid & 63, wave = tid >> 6;
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int n = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += n;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_tot[w];
+  int pos = base + incl - cnt;
+  int64_t* orow = idx_sorted + static_cast<int64_t>(row) * k;
+  for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+    uint32_t m = bits[w];
+    while (m) {
+      const int b = __ffs(m) - 1;
+      m &= m - 1;
+      if (pos < k) orow[pos] = static_cast<int64_t>(w * 32 + b);
+      ++pos;
+    }
+  }
+}
+
+// ---- row gather / scatter ------------------------------------------------
+// One thread per 16-byte chunk of an output row; chunk -> (row, column) with
+// 32-bit arithmetic (host checks the sizes).  An index outside [0, L) makes
+// the row a no-op (gather writes zeros), so no access leaves the tensors.
+template <typename T>
+__global__ __launch_bounds__(256) void mod_gather_kernel(
+    const T* __restrict__ x, const int64_t* __restrict__ idx, T* __restrict__ xs,
+    uint32_t total, uint32_t cpr, uint32_t k, int64_t L, int64_t x_bs, int64_t x_ls) {
+  constexpr int E = Vec<T>::N;
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const uint32_t r = t / cpr, c = t - r * cpr;  // r = b*k + j
+  const uint32_t b = r / k;
+  const int64_t src = idx[r];
+  float f[E];
+  if (src >= 0 && src < L) {
+    load16<T>(x + b * x_bs + src * x_ls + c * E, f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = 0.f;
+  }
+  store16<T>(xs + static_cast<int64_t>(r) * cpr * E + c * E, f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void mod_gather_scalar_kernel(
+    const T* __restrict__ x, const int64_t* __restrict__ idx, T* __restrict__ xs,
+    int64_t total, int64_t D, int64_t k, int64_t L, int64_t x_bs, int64_t x_ls) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int64_t r = t / D, c = t - r * D;
+  const int64_t b = r / k;
+  const int64_t src = idx[r];
+  xs[t] = (src >= 0 && src < L) ? x[b * x_bs + src * x_ls + c] : from_f32<T>(0.f);
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void mod_scatter_kernel(
+    T* __restrict__ out, const T* __restrict__ y, const int64_t* __restrict__ idx,
+    const float* __restrict__ w, uint32_t total, uint32_t cpr, uint32_t k, int64_t L,
+    int64_t o_bs, int64_t o_ls) {
+  constexpr int E = Vec<T>::N;
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const uint32_t r = t / cpr, c = t - r * cpr;
+  const uint32_t b = r / k;
+  const int64_t dst = idx[r];
+  if (dst < 0 || dst >= L) return;
+  T* op = out + b * o_bs + dst * o_ls + c * E;
+  float yf[E];
+  load16<T>(y + static_cast<int64_t>(r) * cpr * E + c * E, yf);
+  if (MODE == HYDRA_SCATTER_ADD) {
+    const float wt = w ? w[r] : 1.f;
+    float of[E];
+    load16<T>(op, of);
+#pragma unroll
+    for (int e = 0; e < E; ++e) of[e] = w ? fmaf(wt, yf[e], of[e]) : of[e] + yf[e];
+    store16<T>(op, of);
+  } else {
+    store16<T>(op, yf);
+  }
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void mod_scatter_scalar_kernel(
+    T* __restrict__ out, const T* __restrict__ y, const int64_t* __restrict__ idx,
+    const float* __restrict__ w, int64_t total, int64_t D, int64_t k, int64_t L,
+    int64_t o_bs, int64_t o_ls) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int64_t r = t / D, c = t - r * D;
+  const int64_t b = r / k;
+  const int64_t dst = idx[r];
+  if (dst < 0 || dst >= L) return;
+  T* op = out + b * o_bs + dst * o_ls + c;
+  const float yv = to_f32(y[t]);
+  if (MODE == HYDRA_SCATTER_ADD) {
+    *op = from_f32<T>(w ? fmaf(w[r], yv, to_f32(*op)) : to_f32(*op) + yv);
+  } else {
+    *op = from_f32<T>(yv);
+  }
+}
+
+}  // namespace hydra
+
+using namespace hydra;
+
+static int max_lds_per_block() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 65536;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+    return 65536;
+  return v;
+}
+
+extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t s_rs,
+                              int64_t k, int64_t* idx_desc, int64_t* idx_sorted,
+                              void* mask, int score_dtype, int mask_dtype,
+                              void* stream) {
+  HYDRA_REQUIRE(B >= 0, "mod_topk: negative batch");
+  HYDRA_REQUIRE(L >= 1 && L <= 16384, "mod_topk: need 1 <= L <= 16384");
+  HYDRA_REQUIRE(k >= 1 && k <= L, "mod_topk: need 1 <= k <= L");
+  HYDRA_REQUIRE(s_rs >= L, "mod_topk: row stride smaller than L");
+  HYDRA_REQUIRE(mask_dtype == HYDRA_F32 || mask_dtype == HYDRA_BF16 || mask_dtype == HYDRA_F16,
+                "mod_topk: unknown mask dtype code");
+  HYDRA_REQUIRE(B <= 65535, "mod_topk: B must be <= 65535");
+  if (B == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(scores != nullptr, "mod_topk: null scores");
+  int P = 64;
+  while (P < L) P <<= 1;
+  const size_t lds = sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);
+  if (lds + 1024 > static_cast<size_t>(max_lds_per_block()))
+    return fail(HYDRA_ERR_UNSUPPORTED, "mod_topk: row does not fit in LDS on this device");
+  auto st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(B));
+  switch (score_dtype) {
+    case HYDRA_F32:
+      mod_topk_kernel<float><<<grid, kTopkThreads, lds, st>>>(
+          static_cast<const float*>(scores), (int)L, s_rs, (int)k, P, idx_desc,
+          idx_sorted, mask, mask_dtype);
+      break;
+    case HYDRA_BF16:
+      mod_topk_kernel<bf16><<<grid, kTopkThreads, lds, st>>>(
+          static_cast<const bf16*>(scores), (int)L, s_rs, (int)k, P, idx_desc,
+          idx_sorted, mask, mask_dtype);
+      break;
+    case HYDRA_F16:
+      mod_topk_kernel<f16><<<grid, kTopkThreads, lds, st>>>(
+          static_cast<const f16*>(scores), (int)L, s_rs, (int)k, P, idx_desc,
+          idx_sorted, mask, mask_dtype);
+      break;
+    default:
+      return fail(HYDRA_ERR_ARG, "mod_topk: unknown score dtype code");
+  }
+  return check_launch("mod_topk_kernel");
+}
+
+template <typename T>
+static int launch_gather(const void* x, const int64_t* idx, void* xs, int64_t B,
+                         int64_t L, int64_t k, int64_t D, int64_t x_bs, int64_t x_ls,
+                         hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  const int64_t cpr = D / E;
+  const int64_t total_vec = B * k * cpr;
+  const bool vec_ok = D % E == 0 && x_bs % E == 0 && x_ls % E == 0 && aligned16(x) &&
+                      aligned16(xs) && total_vec < (int64_t(1) << 31) && B * k < (int64_t(1) << 31);
+  if (vec_ok) {
+    const dim3 grid(static_cast<unsigned>((total_vec + 255) / 256));
+    mod_gather_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(x), idx,
+                                                static_cast<T*>(xs), (uint32_t)total_vec,
+                                                (uint32_t)cpr, (uint32_t)k, L, x_bs, x_ls);
+    return check_launch("mod_gather_kernel");
+  }
+  const int64_t total = B * k * D;
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  mod_gather_scalar_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(x), idx,
+                                                     static_cast<T*>(xs), total, D, k, L,
+                                                     x_bs, x_ls);
+  return check_launch("mod_gather_scalar_kernel");
+}
+
+extern "C" int hydra_mod_gather(const void* x, const int64_t* idx, void* xs, int64_t B,
+                                int64_t L, int64_t k, int64_t D, int64_t x_bs,
+                                int64_t x_ls, int dtype, void* stream) {
+  HYDRA_REQUIRE(B >= 0 && L >= 0 && k >= 0 && D >= 0, "mod_gather: negative size");
+  if (B * k * D == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(x && idx && xs, "mod_gather: null pointer");
+  HYDRA_REQUIRE(x_ls >= D, "mod_gather: row stride smaller than D");
+  HYDRA_REQUIRE((B * k * D + 255) / 256 < (int64_t(1) << 31), "mod_gather: too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_gather<T>(x, idx, xs, B, L, k, D, x_bs, x_ls, st);
+  });
+}
+
+template <typename T>
+static int launch_scatter(void* out, const void* y, const int64_t* idx, const float* w,
+                          int64_t B, int64_t L, int64_t k, int64_t D, int64_t o_bs,
+                          int64_t o_ls, int mode, hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  const int64_t cpr = D / E;
+  const int64_t total_vec = B * k * cpr;
+  auto O = static_cast<T*>(out);
+  auto Y = static_cast<const T*>(y);
+  const bool vec_ok = D % E == 0 && o_bs % E == 0 && o_ls % E == 0 && aligned16(out) &&
+                      aligned16(y) && total_vec < (int64_t(1) << 31) && B * k < (int64_t(1) << 31);
+  if (vec_ok) {
+    const dim3 grid(static_cast<unsigned>((total_vec + 255) / 256));
+    if (mode == HYDRA_SCATTER_ADD)
+      mod_scatter_kernel<T, HYDRA_SCATTER_ADD><<<grid, 256, 0, st>>>(
+          O, Y, idx, w, (uint32_t)total_vec, (uint32_t)cpr, (uint32_t)k, L, o_bs, o_ls);
+    else
+      mod_scatter_kernel<T, HYDRA_SCATTER_REPLACE><<<grid, 256, 0, st>>>(
+          O, Y, idx, w, (uint32_t)total_vec, (uint32_t)cpr, (uint32_t)k, L, o_bs, o_ls);
+    return check_launch("mod_scatter_kernel");
+  }
+  const int64_t total = B * k * D;
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  if (mode == HYDRA_SCATTER_ADD)
+    mod_scatter_scalar_kernel<T, HYDRA_SCATTER_ADD><<<grid, 256, 0, st>>>(
+        O, Y, idx, w, total, D, k, L, o_bs, o_ls);
+  else
+    mod_scatter_scalar_kernel<T, HYDRA_SCATTER_REPLACE><<<grid, 256, 0, st>>>(
+        O, Y, idx, w, total, D, k, L, o_bs, o_ls);
+  return check_launch("mod_scatter_scalar_kernel");
+}
+
+extern "C" int hydra_mod_scatter(void* out, const void* y, const int64_t* idx,
+                                 const float* w, int64_t B, int64_t L, int64_t k,
+                                 int64_t D, int64_t o_bs, int64_t o_ls, int mode,
+                                 int dtype, void* stream) {
+  HYDRA_REQUIRE(B >= 0 && L >= 0 && k >= 0 && D >= 0, "mod_scatter: negative size");
+  HYDRA_REQUIRE(mode == HYDRA_SCATTER_ADD || mode == HYDRA_SCATTER_REPLACE,
+                "mod_scatter: unknown mode");
+  HYDRA_REQUIRE(w == nullptr || mode == HYDRA_SCATTER_ADD,
+                "mod_scatter: weights apply to the ADD mode only");
+  if (B * k * D == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(out && y && idx, "mod_scatter: null pointer");
+  HYDRA_REQUIRE(o_ls >= D, "mod_scatter: row stride smaller than D");
+  HYDRA_REQUIRE((B * k * D + 255) / 256 < (int64_t(1) << 31), "mod_scatter: too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_scatter<T>(out, y, idx, w, B, L, k, D, o_bs, o_ls, mode, st);
+  });
+}

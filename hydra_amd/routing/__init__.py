@@ -1,0 +1,11 @@
+"""hydra_amd.routing -- Mixture-of-Depths hard routing (hydra/routing)."""
+from .base import BaseRouter
+from .mixture_of_depths import MixtureOfDepthsBlock, MoDMLPWrapper, MoDRouter
+from .ops import (compute_capacity_k, gather_by_indices, mod_topk, router_k,
+                  scatter_add_by_indices, scatter_replace, weighted_residual_scatter)
+
+__all__ = [
+    "BaseRouter", "MoDRouter", "MixtureOfDepthsBlock", "MoDMLPWrapper",
+    "compute_capacity_k", "router_k", "mod_topk", "gather_by_indices",
+    "scatter_add_by_indices", "weighted_residual_scatter", "scatter_replace",
+]

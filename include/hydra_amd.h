@@ -1,0 +1,193 @@
+/*
+ * hydra_amd.h -- C ABI of the MI355X (gfx950) hot path of HYDRA.
+ *
+ * Every entry point takes plain device pointers, sizes and strides (in
+ * elements), and a HIP stream passed as `void*` (a hipStream_t; NULL is the
+ * null stream).  Nothing here allocates device memory except where a comment
+ * says so, nothing synchronises the host, and every launch goes on `stream`.
+ *
+ * Return value: 0 on success, otherwise one of HYDRA_ERR_*; the message for
+ * the last failure on the calling thread is returned by hydra_last_error().
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the mcpirate17/HYDRA tree).
+ */
+#ifndef HYDRA_AMD_H
+#define HYDRA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes and element types ------------------------------------ */
+#define HYDRA_OK            0
+#define HYDRA_ERR_ARG       1  /* bad shape / stride / dtype / flag          */
+#define HYDRA_ERR_LAUNCH    2  /* a HIP launch or runtime call failed        */
+#define HYDRA_ERR_UNSUPPORTED 3 /* valid request this build does not cover   */
+
+#define HYDRA_F32  0
+#define HYDRA_BF16 1
+#define HYDRA_F16  2
+
+/* Message of the last failure on this thread ("" if none). */
+const char* hydra_last_error(void);
+/* ABI version (major*10000 + minor*100 + patch). */
+int hydra_abi_version(void);
+
+/* ---- fused element ops (hydra/kernels/fused_ops.py) -------------------- */
+
+/* RMSNorm forward: y[r,:] = x[r,:] * rsqrt(mean(x[r,:]^2) + eps) * w, with the
+ * sum of squares and the products in fp32, one rounding into `dtype`.
+ * Replaces fused_rms_norm (hydra/kernels/fused_ops.py:1114-1132) and its
+ * kernel _fused_rms_norm_kernel (fused_ops.py:969-1007).
+ * x: [rows, dim] with row stride x_rs; w: [dim] (same dtype);
+ * y: [rows, dim] with row stride y_rs. */
+int hydra_rms_norm_fwd(const void* x, const void* w, void* y,
+                       int64_t rows, int64_t dim, int64_t x_rs, int64_t y_rs,
+                       float eps, int dtype, void* stream);
+
+/* RoPE forward on interleaved pairs:
+ *   o[..,2i]   = x[..,2i]*cos[s,i] - x[..,2i+1]*sin[s,i]
+ *   o[..,2i+1] = x[..,2i]*sin[s,i] + x[..,2i+1]*cos[s,i]
+ * Replaces fused_rope (hydra/kernels/fused_ops.py:240-258) and
+ * _fused_rope_triton / _fused_rope_kernel (fused_ops.py:185-297).
+ * x: [B,H,S,D] with element strides xs[4] (xs[3] must be 1);
+ * cos/sin: [S, D/2] with row stride cs_rs (element stride 1), type cs_dtype;
+ * out: contiguous [B,H,S,D] in `dtype`. */
+int hydra_rope_fwd(const void* x, const void* cos, const void* sin, void* out,
+                   int64_t B, int64_t H, int64_t S, int64_t D,
+                   const int64_t* xs, int64_t cs_rs, int dtype, int cs_dtype,
+                   void* stream);
+
+/* SwiGLU activation: out = silu(gate) * up, fp32 math, one rounding.
+ * Replaces fused_swiglu (hydra/kernels/fused_ops.py:808-820) and
+ * _fused_swiglu_kernel (fused_ops.py:703-725).  gate/up may be the two
+ * halves of one [rows, 2*hidden] tensor (row strides g_rs/u_rs);
+ * out: [rows, hidden] with row stride o_rs. */
+int hydra_swiglu_fwd(const void* gate, const void* up, void* out,
+                     int64_t rows, int64_t hidden,
+                     int64_t g_rs, int64_t u_rs, int64_t o_rs,
+                     int dtype, void* stream);
+
+/* QK L2-normalisation + scale:
+ *   q_out = q * rsqrt(sum(q^2) + 1e-8) * scale
+ *   k_out = k * rsqrt(sum(k^2) + 1e-8) * scale * temperature
+ * Replaces fused_qk_norm (hydra/kernels/fused_ops.py:474-493) and
+ * _fused_qk_norm_kernel (fused_ops.py:323-369).  q: [q_rows, hd],
+ * k: [k_rows, hd], all contiguous, same dtype. */
+int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
+                      int64_t q_rows, int64_t k_rows, int64_t hd,
+                      float scale, float temperature, int dtype, void* stream);
+
+/* ---- CCGQA attention (hydra/attention/backends/ccgqa) ------------------ */
+
+/* Feature bits of hydra_ccgqa_prep_fwd, mirroring the CCGQAAttention ctor
+ * switches (attention.py:74-88). */
+#define HYDRA_CCGQA_CONVS       1
+#define HYDRA_CCGQA_QK_MEAN     2
+#define HYDRA_CCGQA_VALUE_SHIFT 4
+#define HYDRA_CCGQA_QK_NORM     8
+#define HYDRA_CCGQA_ROPE        16
+
+/* Everything of CCGQAAttention.forward between the qkv GEMM and the attention
+ * core, in one pass over token tiles: split of the fused projection, value
+ * shift, causal grouped conv1 + dense conv2 (k=3, each left-padded by 2) on q
+ * and k, QK-mean coupling from the pre-conv q/k, L2-norm of q and of k times
+ * the key temperature, and RoPE.  Replaces attention.py:205-266 with
+ * OptimizedConvSequence.forward (kernels/fused_conv.py:39-62).
+ *
+ * qkv:  [B, S, L + 2K] (row stride qkv_rs), L = Hq*hd, K = Hkv*hd; column
+ *       order q | k | v_curr | v_prev (v: | v when no value shift).
+ * wq1:  conv1 of q, PyTorch Conv1d layout [L, hd, 3]; wq2: [L, L, 3];
+ * wk1:  [K, hd, 3];                                    wk2: [K, K, 3];
+ *       (unused and may be NULL without HYDRA_CCGQA_CONVS).
+ * temp: key temperature, 1 element of `dtype` (NULL without QK_NORM).
+ * cos/sin: fp32 [S, hd/2] row stride cs_rs (NULL without ROPE).
+ * q_out: [B, Hq, S, hd]; k_out, v_out: [B, Hkv, S, hd]; all contiguous. */
+int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
+                         const void* wq1, const void* wq2,
+                         const void* wk1, const void* wk2,
+                         const void* temp, const float* cos, const float* sin,
+                         int64_t cs_rs,
+                         void* q_out, void* k_out, void* v_out,
+                         int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                         int64_t hd, int flags, int dtype, void* stream);
+
+/* Key-mask modes of hydra_attn_fwd (key_mask: uint8 [B,S], nonzero = keep).
+ * KEY_PADDING: key t is visible to query s iff key_mask[b,t] != 0 (and t <= s
+ *   when causal).
+ * REFERENCE_SDPA: the literal behaviour of CCGQAAttention.forward when it is
+ *   given a padding mask (attention.py:268-299): it builds
+ *   triu(1) | (mask == 0) as "True = masked" and hands it to SDPA, whose
+ *   boolean masks mean "True = attend", so key t is visible to query s iff
+ *   t > s or key_mask[b,t] == 0.  Kept for result parity; requires causal=1. */
+#define HYDRA_MASK_NONE           0
+#define HYDRA_MASK_KEY_PADDING    1
+#define HYDRA_MASK_REFERENCE_SDPA 2
+
+/* Causal / full GQA softmax attention forward:
+ *   o[b,h,s] = sum_{t visible} softmax_t(scale * q[b,h,s].k[b,j,t]) v[b,j,t]
+ * with j = h / (Hq/Hkv) (repeat_interleave order), "visible" = t <= s when
+ * causal, refined by mask_mode.
+ * Replaces ccgqa_attention_fused (kernels/fused_attention.py:826-840, kernels
+ * _fwd_gqa_kernel :14-110 and _fwd_kernel :341-429) and the SDPA call of
+ * CCGQAAttention.forward (attention.py:268-327).
+ * q: [B,Hq,S,hd], k/v: [B,Hkv,S,hd], element strides qs/ks/vs[4] (last = 1);
+ * o: element strides os[4] (last = 1) -- pass the strides of a [B,S,Hq,hd]
+ *    buffer to write the merged-heads layout directly;
+ * lse: optional fp32 [B,Hq,S] natural-log sum-exp of the scaled scores.
+ * A query row with no visible key gets o = 0 (as CPU SDPA) and lse = -inf.
+ * bf16 with hd in {16,32,64,128} runs on MFMA; other cases on the VALU. */
+int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                   float* lse, const uint8_t* key_mask, int mask_mode,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                   const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                   const int64_t* os, int causal, float scale, int dtype,
+                   void* stream);
+
+/* ---- Mixture-of-Depths hard routing (hydra/routing, model/framework) --- */
+
+/* Per-row top-k of router scores, ties broken by the lower index, in the
+ * total order of torch.topk(largest=True) (NaN above +inf, -0.0 == +0.0).
+ * Replaces torch.topk + mask.scatter_ in MoDRouter.forward
+ * (hydra/routing/mixture_of_depths.py:179-191) and the torch.sort of the
+ * indices in MoDMLPWrapper._forward_hard (model/framework/blocks.py:261).
+ * scores: [B, L] (row stride s_rs) of score_dtype (HYDRA_F32/BF16/F16);
+ * idx_desc: int64 [B, k] in value-descending order (may be NULL);
+ * idx_sorted: int64 [B, k] ascending (may be NULL);
+ * mask: [B, L] of mask_dtype, 1 for selected tokens else 0 (may be NULL).
+ * Limits: 1 <= k <= L <= 16384. */
+int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t s_rs,
+                   int64_t k, int64_t* idx_desc, int64_t* idx_sorted,
+                   void* mask, int score_dtype, int mask_dtype, void* stream);
+
+/* Row gather: xs[b,j,:] = x[b, idx[b,j], :].
+ * Replaces gather_by_indices (hydra/routing/ops.py:257-272) and the gather
+ * of MoDMLPWrapper._forward_hard (blocks.py:263-264).
+ * x: [B, L, D] (strides x_bs, x_ls; unit stride on D); idx: int64 [B, k];
+ * xs: contiguous [B, k, D].  Indices must lie in [0, L). */
+int hydra_mod_gather(const void* x, const int64_t* idx, void* xs,
+                     int64_t B, int64_t L, int64_t k, int64_t D,
+                     int64_t x_bs, int64_t x_ls, int dtype, void* stream);
+
+#define HYDRA_SCATTER_ADD     0 /* out[b,idx] += w * y  (residual add)    */
+#define HYDRA_SCATTER_REPLACE 1 /* out[b,idx]  = y      (clone + scatter) */
+
+/* In-place weighted residual scatter into out: [B, L, D] (strides o_bs,
+ * o_ls), from y: contiguous [B, k, D], at idx: int64 [B, k] (distinct per
+ * row).  w: optional fp32 [B, k] per-row weights (NULL = 1).  ADD replaces
+ * the zeros_like + scatter_ + residual add of MoDMLPWrapper._forward_hard
+ * and its caller (blocks.py:266-268, :603); REPLACE replaces the
+ * clone + scatter_ of MixtureOfDepthsBlock.forward
+ * (mixture_of_depths.py:291-295).  Sums are fp32, one rounding. */
+int hydra_mod_scatter(void* out, const void* y, const int64_t* idx,
+                      const float* w, int64_t B, int64_t L, int64_t k,
+                      int64_t D, int64_t o_bs, int64_t o_ls, int mode,
+                      int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HYDRA_AMD_H */

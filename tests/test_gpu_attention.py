@@ -1,0 +1,149 @@
+"""GPU parity of the attention core (hydra_attn_fwd) against the CPU oracle
+(SDPA restatement of attention.py:268-327, itself pinned to an fp64 brute
+force).  bf16 runs on the MFMA kernel, fp32/fp16 and odd head dims on the
+generic kernel.  Inputs are bf16-representable so both sides see identical
+values; the oracle runs in fp32.  Tolerance: 2e-2 (bf16), 1e-5 (fp32)."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import max_rel_err
+from oracle import ccgqa as occ
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(B, Hq, Hkv, S, hd, seed):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16).float()
+    return mk(B, Hq, S, hd), mk(B, Hkv, S, hd), mk(B, Hkv, S, hd)
+
+
+CASES = [
+    # B, Hq, Hkv, S, hd
+    (4, 4, 1, 512, 64),
+    (2, 8, 2, 512, 16),
+    (1, 4, 4, 257, 32),
+    (2, 8, 1, 100, 128),
+    (1, 2, 2, 1, 64),
+    (1, 4, 2, 31, 64),
+    (3, 6, 3, 65, 16),
+]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
+def test_attention_bf16_mfma(cuda, case, causal):
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    B, Hq, Hkv, S, hd = case
+    q, k, v = _qkv(*case, seed=sum(case))
+    out, lse = attention_forward(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)),
+                                 causal=causal, want_lse=True)
+    ref = occ.attention(q, k, v, causal=causal)
+    assert max_rel_err(out.cpu(), ref) < 2e-2
+    # LSE: log sum_t exp(scale * q.k_t) over visible keys
+    G = Hq // Hkv
+    kk = k.repeat_interleave(G, 1)
+    logits = (q @ kk.transpose(-1, -2)) / math.sqrt(hd)
+    if causal:
+        logits = logits.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    ref_lse = torch.logsumexp(logits, -1)
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("case", [(2, 8, 2, 512, 16), (1, 4, 1, 77, 64), (1, 2, 1, 19, 6)])
+def test_attention_generic(cuda, dtype, case):
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    q, k, v = _qkv(*case, seed=3)
+    out, _ = attention_forward(*(t.to(cuda, dtype) for t in (q, k, v)), causal=True)
+    ref = occ.attention(q, k, v, causal=True)
+    assert max_rel_err(out.cpu(), ref) < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attention_reference_mask_mode(cuda, dtype):
+    """mask_mode REFERENCE_SDPA reproduces attention.py:268-299 literally."""
+    from hydra_amd.attention.backends.ccgqa.ops import MASK_REFERENCE_SDPA, attention_forward
+
+    B, Hq, Hkv, S, hd = 2, 4, 2, 70, 32
+    q, k, v = _qkv(B, Hq, Hkv, S, hd, seed=11)
+    g = torch.Generator().manual_seed(12)
+    mask = (torch.rand(B, S, generator=g) > 0.2).long()
+    mask[:, 0] = 1
+    out, _ = attention_forward(*(t.to(cuda, dtype) for t in (q, k, v)), causal=True,
+                               key_mask=mask.to(cuda), mask_mode=MASK_REFERENCE_SDPA)
+    ref = occ.attention(q, k, v, causal=True, mask=mask)
+    assert max_rel_err(out.cpu(), ref) < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attention_key_padding_mode(cuda, dtype):
+    from hydra_amd.attention.backends.ccgqa.ops import MASK_KEY_PADDING, attention_forward
+
+    B, Hq, Hkv, S, hd = 2, 4, 1, 90, 64
+    q, k, v = _qkv(B, Hq, Hkv, S, hd, seed=13)
+    g = torch.Generator().manual_seed(14)
+    mask = (torch.rand(B, S, generator=g) > 0.3).long()
+    mask[:, 0] = 1
+    out, _ = attention_forward(*(t.to(cuda, dtype) for t in (q, k, v)), causal=True,
+                               key_mask=mask.to(cuda), mask_mode=MASK_KEY_PADDING)
+    ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
+    assert max_rel_err(out.cpu(), ref) < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+def test_attention_fully_masked_row_is_zero(cuda):
+    from hydra_amd.attention.backends.ccgqa.ops import MASK_KEY_PADDING, attention_forward
+
+    q, k, v = _qkv(1, 2, 1, 40, 64, seed=15)
+    mask = torch.ones(1, 40, dtype=torch.long)
+    mask[0, :5] = 0  # queries 0..4 see no key
+    out, lse = attention_forward(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), causal=True,
+                                 key_mask=mask.to(cuda), mask_mode=MASK_KEY_PADDING, want_lse=True)
+    assert torch.count_nonzero(out[:, :, :5].cpu()) == 0
+    assert torch.isinf(lse[:, :, :5].cpu()).all()
+    assert torch.isfinite(out.cpu()).all()
+
+
+def test_attention_c3_full_size(cuda):
+    """Config 3 core at full size: B4, Hq4/Hkv1, S4096, hd64, causal."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    q, k, v = _qkv(4, 4, 1, 4096, 64, seed=21)
+    out, _ = attention_forward(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), causal=True)
+    ref = occ.attention(q, k, v, causal=True)
+    assert max_rel_err(out.cpu(), ref) < 2e-2
+
+
+def test_attention_merged_output_layout(cuda):
+    """Writing straight into a [B,S,Hq,hd] buffer equals the transposed copy."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    B, Hq, Hkv, S, hd = 2, 4, 1, 130, 64
+    q, k, v = (t.to(cuda, torch.bfloat16) for t in _qkv(B, Hq, Hkv, S, hd, seed=22))
+    o1, _ = attention_forward(q, k, v, causal=True)
+    buf = torch.empty(B, S, Hq, hd, dtype=torch.bfloat16, device=cuda)
+    attention_forward(q, k, v, causal=True, out=buf.transpose(1, 2))
+    assert torch.equal(buf.transpose(1, 2).cpu(), o1.cpu())
+
+
+def test_ccgqa_attention_fused_api(cuda):
+    from hydra_amd.attention.backends.ccgqa.kernels import ccgqa_attention_fused
+
+    q, k, v = _qkv(2, 4, 2, 96, 32, seed=23)
+    out = ccgqa_attention_fused(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), is_causal=True)
+    assert max_rel_err(out.cpu(), occ.attention(q, k, v, causal=True)) < 2e-2
+
+
+def test_attention_deterministic(cuda):
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    q, k, v = (t.to(cuda, torch.bfloat16) for t in _qkv(2, 4, 1, 300, 64, seed=24))
+    a, _ = attention_forward(q, k, v, causal=True)
+    b, _ = attention_forward(q, k, v, causal=True)
+    assert torch.equal(a, b)

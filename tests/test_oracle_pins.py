@@ -1,0 +1,355 @@
+"""Pins of the CPU oracle (oracle/) -- CPU only.
+
+Each oracle function is checked against something independent of its own
+formula: a brute-force fp64 loop, a closed form at a chosen point, an
+invariant, a library routine it must agree with, the reference's own
+equivalence tests (restated), or the golden vectors written by running the
+reference (tests/golden/make_golden.py).  The checks are chosen so a dropped
+term, a flipped sign, a wrong tap order or a transposed operand fails one.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import GOLDEN, bf16_from_bits, max_rel_err
+from oracle import ccgqa as occ
+from oracle import fused_ops as ofo
+from oracle import mod as omod
+
+
+# ---------------------------------------------------------------- fused ops
+def test_rms_norm_bruteforce_and_invariant():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 7, 33, generator=g, dtype=torch.float64)
+    w = 1 + 0.1 * torch.randn(33, generator=g, dtype=torch.float64)
+    y = ofo.rms_norm(x, w, 1e-6)
+    for r in range(3):
+        for s in range(7):
+            ms = sum(float(v) ** 2 for v in x[r, s]) / 33
+            ref = [float(x[r, s, i]) / math.sqrt(ms + 1e-6) * float(w[i]) for i in range(33)]
+            assert np.allclose(y[r, s].numpy(), ref, rtol=1e-12, atol=1e-12)
+    # invariant: rms(y / w) == 1 (eps negligible here)
+    rms = (y / w).pow(2).mean(-1).sqrt()
+    assert torch.allclose(rms, torch.ones_like(rms), atol=1e-6)
+    # the Triton-arithmetic variant agrees in fp32
+    assert max_rel_err(ofo.rms_norm_fp32(x.float(), w.float()), y) < 1e-6
+
+
+def test_rope_known_answer_and_norm():
+    # One pair rotated by a known angle: position s, pair i has angle s * theta^(-2i/D).
+    D, S = 4, 3
+    cos, sin = ofo.rope_cache(D, S)
+    x = torch.zeros(1, 1, S, D)
+    x[..., 0] = 1.0  # pair 0 = (1, 0)
+    x[..., 3] = 1.0  # pair 1 = (0, 1)
+    y = ofo.rope(x, cos, sin)
+    for s in range(S):
+        a0 = s * 1.0
+        a1 = s * 10000.0 ** (-2 / D)
+        # (1,0) -> (cos a, sin a); (0,1) -> (-sin a, cos a)
+        assert math.isclose(y[0, 0, s, 0].item(), math.cos(a0), abs_tol=1e-6)
+        assert math.isclose(y[0, 0, s, 1].item(), math.sin(a0), abs_tol=1e-6)
+        assert math.isclose(y[0, 0, s, 2].item(), -math.sin(a1), abs_tol=1e-6)
+        assert math.isclose(y[0, 0, s, 3].item(), math.cos(a1), abs_tol=1e-6)
+    # position 0 is the identity; every pair keeps its norm
+    g = torch.Generator().manual_seed(1)
+    xr = torch.randn(2, 3, 9, 16, generator=g)
+    cos, sin = ofo.rope_cache(16, 9)
+    yr = ofo.rope(xr, cos, sin)
+    assert torch.equal(yr[:, :, 0], xr[:, :, 0])
+    pn = lambda t: t.reshape(*t.shape[:-1], -1, 2).norm(dim=-1)
+    assert torch.allclose(pn(yr), pn(xr), atol=1e-5)
+
+
+def test_rope_matches_reference_fallback_test():
+    """tests/test_ccgqa_attention_refactors.py:161-196 restated: the even/odd
+    slot formula, bit-exact."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 4, 32, 16, generator=g)
+    cos, sin = ofo.rope_cache(16, 128)
+    c, s = cos[:, :, :32], sin[:, :, :32]
+    ref = torch.empty_like(x)
+    x1, x2 = x[..., ::2], x[..., 1::2]
+    ref[..., ::2] = x1 * c - x2 * s
+    ref[..., 1::2] = x1 * s + x2 * c
+    assert torch.equal(ofo.rope(x, cos, sin), ref)
+
+
+def test_swiglu_closed_form():
+    g = torch.Generator().manual_seed(2)
+    gate = torch.randn(5, 17, generator=g, dtype=torch.float64) * 4
+    up = torch.randn(5, 17, generator=g, dtype=torch.float64)
+    ref = gate / (1 + torch.exp(-gate)) * up
+    assert torch.allclose(ofo.swiglu(gate, up), ref, rtol=1e-12, atol=1e-12)
+    assert ofo.swiglu(torch.tensor([0.0]), torch.tensor([5.0])).item() == 0.0
+    assert max_rel_err(ofo.swiglu_fp32(gate.float(), up.float()), ref) < 1e-6
+
+
+def test_qk_norm_norms():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 4, 5, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(2, 2, 5, 16, generator=g, dtype=torch.float64)
+    qn, kn = ofo.qk_norm(q, k, 3.0, 0.5)
+    assert torch.allclose(qn.norm(dim=-1), torch.full((2, 4, 5), 3.0, dtype=torch.float64))
+    assert torch.allclose(kn.norm(dim=-1), torch.full((2, 2, 5), 1.5, dtype=torch.float64))
+    # direction preserved
+    assert torch.allclose(qn / 3.0 * q.norm(dim=-1, keepdim=True), q)
+    qt, kt = ofo.qk_norm_triton_formula(q.float(), k.float(), 3.0, 0.5)
+    assert max_rel_err(qt, qn) < 1e-6 and max_rel_err(kt, kn) < 1e-6
+
+
+def test_fused_ops_golden():
+    d = np.load(GOLDEN / "fused_ops_cpu.npz")
+    x, w = bf16_from_bits(d["x"]), bf16_from_bits(d["w"])
+    assert torch.equal(ofo.rms_norm(x, w, float(d["eps"])), torch.from_numpy(d["rms_out"]))
+    gate, up = bf16_from_bits(d["gate"]), bf16_from_bits(d["up"])
+    assert torch.equal(ofo.swiglu(gate, up), torch.from_numpy(d["swiglu_out"]))
+    xr = bf16_from_bits(d["xr"])
+    cos, sin = torch.from_numpy(d["cos"]), torch.from_numpy(d["sin"])
+    assert torch.equal(ofo.rope(xr, cos, sin), torch.from_numpy(d["rope_out"]))
+    q, k = bf16_from_bits(d["q"]), bf16_from_bits(d["k"])
+    qn, kn = ofo.qk_norm(q, k, float(d["scale"]), float(d["temperature"]))
+    assert torch.equal(qn, torch.from_numpy(d["qn_out"]))
+    assert torch.equal(kn, torch.from_numpy(d["kn_out"]))
+
+
+# -------------------------------------------------------------------- CCGQA
+def _conv_bruteforce(x, w1, w2, groups1):
+    """fp64 triple loop: y[s,o] = sum_t sum_c w[o,c,t] * u[s+t-2, c], u = 0 for s<0."""
+    B, N, C = x.shape
+    cpg = C // groups1
+    y1 = torch.zeros(B, N, C, dtype=torch.float64)
+    for b in range(B):
+        for s in range(N):
+            for o in range(C):
+                g = o // cpg
+                acc = 0.0
+                for t in range(3):
+                    src = s + t - 2
+                    if src < 0:
+                        continue
+                    for c in range(cpg):
+                        acc += float(w1[o, c, t]) * float(x[b, src, g * cpg + c])
+                y1[b, s, o] = acc
+    y2 = torch.zeros(B, N, C, dtype=torch.float64)
+    for b in range(B):
+        for s in range(N):
+            for o in range(C):
+                acc = 0.0
+                for t in range(3):
+                    src = s + t - 2
+                    if src < 0:
+                        continue
+                    for c in range(C):
+                        acc += float(w2[o, c, t]) * float(y1[b, src, c])
+                y2[b, s, o] = acc
+    return y2
+
+
+def test_causal_conv_seq_bruteforce_and_causality():
+    g = torch.Generator().manual_seed(4)
+    B, N, C, G = 2, 7, 6, 3
+    x = torch.randn(B, N, C, generator=g, dtype=torch.float64)
+    w1 = torch.randn(C, C // G, 3, generator=g, dtype=torch.float64)
+    w2 = torch.randn(C, C, 3, generator=g, dtype=torch.float64)
+    y = occ.causal_conv_seq(x, w1, w2, G)
+    assert torch.allclose(y, _conv_bruteforce(x, w1, w2, G), rtol=1e-10, atol=1e-10)
+    # causality: perturbing token 4 leaves outputs 0..3 unchanged, changes 4..6
+    x2 = x.clone()
+    x2[:, 4] += 1.0
+    y2 = occ.causal_conv_seq(x2, w1, w2, G)
+    assert torch.equal(y2[:, :4], y[:, :4])
+    assert not torch.allclose(y2[:, 4:], y[:, 4:])
+
+
+def _cfg(**kw):
+    base = dict(dim=64, n_heads=4, n_kv_heads=2, compression_factor=2, max_seq_len=128)
+    base.update(kw)
+    return occ.CCGQAConfig(**base)
+
+
+def test_value_shift_matches_padcat():
+    """tests/test_ccgqa_attention_refactors.py:109-132 restated."""
+    cfg = _cfg(use_rope=False, use_qk_norm=False, use_convs=False, use_qk_mean=False)
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(2, 32, cfg.latent_dim + 2 * cfg.kv_dim, generator=g)
+    _, _, v = occ.prep({}, qkv, cfg)
+    L, K = cfg.latent_dim, cfg.kv_dim
+    v_curr, v_prev = qkv[..., L + K:L + K + K // 2], qkv[..., L + K + K // 2:]
+    v_ref = torch.cat([v_curr, F.pad(v_prev[:, :-1, :], (0, 0, 1, 0))], dim=-1)
+    v_ref = v_ref.view(2, 32, cfg.n_kv_heads, cfg.head_dim).transpose(1, 2)
+    assert torch.equal(v, v_ref)
+
+
+def test_qk_mean_headspace_matches_expand():
+    """tests/test_ccgqa_attention_refactors.py:135-158 restated."""
+    cfg = _cfg(use_rope=False, use_qk_norm=False, use_convs=False, use_value_shift=False)
+    g = torch.Generator().manual_seed(0)
+    B, S = 2, 32
+    L, K, hd = cfg.latent_dim, cfg.kv_dim, cfg.head_dim
+    qkv = torch.randn(B, S, L + 2 * K, generator=g)
+    q, k, _ = occ.prep({}, qkv, cfg)
+    q0, k0 = qkv[..., :L], qkv[..., L:L + K]
+    qm = q0.view(B, S, cfg.n_heads, hd).mean(2)
+    km = k0.view(B, S, cfg.n_kv_heads, hd).mean(2)
+    q_old = q0 + 0.5 * km.unsqueeze(2).expand(-1, -1, cfg.n_heads, -1).reshape(B, S, L)
+    k_old = k0 + 0.5 * qm.unsqueeze(2).expand(-1, -1, cfg.n_kv_heads, -1).reshape(B, S, K)
+    assert torch.equal(q, q_old.view(B, S, cfg.n_heads, hd).transpose(1, 2))
+    assert torch.equal(k, k_old.view(B, S, cfg.n_kv_heads, hd).transpose(1, 2))
+
+
+def test_qk_mean_uses_preconv_values():
+    """The coupling term comes from q/k before the convs: with zero conv
+    weights the conv path contributes nothing and q == 0.5 * mean(k_pre)."""
+    cfg = _cfg(use_rope=False, use_qk_norm=False, use_value_shift=False)
+    g = torch.Generator().manual_seed(5)
+    params = occ.init_params(cfg, g)
+    for n in list(params):
+        if "conv" in n:
+            params[n] = torch.zeros_like(params[n])
+    qkv = torch.randn(1, 6, cfg.latent_dim + 2 * cfg.kv_dim, generator=g)
+    q, _, _ = occ.prep(params, qkv, cfg)
+    L, K, hd = cfg.latent_dim, cfg.kv_dim, cfg.head_dim
+    km = qkv[..., L:L + K].view(1, 6, cfg.n_kv_heads, hd).mean(2)
+    assert torch.allclose(q, (0.5 * km).unsqueeze(1).expand(-1, cfg.n_heads, -1, -1))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("use_mask", [False, True])
+def test_attention_bruteforce(causal, use_mask):
+    g = torch.Generator().manual_seed(6)
+    B, Hq, Hkv, S, hd = 2, 4, 2, 9, 8
+    q = torch.randn(B, Hq, S, hd, generator=g)
+    k = torch.randn(B, Hkv, S, hd, generator=g)
+    v = torch.randn(B, Hkv, S, hd, generator=g)
+    mask = None
+    if use_mask:
+        mask = (torch.rand(B, S, generator=g) > 0.3).long()
+        mask[:, 0] = 1
+    if use_mask and causal:
+        # the reference hands "True = masked" to SDPA (True = attend): visible
+        # keys are t > s or padded ones.
+        out = occ.attention(q, k, v, causal=True, mask=mask)
+        Bm = mask.clone()
+        ref = torch.zeros(B, Hq, S, hd, dtype=torch.float64)
+        for b in range(B):
+            for h in range(Hq):
+                for s in range(S):
+                    ts = [t for t in range(S) if t > s or Bm[b, t] == 0]
+                    if not ts:
+                        continue
+                    lg = torch.stack([(q[b, h, s].double() * k[b, h // 2, t].double()).sum() / math.sqrt(hd) for t in ts])
+                    p = torch.softmax(lg, 0)
+                    ref[b, h, s] = sum(p[i] * v[b, h // 2, t].double() for i, t in enumerate(ts))
+        assert max_rel_err(out, ref) < 1e-5
+        return
+    if use_mask:
+        pytest.skip("padding mask is only defined together with causality in the reference")
+    out = occ.attention(q, k, v, causal=causal)
+    ref = occ.attention_bruteforce(q, k, v, causal=causal)
+    assert max_rel_err(out, ref) < 1e-5
+
+
+def test_attention_gqa_equals_repeat_interleave():
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, 6, 10, 8, generator=g)
+    k = torch.randn(1, 2, 10, 8, generator=g)
+    v = torch.randn(1, 2, 10, 8, generator=g)
+    out = occ.attention(q, k, v, causal=True)
+    ref = F.scaled_dot_product_attention(q, k.repeat_interleave(3, 1), v.repeat_interleave(3, 1), is_causal=True)
+    assert torch.equal(out, ref)
+
+
+GOLDEN_CCGQA = sorted(GOLDEN.glob("ccgqa_*.npz"))
+
+
+def load_ccgqa_golden(path):
+    d = np.load(path)
+    meta = dict(eval(str(d["meta"])))  # written by make_golden.py as a repr of sorted items
+    B, S, msl = meta.pop("B"), meta.pop("S"), meta.pop("max_seq_len")
+    cfg = occ.CCGQAConfig(max_seq_len=msl, **meta)
+    params = {k[2:]: bf16_from_bits(d[k]) for k in d.files if k.startswith("w.")}
+    x = bf16_from_bits(d["x"])
+    mask = torch.from_numpy(d["mask"]).long() if "mask" in d.files else None
+    return cfg, params, x, mask, torch.from_numpy(d["out"])
+
+
+@pytest.mark.parametrize("path", GOLDEN_CCGQA, ids=[p.stem for p in GOLDEN_CCGQA])
+def test_ccgqa_forward_golden(path):
+    cfg, params, x, mask, out = load_ccgqa_golden(path)
+    got = occ.forward(params, x, cfg, mask=mask)
+    assert max_rel_err(got, out) < 1e-6
+
+
+def test_flop_figures_match_baseline():
+    """The algorithmic work the roofline is computed from (config 3)."""
+    cfg = occ.CCGQAConfig(dim=1024, n_heads=4, n_kv_heads=1, compression_factor=4)
+    f = occ.flops(cfg, 4, 4096)
+    assert f["core"] == 34_368_126_976
+    assert abs(f["total"] / 1e9 - 64.70) < 0.01
+
+
+# ---------------------------------------------------------------------- MoD
+def test_topk_bruteforce_ties_nan_signed_zero():
+    rows = np.array([
+        [1.0, 3.0, 3.0, -1.0, 3.0, 0.5],
+        [0.0, -0.0, 0.0, -0.0, 1.0, -1.0],
+        [np.nan, 2.0, np.nan, -np.inf, np.inf, 2.0],
+    ])
+    for k in range(1, 7):
+        assert np.array_equal(omod.topk_desc_lowest_index(rows, k), omod.topk_desc_bruteforce(rows, k))
+    assert omod.topk_desc_lowest_index(rows, 3)[0].tolist() == [1, 2, 4]
+    assert omod.topk_desc_lowest_index(rows, 4)[1].tolist() == [4, 0, 1, 2]
+    assert omod.topk_desc_lowest_index(rows, 4)[2].tolist() == [0, 2, 4, 1]
+
+
+def test_topk_value_sequence_matches_torch():
+    g = torch.Generator().manual_seed(8)
+    s = omod.make_tied_logits(4, 512, 0.05, g)
+    for k in (1, 100, 384, 512):
+        ours = omod.topk_desc_lowest_index(s.numpy(), k)
+        vals = torch.topk(s, k, dim=-1).values
+        assert torch.equal(torch.gather(s, 1, torch.from_numpy(ours)), vals)
+
+
+@pytest.mark.parametrize("cap", ["0750", "0500", "0125"])
+def test_mod_router_golden(cap):
+    d = np.load(GOLDEN / f"mod_router_cap{cap}.npz")
+    x, w, b = bf16_from_bits(d["x"]), bf16_from_bits(d["w"]), bf16_from_bits(d["b"])
+    scores = F.linear(x, w, b).squeeze(-1)
+    assert torch.equal(scores, torch.from_numpy(d["scores"]))
+    L = x.shape[1]
+    k = omod.router_k(L, float(d["capacity_ratio"]))
+    assert k == d["indices"].shape[1]
+    ours = omod.topk_desc_lowest_index(d["scores"], k)
+    assert np.array_equal(ours, d["stable_order"])
+    # torch.topk (what the reference calls) gives the same value sequence
+    assert np.array_equal(np.take_along_axis(d["scores"], ours, 1),
+                          np.take_along_axis(d["scores"], d["indices"], 1))
+    # the reference mask marks exactly torch.topk's set
+    assert np.array_equal(omod.mask_from_indices(d["indices"], L), d["mask"])
+
+
+def test_residual_scatter_invariants():
+    g = torch.Generator().manual_seed(9)
+    h = torch.randn(2, 10, 4, generator=g)
+    idx = torch.tensor([[7, 1, 3], [0, 9, 5]])
+    y = torch.randn(2, 3, 4, generator=g)
+    out = omod.residual_scatter(h, y, idx)
+    for b in range(2):
+        sel = set(idx[b].tolist())
+        for s in range(10):
+            if s in sel:
+                j = idx[b].tolist().index(s)
+                assert torch.equal(out[b, s], h[b, s] + y[b, j])
+            else:
+                assert torch.equal(out[b, s], h[b, s])
+    rep = omod.replace_scatter(h, y, idx)
+    assert torch.equal(rep[0, 7], y[0, 0]) and torch.equal(rep[0, 2], h[0, 2])
+    gth = omod.gather(h, idx)
+    assert torch.equal(gth[1, 1], h[1, 9])
