@@ -68,8 +68,9 @@ class C3Step:
 
         self.flags = prep_flags(True, True, True, True, True)
         mm = self.m
-        self.convw = (mm.q_conv.conv1.weight.detach(), mm.q_conv.conv2.weight.detach(),
-                      mm.k_conv.conv1.weight.detach(), mm.k_conv.conv2.weight.detach())
+        self.convw = mm._packed_conv_weights((mm.q_conv.conv1.weight, mm.q_conv.conv2.weight,
+                                              mm.k_conv.conv1.weight, mm.k_conv.conv2.weight),
+                                             torch.bfloat16)
         self.cos = mm.cos_cached[0, 0, :S].float().contiguous()
         self.sin = mm.sin_cached[0, 0, :S].float().contiguous()
         self.out = torch.empty(B, S, mm.latent_dim, dtype=torch.bfloat16, device=dev)
@@ -85,7 +86,8 @@ class C3Step:
         if ev:
             ev[1].record()
         q, k, v = ccgqa_prep(qkv, m.n_heads, m.n_kv_heads, m.head_dim, self.flags, *self.convw,
-                             temperature=m.key_temperature, cos=self.cos, sin=self.sin)
+                             temperature=m.key_temperature, cos=self.cos, sin=self.sin,
+                             packed=True)
         if ev:
             ev[2].record()
         o_view = self.out.view(self.B, self.S, m.n_heads, m.head_dim).transpose(1, 2)

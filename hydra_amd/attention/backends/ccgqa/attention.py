@@ -29,7 +29,7 @@ import torch.nn.functional as F
 from ...._autograd import track
 from ...._lib import MASK_KEY_PADDING, MASK_REFERENCE_SDPA
 from .kernels.fused_conv import OptimizedConvSequence
-from .ops import attention_forward, ccgqa_prep, prep_flags
+from .ops import attention_forward, ccgqa_prep, pack_conv_weight, prep_flags
 
 # Kept for callers that probe these names (attention.py:13-28).
 FUSED_KERNELS_AVAILABLE = True
@@ -113,24 +113,34 @@ class CCGQAAttention(nn.Module):
                            self.use_qk_norm, self.use_rope)
         convw = ((self.q_conv.conv1.weight, self.q_conv.conv2.weight,
                   self.k_conv.conv1.weight, self.k_conv.conv2.weight)
-                 if self.use_convs else (None, None, None, None))
+                 if self.use_convs else ())
         with torch.no_grad():
+            packed = self._packed_conv_weights(convw, x.dtype) if self.use_convs else (None,) * 4
             q, k, v = ccgqa_prep(
-                qkv.detach(), self.n_heads, self.n_kv_heads, self.head_dim, flags, *[
-                    None if w is None else w.detach() for w in convw],
-                temperature=self.key_temperature.detach() if self.use_qk_norm else None,
+                qkv.detach(), self.n_heads, self.n_kv_heads, self.head_dim, flags, *packed,
+                temperature=self.key_temperature if self.use_qk_norm else None,
                 cos=self.cos_cached if self.use_rope else None,
-                sin=self.sin_cached if self.use_rope else None)
+                sin=self.sin_cached if self.use_rope else None, packed=True)
             out = torch.empty((B, S, self.latent_dim), dtype=x.dtype, device=x.device)
             o_view = out.view(B, S, self.n_heads, self.head_dim).transpose(1, 2)
             attention_forward(q, k, v, causal=True, scale=self.scale,
                               key_mask=mask, mask_mode=_mask_mode() if mask is not None else 0,
                               out=o_view)
-        out = track(out, x, self.qkv_proj.weight, self.key_temperature, *[w for w in convw if w is not None])
+        out = track(out, x, self.qkv_proj.weight, self.key_temperature, *convw)
         out = F.linear(out, self.o_proj.weight)
         if self.output_scale != 1.0:
             out = out * self.output_scale
         return out
+
+    def _packed_conv_weights(self, convw, dtype):
+        """Tap-major copies of the four conv weights in `dtype`, rebuilt only
+        when a weight changes (tensor version counter) or moves."""
+        key = tuple((w.data_ptr(), w._version, w.device, dtype) for w in convw)
+        cache = getattr(self, "_packed_cache", None)
+        if cache is None or cache[0] != key:
+            cache = (key, tuple(pack_conv_weight(w, dtype) for w in convw))
+            self._packed_cache = cache
+        return cache[1]
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):

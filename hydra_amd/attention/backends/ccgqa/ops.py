@@ -20,10 +20,18 @@ def prep_flags(use_convs: bool, use_qk_mean: bool, use_value_shift: bool,
             | (CCGQA_QK_NORM if use_qk_norm else 0) | (CCGQA_ROPE if use_rope else 0))
 
 
+def pack_conv_weight(w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Conv1d weight [out, in/groups, k] -> the tap-major [k, out, in/groups]
+    layout the prep kernel reads."""
+    return w.detach().to(dtype).permute(2, 0, 1).contiguous()
+
+
 def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, flags: int,
-               wq1=None, wq2=None, wk1=None, wk2=None, temperature=None, cos=None, sin=None):
+               wq1=None, wq2=None, wk1=None, wk2=None, temperature=None, cos=None, sin=None,
+               packed: bool = False):
     """q [B,Hq,S,hd], k/v [B,Hkv,S,hd] from the fused projection qkv [B,S,L+2K]
-    (CCGQAAttention.forward, attention.py:205-266)."""
+    (CCGQAAttention.forward, attention.py:205-266).  Conv weights are in
+    PyTorch Conv1d layout, or already tap-major when packed=True."""
     _lib.require_gpu("ccgqa_prep", qkv, wq1, wq2, wk1, wk2, temperature, cos, sin)
     B, S, W = qkv.shape
     L, K = n_heads * head_dim, n_kv_heads * head_dim
@@ -32,11 +40,20 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
     if qkv.stride(-1) != 1 or (B > 1 and qkv.stride(0) != S * qkv.stride(1)):
         qkv = qkv.contiguous()
     dt = qkv.dtype
-
-    def _w(t):
-        return None if t is None else t.to(dt).contiguous()
-
-    wq1, wq2, wk1, wk2, temp = map(_w, (wq1, wq2, wk1, wk2, temperature))
+    if flags & CCGQA_CONVS:
+        ws = (wq1, wq2, wk1, wk2)
+        if packed:
+            ws = tuple(w.to(dt).contiguous() for w in ws)
+        else:
+            ws = tuple(pack_conv_weight(w, dt) for w in ws)
+        exp = [(3, L, head_dim), (3, L, L), (3, K, head_dim), (3, K, K)]
+        for w, e in zip(ws, exp):
+            if tuple(w.shape) != e:
+                raise ValueError(f"ccgqa_prep: packed conv weight shape {tuple(w.shape)} != {e}")
+        wq1, wq2, wk1, wk2 = ws
+    else:
+        wq1 = wq2 = wk1 = wk2 = None
+    temp = None if temperature is None else temperature.detach().to(dt).contiguous()
     if flags & CCGQA_ROPE:
         if cos.dim() == 4:
             cos, sin = cos[0, 0], sin[0, 0]
@@ -112,5 +129,5 @@ def conv_sequence(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, groups1: 
     return q.transpose(1, 2).reshape(B, N, C)
 
 
-__all__ = ["prep_flags", "ccgqa_prep", "attention_forward", "conv_sequence",
+__all__ = ["prep_flags", "pack_conv_weight", "ccgqa_prep", "attention_forward", "conv_sequence",
            "MASK_NONE", "MASK_KEY_PADDING", "MASK_REFERENCE_SDPA"]

@@ -15,12 +15,19 @@
 //    swap between the two half-waves.
 //  * O^T = V^T P^T: the bf16 P fragment is taken straight from the score
 //    accumulator registers; V is transposed while it is staged into LDS.
-//  * Causal: the grid runs the longest query blocks first, blocks above the
-//    diagonal are skipped, and only diagonal tiles evaluate the mask.
-//  * Softmax runs in the exp2 domain with fp32 statistics.
+//  * Softmax runs in the exp2 domain with fp32 statistics; the scale is
+//    folded into one FMA per score, and the running max (with the O
+//    rescale it implies) only moves when a tile's max exceeds it by 2^8.
+//  * K/V tiles are double-buffered in LDS: one barrier per key tile, the
+//    global loads of tile j+1 are in flight while tile j is computed.
+//  * Causal: the grid runs the longest query blocks first (with the second
+//    half of the grid in reverse, so co-resident workgroups balance), blocks
+//    above the diagonal are skipped, only diagonal tiles evaluate the mask.
 // Generic path (attn_fwd_generic_kernel): one thread per query row, fp32
 // math, any element type, even head_dim <= 256.
 #include "common.h"
+
+#include <type_traits>
 
 namespace hydra {
 
@@ -35,16 +42,12 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(from_f32<bf16>(lo).bits) |
-         (static_cast<uint32_t>(from_f32<bf16>(hi).bits) << 16);
-}
 
 template <int HD, bool CAUSAL, int MASK>
 __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
-    int S, int Hq, int Hkv, int G, int ntasks,
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg,
     int64_t qs0, int64_t qs1, int64_t qs2,
     int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2,
@@ -57,16 +60,28 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
   constexpr int DC = HD / 8;            // 16-byte chunks per K/V row
   constexpr int KCH = (BN * DC + 255) / 256;        // K chunks per thread
   constexpr int VCH = ((BN / 2) * DC + 255) / 256;  // V key-pair units per thread
+  constexpr int KBUF = BN * KROW, VBUF = DT * 32 * VROW;
+  // Lazy rescaling: the running max used for exp2 only moves when a score
+  // exceeds it by more than this (log2 units), so P stays <= 2^8.
+  constexpr float kRescale = 8.f;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[DT * 32 * VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * KBUF];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2 * VBUF];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, hf = lane >> 5;
-  const int bk = blockIdx.y;
+  // Causal balance: workgroups are ranked by work (longest first) and the
+  // second half of the grid takes the ranks in reverse, so the two
+  // workgroups that share a CU carry complementary amounts of work.
+  const int BH = gridDim.x / nwg;
+  const int total = gridDim.x;
+  const int half = (total + 1) / 2;
+  const int pos = blockIdx.x;
+  const int rank = pos < half ? pos : total - 1 - (pos - half);
+  const int wg = nwg - 1 - rank / BH;
+  const int bk = rank - (rank / BH) * BH;
   const int b = bk / Hkv, kvh = bk - b * Hkv;
-  const int wg = gridDim.x - 1 - blockIdx.x;  // longest query blocks first
   const int task = wg * 4 + wave;
   const bool active = task < ntasks;
   const int qb = task / G;
@@ -75,14 +90,17 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
   const int qi = q0 + n;
   const int last_task = min(wg * 4 + 3, ntasks - 1);
   const int wg_qmax = (last_task / G) * 32 + 31;
-  const int kend = CAUSAL ? min(S, wg_qmax + 1) : S;
+  const int kend = (CAUSAL && MASK != 2) ? min(S, wg_qmax + 1) : S;
   const int nkb = (kend + BN - 1) / BN;
 
   const bf16* kbase = k + b * ks0 + kvh * ks1;
   const bf16* vbase = v + b * vs0 + kvh * vs1;
 
-  if (DT * 32 > HD) {  // zero the padding rows of V^T once
-    for (int i = tid; i < (DT * 32 - HD) * VROW; i += 256) Vt[HD * VROW + i] = 0;
+  if (DT * 32 > HD) {  // zero the padding rows of both V^T buffers once
+    for (int i = tid; i < (DT * 32 - HD) * VROW; i += 256) {
+      Vt[HD * VROW + i] = 0;
+      Vt[VBUF + HD * VROW + i] = 0;
+    }
   }
 
   // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7].
@@ -96,6 +114,10 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
       qf[s] = as_bf16x8(raw);
     }
   }
+
+  // Retire the Q loads here: otherwise the in-order vmcnt makes the first
+  // MFMA of every iteration wait for the next tile's prefetch as well.
+  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
 
   uint4 kreg[KCH];
   uint4 vreg[VCH][2];
@@ -121,12 +143,14 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
       }
     }
   };
-  auto stage = [&]() {
+  auto stage = [&](int buf) {
+    uint16_t* kd = Ks + buf * KBUF;
+    uint16_t* vd = Vt + buf * VBUF;
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
       const int c = tid + 256 * j;
       const int key = c / DC, dc = c - key * DC;
-      if (c < BN * DC) *reinterpret_cast<uint4*>(&Ks[key * KROW + dc * 8]) = kreg[j];
+      if (c < BN * DC) *reinterpret_cast<uint4*>(&kd[key * KROW + dc * 8]) = kreg[j];
     }
 #pragma unroll
     for (int j = 0; j < VCH; ++j) {
@@ -138,10 +162,10 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
-          const uint32_t lo = (a[e] & 0xffffu) | (c2[e] << 16);
-          const uint32_t hi = (a[e] >> 16) | (c2[e] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(&Vt[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
-          *reinterpret_cast<uint32_t*>(&Vt[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
+          const uint32_t lo = __builtin_amdgcn_perm(c2[e], a[e], 0x05040100u);
+          const uint32_t hi = __builtin_amdgcn_perm(c2[e], a[e], 0x07060302u);
+          *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
+          *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
         }
       }
     }
@@ -154,85 +178,121 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  if (nkb > 0) fetch(0);
-  for (int kb = 0; kb < nkb; ++kb) {
-    stage();
-    __syncthreads();
-    if (kb + 1 < nkb) fetch((kb + 1) * BN);
+  // One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is
+  // compile-time, so the tiles that are fully visible to every wave of the
+  // workgroup run with no mask code at all.
+  auto tile = [&](int kb, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    const int buf = kb & 1;
     const int key0 = kb * BN;
-    const bool live = active && !(CAUSAL && key0 > q0 + 31);
-    if (live) {
-      f32x16_t st[2];
+    const uint16_t* kt = Ks + buf * KBUF;
+    const uint16_t* vt = Vt + buf * VBUF;
+    f32x16_t st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-          const uint4 a = *reinterpret_cast<const uint4*>(&Ks[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
-          st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
-        }
+        const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
       }
-      const bool need_mask = MASK != 0 || key0 + BN > S || (CAUSAL && key0 + BN - 1 > q0);
-      float mx = -INFINITY;
+    if constexpr (MASKED) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float x = st[mt][r] * scale_log2;
-          if (need_mask) {
-            const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
-            bool ok = key < S;
-            if (CAUSAL) ok = ok && key <= qi;
-            if (MASK != 0) {
-              const bool keep = kmask[static_cast<int64_t>(b) * S + min(key, S - 1)] != 0;
-              ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
-            }
-            x = ok ? x : -INFINITY;
+          const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
+          bool ok = key < S;
+          if (CAUSAL && MASK != 2) ok = ok && key <= qi;
+          if (MASK != 0) {
+            const bool keep = kmask[static_cast<int64_t>(b) * S + min(key, S - 1)] != 0;
+            ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
           }
-          st[mt][r] = x;
-          mx = fmaxf(mx, x);
+          st[mt][r] = ok ? st[mt][r] : -INFINITY;
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_i, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
-      float rs = 0.f;
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(st[mt][r] - m_use);
-          st[mt][r] = p;
-          rs += p;
-        }
-      rs += __shfl_xor(rs, 32);
-      l_i = l_i * alpha + rs;
-      m_i = m_new;
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;  // scaled row max of this tile
+    // Move the reference max only when this tile would push P past 2^8; the
+    // test is made wave-uniform so the common case is one skipped branch.
+    if (__any(mx > m_i + kRescale)) {
+      const bool move = mx > m_i + kRescale;
+      // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
+      // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
+      const float m_new = move ? mx : m_i;
+      l_i *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-      // O^T += V^T P^T over 4 k-steps of 16 keys.
+      m_i = m_new;
+    }
+    const float m_use = m_i == -INFINITY ? 0.f : m_i;
+    float rs = 0.f;
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int mt = s2 >> 1, rb = 8 * (s2 & 1);
-        uint4 praw;
-        praw.x = pack_bf16x2(st[mt][rb + 0], st[mt][rb + 1]);
-        praw.y = pack_bf16x2(st[mt][rb + 2], st[mt][rb + 3]);
-        praw.z = pack_bf16x2(st[mt][rb + 4], st[mt][rb + 5]);
-        praw.w = pack_bf16x2(st[mt][rb + 6], st[mt][rb + 7]);
-        const bf16x8_t pf = as_bf16x8(praw);
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const uint16_t* vr = &Vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
-          const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[mt][r], scale_log2, -m_use));
+        st[mt][r] = p;
+        rs += p;
+      }
+    l_i += rs + __shfl_xor(rs, 32);
+    // O^T += V^T P^T over 4 k-steps of 16 keys.
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int mt = s2 >> 1, rb = 8 * (s2 & 1);
+      uint4 praw;
+      praw.x = pack2<bf16>(st[mt][rb + 0], st[mt][rb + 1]);
+      praw.y = pack2<bf16>(st[mt][rb + 2], st[mt][rb + 3]);
+      praw.z = pack2<bf16>(st[mt][rb + 4], st[mt][rb + 5]);
+      praw.w = pack2<bf16>(st[mt][rb + 6], st[mt][rb + 7]);
+      const bf16x8_t pf = as_bf16x8(praw);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint16_t* vr = &vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+        const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
       }
     }
+  };
+
+  // Tiles [0, nfull) are in bounds and at or below the diagonal of every
+  // wave of the workgroup; the rest need the mask.
+  const int wg_qmin = ((wg * 4) / G) * 32;
+  int nfull = 0;
+  if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
+  nfull = min(nfull, nkb);
+
+  if (nkb > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+  int kb = 0;
+  for (; kb < nfull; ++kb) {
+    if (kb + 1 < nkb) fetch((kb + 1) * BN);
+    if (active) tile(kb, std::false_type());
+    // The next tile goes into the other buffer, which every wave finished
+    // reading before the barrier that ended the previous iteration.
+    if (kb + 1 < nkb) stage((kb & 1) ^ 1);
+    __syncthreads();
+  }
+  for (; kb < nkb; ++kb) {
+    if (kb + 1 < nkb) fetch((kb + 1) * BN);
+    const bool live = active && !(CAUSAL && MASK != 2 && kb * BN > q0 + 31);
+    if (live) tile(kb, std::true_type());
+    if (kb + 1 < nkb) stage((kb & 1) ^ 1);
     __syncthreads();
   }
 
@@ -246,8 +306,8 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
       const int d = 32 * dt + 8 * g4 + 4 * hf;
       if (d < HD) {
         uint2 w;
-        w.x = pack_bf16x2(acc[dt][4 * g4 + 0] * inv, acc[dt][4 * g4 + 1] * inv);
-        w.y = pack_bf16x2(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
+        w.x = pack2<bf16>(acc[dt][4 * g4 + 0] * inv, acc[dt][4 * g4 + 1] * inv);
+        w.y = pack2<bf16>(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
         *reinterpret_cast<uint2*>(orow + d) = w;
       }
     }
@@ -315,7 +375,8 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   const int G = static_cast<int>(Hq / Hkv);
   const int nqb = static_cast<int>((S + 31) / 32);
   const int ntasks = G * nqb;
-  const dim3 grid(static_cast<unsigned>((ntasks + 3) / 4), static_cast<unsigned>(B * Hkv));
+  const int nwg = (ntasks + 3) / 4;
+  const dim3 grid(static_cast<unsigned>(nwg * B * Hkv));
   const float sl2 = scale * kLog2e;
   auto Q = static_cast<const bf16*>(q);
   auto K = static_cast<const bf16*>(k);
@@ -323,7 +384,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   auto O = static_cast<bf16*>(o);
 #define HYDRA_ATTN_LAUNCH(C, M)                                                      \
   attn_fwd_mfma_kernel<HD, C, M><<<grid, 256, 0, st>>>(                              \
-      Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, qs[0], qs[1],   \
+      Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, nwg, qs[0], qs[1], \
       qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], sl2)
   // The reference-SDPA mask mode opens keys above the diagonal, so it walks
   // every key tile (no causal tile skipping).
@@ -386,7 +447,8 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   if (B * S == 0) return HYDRA_OK;
   HYDRA_REQUIRE(q && k && v && o, "attn_fwd: null pointer");
   HYDRA_REQUIRE(S < (int64_t(1) << 30), "attn_fwd: sequence too long");
-  HYDRA_REQUIRE(B * Hkv <= 65535, "attn_fwd: B*n_kv_heads must be <= 65535");
+  HYDRA_REQUIRE(B * Hkv * ((Hq / Hkv) * ((S + 31) / 32) + 3) / 4 < (int64_t(1) << 31),
+                "attn_fwd: too many workgroups");
   const uint8_t* km = mask_mode == HYDRA_MASK_NONE ? nullptr : key_mask;
   auto st = static_cast<hipStream_t>(stream);
   const bool mfma_shape = (hd == 16 || hd == 32 || hd == 64 || hd == 128);

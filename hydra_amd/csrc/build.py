@@ -29,6 +29,8 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     # keep the compiler from forming packed-fp32 VALU instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: no AGPR<->VGPR copies around the softmax
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -19,9 +19,17 @@
 // to that dtype at the same point, so the result tracks the reference's
 // rounding sequence and not just its mathematics.
 //
-// This is the generic (VALU, fp32 arithmetic) variant: any dtype, any even
-// head_dim.  Conv weights are read in PyTorch Conv1d layout [out, in/groups, 3].
+// Conv weights come tap-major, [3][out][in/groups] (PyTorch's Conv1d weight
+// [out, in/groups, 3] permuted (2, 0, 1)), so a row of input channels for one
+// (tap, output channel) is contiguous.
+//
+// Two variants: ccgqa_prep_mfma_kernel (bf16, head_dim in {32, 64, 128}) runs
+// both convs as v_mfma_f32_32x32x16_bf16 tiles over LDS-staged token rows;
+// ccgqa_prep_generic_kernel (VALU, fp32 arithmetic) takes every other case.
 #include "common.h"
+
+#include <cstdlib>
+#include <type_traits>
 
 namespace hydra {
 
@@ -70,10 +78,11 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
         const bool is_q = o < L;
         const int oo = is_q ? o : o - L;
         const int col0 = (is_q ? 0 : L) + (oo / hd) * hd;
-        const T* w = (is_q ? wq1 : wk1) + static_cast<int64_t>(oo) * hd * 3;
+        const int O = is_q ? L : K;
         for (int t = 0; t < 3; ++t) {
+          const T* w = (is_q ? wq1 : wk1) + (static_cast<int64_t>(t) * O + oo) * hd;
           const T* xr = xs + (r + t) * CW + col0;
-          for (int c = 0; c < hd; ++c) acc = fmaf(to_f32(w[c * 3 + t]), to_f32(xr[c]), acc);
+          for (int c = 0; c < hd; ++c) acc = fmaf(to_f32(w[c]), to_f32(xr[c]), acc);
         }
       }
       y1[i] = from_f32<T>(acc);  // conv2's causal padding is zeros: s < 0 -> 0
@@ -86,11 +95,11 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
       const int oo = is_q ? o : o - L;
       const int C = is_q ? L : K;
       const int col0 = is_q ? 0 : L;
-      const T* w = (is_q ? wq2 : wk2) + static_cast<int64_t>(oo) * C * 3;
       float acc = 0.f;
       for (int t = 0; t < 3; ++t) {
+        const T* w = (is_q ? wq2 : wk2) + (static_cast<int64_t>(t) * C + oo) * C;
         const T* yr = y1 + (r + t) * CW + col0;
-        for (int c = 0; c < C; ++c) acc = fmaf(to_f32(w[c * 3 + t]), to_f32(yr[c]), acc);
+        for (int c = 0; c < C; ++c) acc = fmaf(to_f32(w[c]), to_f32(yr[c]), acc);
       }
       y2[i] = from_f32<T>(acc);
     }
@@ -182,6 +191,322 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
   }
 }
 
+
+// ===========================================================================
+// bf16 MFMA variant.
+//
+// LDS (bf16, rows padded by 8 elements): X = qkv q|k columns of tokens
+// [s0-4, s0+TT), Y1 = conv1 output of tokens [s0-2, s0+TT), Y2 = conv2 output
+// of tokens [s0, s0+TT).  Both convs are computed transposed,
+//   Y^T[o, s] = sum_t sum_c W[t][o][c] * In[s + t - 2, c],
+// as 32(out channels) x 32(tokens) tiles: A = weights straight from global
+// (L2-resident, 16-byte loads along c), B = token rows from LDS (16 bytes
+// along c), so lane l owns token l%32 of the tile.  A task is one 32-channel
+// m-tile times all TT/32 token tiles, so each A fragment feeds TT/32 MFMAs.
+// The two halo rows of Y1 (tokens s0-2, s0-1) are computed on the VALU.
+// The epilogue (QK-mean, L2-norm, temperature, RoPE) uses HD/8 lanes per
+// (token, head) row and 16-byte vectors.
+// ===========================================================================
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_p;
+typedef __attribute__((ext_vector_type(16))) float f32x16_p;
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_p;
+
+__device__ __forceinline__ bf16x8_p ld_bf16x8(const void* p) {
+  return __builtin_bit_cast(bf16x8_p, *reinterpret_cast<const uint4*>(p));
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi on packed bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_p, a),
+                                         __builtin_bit_cast(bf16x2_p, b), acc, false);
+}
+
+// One MFMA conv task: the 32 output channels of the m-tile (weight rows
+// from wbase, lane row n, k half hf) times all NT token tiles, over 3 taps x
+// CS k-steps of 16 input channels.  A (weights) streams from L2, B (token
+// rows) from LDS at bbase + brow(j, t); row pointers are formed once per tap
+// and the channel loop only adds immediates.
+template <int NT, typename BRow>
+__device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int CS,
+                                          const uint16_t* bbase, BRow brow,
+                                          f32x16_p (&acc)[NT]) {
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const bf16* wt = wbase + t * wtap;
+    const uint16_t* bt[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) bt[j] = bbase + brow(j, t);
+#pragma unroll 8
+    for (int c = 0; c < CS; ++c) {
+      const bf16x8_p a = ld_bf16x8(wt + 16 * c);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const bf16x8_p bb = ld_bf16x8(bt[j] + 16 * c);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bb, acc[j], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// 8 waves: two per SIMD, so one wave's VALU work and L2 latency overlap
+// another's MFMAs.
+constexpr int kPrepThreads = 512;
+
+template <int HD, int TT>
+__global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
+    const bf16* __restrict__ qkv, int64_t qkv_rs, const bf16* __restrict__ wq1,
+    const bf16* __restrict__ wq2, const bf16* __restrict__ wk1, const bf16* __restrict__ wk2,
+    const bf16* __restrict__ temp, const float* __restrict__ cs, const float* __restrict__ sn,
+    int64_t cs_rs, bf16* __restrict__ qo, bf16* __restrict__ ko, bf16* __restrict__ vo, int S,
+    int Hq, int Hkv, int flags) {
+  constexpr int NT = TT / 32;  // token tiles
+  constexpr int LPR = HD / 8;  // epilogue lanes per (token, head) row
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  uint16_t* sm = reinterpret_cast<uint16_t*>(smem_raw);
+  const int L = Hq * HD, K = Hkv * HD, CW = L + K, RS = CW + 8;
+  uint16_t* X = sm;                   // row r <-> token s0 - 4 + r
+  uint16_t* Y1 = X + (TT + 4) * RS;   // row r <-> token s0 - 2 + r
+  uint16_t* Y2 = Y1 + (TT + 2) * RS;  // row r <-> token s0 + r
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = lane & 31, hf = lane >> 5;
+  const int b = blockIdx.y;
+  const int s0 = blockIdx.x * TT;
+  const bool convs = flags & HYDRA_CCGQA_CONVS;
+  const bool qk_mean = flags & HYDRA_CCGQA_QK_MEAN;
+  const bool vshift = flags & HYDRA_CCGQA_VALUE_SHIFT;
+  const bool qk_norm = flags & HYDRA_CCGQA_QK_NORM;
+  const bool rope = flags & HYDRA_CCGQA_ROPE;
+  const bf16* xb = qkv + static_cast<int64_t>(b) * S * qkv_rs;
+
+  // ---- stage q0|k0 rows --------------------------------------------------
+  const int cw8 = CW / 8;
+  for (int i = tid; i < (TT + 4) * cw8; i += kPrepThreads) {
+    const int r = i / cw8, c = (i - r * cw8) * 8;
+    const int s = s0 - 4 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (s >= 0 && s < S) v = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + c);
+    *reinterpret_cast<uint4*>(X + r * RS + c) = v;
+  }
+  __syncthreads();
+
+  if (convs) {
+    // ---- conv1 halo rows (tokens s0-2, s0-1) on the VALU -------------------
+    for (int i = tid; i < 2 * CW; i += kPrepThreads) {
+      const int r = i / CW, o = i - r * CW;
+      const int s = s0 - 2 + r;
+      float acc = 0.f;
+      if (s >= 0) {
+        const bool is_q = o < L;
+        const int oo = is_q ? o : o - L;
+        const int O = is_q ? L : K;
+        const int col0 = (is_q ? 0 : L) + (oo / HD) * HD;
+        const bf16* w1 = is_q ? wq1 : wk1;
+        for (int t = 0; t < 3; ++t) {
+          const bf16* wr = w1 + (static_cast<int64_t>(t) * O + oo) * HD;
+          const uint16_t* xr = X + (r + t) * RS + col0;
+#pragma unroll 4
+          for (int c = 0; c < HD; c += 8) {
+            const uint4 wv = *reinterpret_cast<const uint4*>(wr + c);
+            const uint4 xv = *reinterpret_cast<const uint4*>(xr + c);
+            acc = dot2_bf16(wv.x, xv.x, acc);
+            acc = dot2_bf16(wv.y, xv.y, acc);
+            acc = dot2_bf16(wv.z, xv.z, acc);
+            acc = dot2_bf16(wv.w, xv.w, acc);
+          }
+        }
+      }
+      Y1[r * RS + o] = from_f32<bf16>(acc).bits;
+    }
+    // ---- conv1 main rows on MFMA ---------------------------------------------
+    for (int mt = wave; mt < CW / 32; mt += kPrepThreads / 64) {
+      const int o0 = 32 * mt;
+      const bool is_q = o0 < L;
+      const int oo0 = is_q ? o0 : o0 - L;
+      const int O = is_q ? L : K;
+      const int cbase = (is_q ? 0 : L) + (oo0 / HD) * HD;
+      const bf16* wbase = (is_q ? wq1 : wk1) + static_cast<int64_t>(oo0 + n) * HD + 8 * hf;
+      f32x16_p acc[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+      // output token s0+32j+n, tap t reads token s0+32j+n+t-2 = X row 32j+n+2+t
+      conv_task<NT>(wbase, static_cast<int64_t>(O) * HD, HD / 16, X + cbase + 8 * hf,
+                       [&](int j, int t) { return (32 * j + n + 2 + t) * RS; }, acc);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          uint2 w;
+          w.x = pack2<bf16>(acc[j][4 * g4 + 0], acc[j][4 * g4 + 1]);
+          w.y = pack2<bf16>(acc[j][4 * g4 + 2], acc[j][4 * g4 + 3]);
+          *reinterpret_cast<uint2*>(Y1 + (2 + 32 * j + n) * RS + o0 + 8 * g4 + 4 * hf) = w;
+        }
+    }
+    __syncthreads();
+    // ---- conv2 on MFMA -------------------------------------------------------
+    for (int mt = wave; mt < CW / 32; mt += kPrepThreads / 64) {
+      const int o0 = 32 * mt;
+      const bool is_q = o0 < L;
+      const int oo0 = is_q ? o0 : o0 - L;
+      const int C = is_q ? L : K;
+      const int cbase = is_q ? 0 : L;
+      const bf16* wbase = (is_q ? wq2 : wk2) + static_cast<int64_t>(oo0 + n) * C + 8 * hf;
+      f32x16_p acc[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+      // output token s0+32j+n, tap t reads token s0+32j+n+t-2 = Y1 row 32j+n+t
+      conv_task<NT>(wbase, static_cast<int64_t>(C) * C, C / 16, Y1 + cbase + 8 * hf,
+                       [&](int j, int t) { return (32 * j + n + t) * RS; }, acc);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          uint2 w;
+          w.x = pack2<bf16>(acc[j][4 * g4 + 0], acc[j][4 * g4 + 1]);
+          w.y = pack2<bf16>(acc[j][4 * g4 + 2], acc[j][4 * g4 + 3]);
+          *reinterpret_cast<uint2*>(Y2 + (32 * j + n) * RS + o0 + 8 * g4 + 4 * hf) = w;
+        }
+    }
+  } else {
+    for (int i = tid; i < TT * cw8; i += kPrepThreads) {
+      const int r = i / cw8, c = (i - r * cw8) * 8;
+      *reinterpret_cast<uint4*>(Y2 + r * RS + c) = *reinterpret_cast<const uint4*>(X + (r + 4) * RS + c);
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue: QK-mean, L2-norm (+temperature), RoPE, store -------------
+  // The reference divides by the (bf16) norm; here that is one fp32 division
+  // per row and a multiply per element, then the same bf16 roundings.
+  const int G = Hq / Hkv;
+  const float tval = (qk_norm && temp) ? to_f32(temp[0]) : 1.f;
+  const float inv_hq = 1.f / static_cast<float>(Hq), inv_hkv = 1.f / static_cast<float>(Hkv);
+  const int nheads = Hq + Hkv;
+  const int rows = TT * nheads;
+  for (int base = 0; base < rows * LPR; base += kPrepThreads) {
+    const int i = base + tid;
+    const bool live = i < rows * LPR;
+    const int row = i / LPR, c8 = (i % LPR) * 8;
+    const int r = row / nheads, hh = row - r * nheads;
+    const int s = s0 + r;
+    const bool is_k = hh >= Hq;
+    const int head = is_k ? hh - Hq : hh;
+    const int col0 = (is_k ? L : 0) + head * HD;
+    float v[8];
+    float ss = 0.f;
+    if (live) {
+      load16<bf16>(reinterpret_cast<const bf16*>(Y2 + r * RS + col0 + c8), v);
+      if (qk_mean) {
+        const bf16* x0 = reinterpret_cast<const bf16*>(X + (r + 4) * RS);
+        float add[8];
+        if (G == 1) {
+          float a[8], c[8];
+          load16<bf16>(x0 + head * HD + c8, a);
+          load16<bf16>(x0 + L + head * HD + c8, c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(a[e] + c[e]));
+        } else {
+          // k heads take the mean of the q heads, q heads the mean of the k heads
+          const int nh = is_k ? Hq : Hkv;
+          const bf16* src = x0 + (is_k ? 0 : L) + c8;
+          float acc[8];
+          load16<bf16>(src, acc);
+          for (int hx = 1; hx < nh; ++hx) {
+            float a[8];
+            load16<bf16>(src + hx * HD, a);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += a[e];
+          }
+          const float inv = is_k ? inv_hq : inv_hkv;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(acc[e] * inv));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = rnd<bf16>(v[e] + add[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+    ss = wave_sum<LPR>(ss);
+    if (!live || s >= S) continue;
+    if (qk_norm) {
+      const float rinv = 1.f / fmaxf(rnd<bf16>(__builtin_sqrtf(ss)), 1e-12f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = rnd<bf16>(v[e] * rinv);
+        if (is_k) v[e] = rnd<bf16>(v[e] * tval);
+      }
+    }
+    if (rope) {
+      const float4 cv = *reinterpret_cast<const float4*>(cs + static_cast<int64_t>(s) * cs_rs + c8 / 2);
+      const float4 sv = *reinterpret_cast<const float4*>(sn + static_cast<int64_t>(s) * cs_rs + c8 / 2);
+      const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
+      const float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float x1 = v[2 * p], x2 = v[2 * p + 1];
+        v[2 * p] = x1 * cc[p] - x2 * sc[p];
+        v[2 * p + 1] = x1 * sc[p] + x2 * cc[p];
+      }
+    }
+    bf16* dst = (is_k ? ko : qo) +
+                ((static_cast<int64_t>(b) * (is_k ? Hkv : Hq) + head) * S + s) * HD + c8;
+    store16<bf16>(dst, v);
+  }
+
+  // ---- v (value shift), 16-byte copies -------------------------------------
+  const int k8 = K / 8;
+  for (int i = tid; i < TT * k8; i += kPrepThreads) {
+    const int r = i / k8, c = (i - r * k8) * 8;
+    const int s = s0 + r;
+    if (s >= S) continue;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (vshift && c >= K / 2) {
+      if (s > 0) val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s - 1) * qkv_rs + L + K + c);
+    } else {
+      val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + c);
+    }
+    const int j = c / HD, d = c - j * HD;
+    *reinterpret_cast<uint4*>(vo + ((static_cast<int64_t>(b) * Hkv + j) * S + s) * HD + d) = val;
+  }
+}
+
+template <int HD>
+static int launch_prep_mfma(const void* qkv, int64_t qkv_rs, const void* wq1, const void* wq2,
+                            const void* wk1, const void* wk2, const void* temp, const float* cs,
+                            const float* sn, int64_t cs_rs, void* qo, void* ko, void* vo,
+                            int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int flags,
+                            size_t max_lds, hipStream_t st) {
+  const int64_t RS = (Hq + Hkv) * HD + 8;
+  auto lds_for = [&](int TT) { return static_cast<size_t>(3 * TT + 6) * RS * 2; };
+  auto go = [&](auto tt_tag) -> int {
+    constexpr int TT = decltype(tt_tag)::value;
+    const size_t lds = lds_for(TT);
+    auto kern = ccgqa_prep_mfma_kernel<HD, TT>;
+    hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    const dim3 grid(static_cast<unsigned>((S + TT - 1) / TT), static_cast<unsigned>(B));
+    kern<<<grid, kPrepThreads, lds, st>>>(
+        static_cast<const bf16*>(qkv), qkv_rs, static_cast<const bf16*>(wq1),
+        static_cast<const bf16*>(wq2), static_cast<const bf16*>(wk1),
+        static_cast<const bf16*>(wk2), static_cast<const bf16*>(temp), cs, sn, cs_rs,
+        static_cast<bf16*>(qo), static_cast<bf16*>(ko), static_cast<bf16*>(vo), (int)S,
+        (int)Hq, (int)Hkv, flags);
+    return check_launch("ccgqa_prep_mfma_kernel");
+  };
+  // 64-token tiles halve the weight traffic per MFMA; use them when they still
+  // give at least one workgroup per CU (256), else 32-token tiles.
+  int tt = B * ((S + 63) / 64) >= 256 ? 64 : 32;
+  if (const char* e = getenv("HYDRA_PREP_TT")) tt = atoi(e) == 32 ? 32 : 64;
+  if (tt == 64 && lds_for(64) <= max_lds) return go(std::integral_constant<int, 64>());
+  if (lds_for(32) <= max_lds) return go(std::integral_constant<int, 32>());
+  return -1;  // does not fit: caller falls back to the generic kernel
+}
+
 template <typename T>
 static int launch_prep_generic(const void* qkv, int64_t qkv_rs, const void* wq1,
                                const void* wq2, const void* wk1, const void* wk2,
@@ -232,6 +557,26 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
   HYDRA_REQUIRE(B <= 65535, "ccgqa_prep: batch must be <= 65535");
   HYDRA_REQUIRE(S * (L + 2 * K) < (int64_t(1) << 40), "ccgqa_prep: too large");
   auto st = static_cast<hipStream_t>(stream);
+  const bool rope = flags & HYDRA_CCGQA_ROPE;
+  const bool mfma_ok =
+      dtype == HYDRA_BF16 && (hd == 32 || hd == 64 || hd == 128) && K % 32 == 0 &&
+      qkv_rs % 8 == 0 && aligned16(qkv) && aligned16(q_out) && aligned16(k_out) &&
+      aligned16(v_out) &&
+      (!(flags & HYDRA_CCGQA_CONVS) || (aligned16(wq1) && aligned16(wq2) && aligned16(wk1) &&
+                                        aligned16(wk2))) &&
+      (!rope || (cs_rs % 4 == 0 && aligned16(cos) && aligned16(sin)));
+  if (mfma_ok) {
+    int dev = 0, max_lds = 65536;
+    if (hipGetDevice(&dev) == hipSuccess)
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    int rc = -1;
+    switch (hd) {
+      case 32: rc = launch_prep_mfma<32>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
+      case 64: rc = launch_prep_mfma<64>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
+      default: rc = launch_prep_mfma<128>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
+    }
+    if (rc >= 0) return rc;
+  }
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     return launch_prep_generic<T>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs,
                                   q_out, k_out, v_out, B, S, Hq, Hkv, hd, flags, st);

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
+#include <type_traits>
 
 #include "../../include/hydra_amd.h"
 
@@ -27,20 +28,30 @@ __device__ __forceinline__ float to_f32(f16 v) {
 template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
-  uint32_t u = __float_as_uint(v);
+  // gfx950 converts in hardware (v_cvt_pk_bf16_f32): round to nearest even,
+  // NaN stays NaN.
   bf16 r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN: keep it quiet
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
   return r;
 }
 template <> __device__ __forceinline__ f16 from_f32<f16>(float v) {
   f16 r;
   r.bits = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
   return r;
+}
+
+// Two values rounded to a 16-bit type, packed low | high << 16 (one
+// v_cvt_pk_bf16_f32 for bf16).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (sizeof(T) == 2 && std::is_same<T, bf16>::value) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    return static_cast<uint32_t>(from_f32<T>(lo).bits) |
+           (static_cast<uint32_t>(from_f32<T>(hi).bits) << 16);
+  }
 }
 
 // Elements of T in one 16-byte vector.
@@ -75,10 +86,7 @@ __device__ __forceinline__ void store16(T* p, const float* in) {
   } else {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      w[i] = static_cast<uint32_t>(from_f32<T>(in[2 * i]).bits) |
-             (static_cast<uint32_t>(from_f32<T>(in[2 * i + 1]).bits) << 16);
-    }
+    for (int i = 0; i < 4; ++i) w[i] = pack2<T>(in[2 * i], in[2 * i + 1]);
     raw.x = w[0]; raw.y = w[1]; raw.z = w[2]; raw.w = w[3];
   }
   *reinterpret_cast<uint4*>(p) = raw;

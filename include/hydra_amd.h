@@ -100,12 +100,16 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
  *
  * qkv:  [B, S, L + 2K] (row stride qkv_rs), L = Hq*hd, K = Hkv*hd; column
  *       order q | k | v_curr | v_prev (v: | v when no value shift).
- * wq1:  conv1 of q, PyTorch Conv1d layout [L, hd, 3]; wq2: [L, L, 3];
- * wk1:  [K, hd, 3];                                    wk2: [K, K, 3];
+ * wq1/wq2/wk1/wk2: the four Conv1d weights (q_conv.conv1/conv2,
+ *       k_conv.conv1/conv2) in tap-major layout [3][out][in/groups], i.e.
+ *       PyTorch's [out, in/groups, 3] permuted (2, 0, 1):
+ *       wq1 [3][L][hd], wq2 [3][L][L], wk1 [3][K][hd], wk2 [3][K][K]
  *       (unused and may be NULL without HYDRA_CCGQA_CONVS).
  * temp: key temperature, 1 element of `dtype` (NULL without QK_NORM).
  * cos/sin: fp32 [S, hd/2] row stride cs_rs (NULL without ROPE).
- * q_out: [B, Hq, S, hd]; k_out, v_out: [B, Hkv, S, hd]; all contiguous. */
+ * q_out: [B, Hq, S, hd]; k_out, v_out: [B, Hkv, S, hd]; all contiguous.
+ * bf16 with hd in {32, 64, 128} runs both convs on MFMA (up to ~100 KB of LDS
+ * per workgroup at L+K = 320); other cases run on the VALU. */
 int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
                          const void* wq1, const void* wq2,
                          const void* wk1, const void* wk2,

@@ -18,15 +18,19 @@ def router_k(seq_len: int, capacity_ratio: float) -> int:
 
 
 def topk_desc_lowest_index(scores: np.ndarray, k: int) -> np.ndarray:
-    """Top-k per row in torch.topk's value order (NaN largest, -0.0 == +0.0),
-    ties by ascending index: a stable sort on the negated order key.
+    """Top-k per row in torch.topk's value order (NaN above +inf, -0.0 ==
+    +0.0), ties by ascending index: a stable two-key sort (NaN flag first,
+    then the negated value).
 
     torch.topk (mixture_of_depths.py:187) fixes the value sequence; the tie
     rule (lowest index first) is the one the MoD path is specified with."""
     s = np.asarray(scores, dtype=np.float64)
-    key = np.where(np.isnan(s), -np.inf, -s)  # NaN first, then descending
-    key = np.where(key == 0.0, 0.0, key)      # fold -0.0 into +0.0
-    return np.argsort(key, axis=-1, kind="stable")[:, :k].astype(np.int64)
+    nan = np.isnan(s)
+    neg = np.where(nan, 0.0, -s)
+    neg = np.where(neg == 0.0, 0.0, neg)  # fold -0.0 into +0.0
+    # np.lexsort is stable; the last key is the primary one.
+    order = np.lexsort((neg, ~nan), axis=-1)
+    return order[:, :k].astype(np.int64)
 
 
 def topk_desc_bruteforce(scores, k: int):

@@ -300,12 +300,17 @@ def test_topk_bruteforce_ties_nan_signed_zero():
         [1.0, 3.0, 3.0, -1.0, 3.0, 0.5],
         [0.0, -0.0, 0.0, -0.0, 1.0, -1.0],
         [np.nan, 2.0, np.nan, -np.inf, np.inf, 2.0],
+        [np.inf, 2.0, np.nan, -np.inf, np.inf, np.nan],
     ])
     for k in range(1, 7):
         assert np.array_equal(omod.topk_desc_lowest_index(rows, k), omod.topk_desc_bruteforce(rows, k))
     assert omod.topk_desc_lowest_index(rows, 3)[0].tolist() == [1, 2, 4]
     assert omod.topk_desc_lowest_index(rows, 4)[1].tolist() == [4, 0, 1, 2]
     assert omod.topk_desc_lowest_index(rows, 4)[2].tolist() == [0, 2, 4, 1]
+    # NaN ranks above +inf whatever the positions (torch.topk's order)
+    assert omod.topk_desc_lowest_index(rows, 4)[3].tolist() == [2, 5, 0, 4]
+    t = torch.topk(torch.from_numpy(rows[3]), 4).values
+    assert np.isnan(t[0].item()) and np.isnan(t[1].item()) and t[2].item() == np.inf
 
 
 def test_topk_value_sequence_matches_torch():
