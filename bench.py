@@ -66,7 +66,9 @@ class C3Step:
         self.x = x.to(dev, torch.bfloat16)
         from hydra_amd.attention.backends.ccgqa.ops import prep_flags
 
-        self.flags = prep_flags(True, True, True, True, True)
+        from hydra_amd._lib import CCGQA_V_TRANSPOSED
+
+        self.flags = prep_flags(True, True, True, True, True) | CCGQA_V_TRANSPOSED
         mm = self.m
         self.convw = mm._packed_conv_weights((mm.q_conv.conv1.weight, mm.q_conv.conv2.weight,
                                               mm.k_conv.conv1.weight, mm.k_conv.conv2.weight),
@@ -129,16 +131,35 @@ def bench_c3(dev, steps, warmup):
 
 # ----------------------------------------------------------------- config 2
 def _time_rotating(fn, sets, iters, warmup=3):
-    for i in range(warmup):
-        fn(*sets[i % len(sets)])
+    """Average GPU time per call of fn over rotating argument sets.
+
+    The calls are captured once into a HIP graph (torch.cuda.graph) and the
+    graph is replayed, so the figure is kernel time on the GPU timeline and
+    not the Python/ctypes launch cost, which exceeds a ~10 us kernel."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(warmup):
+            fn(*sets[i % len(sets)])
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    n_per = max(len(sets), 8)
+    with torch.cuda.graph(graph):
+        for i in range(n_per):
+            fn(*sets[i % len(sets)])
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, iters // n_per)
     a, b = _events(2)
     a.record()
-    for i in range(iters):
-        fn(*sets[i % len(sets)])
+    for _ in range(reps):
+        graph.replay()
     b.record()
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / iters
+    ms = a.elapsed_time(b) / (reps * n_per)
+    del graph
+    return ms
 
 
 def bench_fused_ops(dev, iters=60):
@@ -241,6 +262,30 @@ def cpu_baseline(budget_s=12.0):
                       f"torch {torch.__version__}"}
 
 
+def calibrate_copy(mib=512, reps=3):
+    """A plain device copy of known size: under rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE, its counters give the scale between the counter readings and
+    real HBM bytes (expected reading: mib*1024 KiB each way)."""
+    a = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_each_way": mib << 20, "reps": reps}))
+
+
+def measured_traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed PMC summary
+    (profiles/traffic.json, written from rocprofv3 FETCH_SIZE + WRITE_SIZE
+    passes scaled by the copy calibration); None when absent."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(path.read_text())["kernels"][kernel_key]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +293,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the fused-op and MoD sections")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 512 MiB device copy (traffic-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the hot path has no multi-GPU "
@@ -256,6 +303,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU", file=sys.stderr)
         sys.exit(1)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     from hydra_amd import _lib
 
     _lib.load()
@@ -282,7 +332,8 @@ def main():
                    "global_batch": step.B, "seq_len": step.S, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "attn_fwd_mfma_kernel<64,causal>", "bound": "mfma",
                      "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                     "frac": achieved / BF16_PEAK_TFLOPS,
+                     "traffic": measured_traffic("attn_fwd_mfma_kernel<64,true,0>"),
                      "flops_per_launch": fl["core"], "avg_ms": attn_ms},
         "stages_ms": stages,
         "module_tflops": fl["total"] / (ms_step * 1e-3) / 1e12,

@@ -21,6 +21,7 @@ LIB_PATH = Path(os.environ.get("HYDRA_AMD_LIB", Path(__file__).with_name("libhyd
 OK, ERR_ARG, ERR_LAUNCH, ERR_UNSUPPORTED = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
 CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_VALUE_SHIFT, CCGQA_QK_NORM, CCGQA_ROPE = 1, 2, 4, 8, 16
+CCGQA_V_TRANSPOSED = 32
 MASK_NONE, MASK_KEY_PADDING, MASK_REFERENCE_SDPA = 0, 1, 2
 SCATTER_ADD, SCATTER_REPLACE = 0, 1
 

@@ -27,7 +27,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ...._autograd import track
-from ...._lib import MASK_KEY_PADDING, MASK_REFERENCE_SDPA
+from ...._lib import CCGQA_V_TRANSPOSED, MASK_KEY_PADDING, MASK_REFERENCE_SDPA
 from .kernels.fused_conv import OptimizedConvSequence
 from .ops import attention_forward, ccgqa_prep, pack_conv_weight, prep_flags
 
@@ -111,6 +111,8 @@ class CCGQAAttention(nn.Module):
         qkv = F.linear(x, self.qkv_proj.weight)
         flags = prep_flags(self.use_convs, self.use_qk_mean, self.use_value_shift,
                            self.use_qk_norm, self.use_rope)
+        if x.dtype == torch.bfloat16 and S % 8 == 0 and self.head_dim in (16, 32, 64, 128):
+            flags |= CCGQA_V_TRANSPOSED  # V^T feeds the MFMA attention without a transpose
         convw = ((self.q_conv.conv1.weight, self.q_conv.conv2.weight,
                   self.k_conv.conv1.weight, self.k_conv.conv2.weight)
                  if self.use_convs else ())

@@ -8,7 +8,7 @@ from typing import Optional
 import torch
 
 from ...._lib import (CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_QK_NORM, CCGQA_ROPE,
-                      CCGQA_VALUE_SHIFT, MASK_KEY_PADDING, MASK_NONE,
+                      CCGQA_V_TRANSPOSED, CCGQA_VALUE_SHIFT, MASK_KEY_PADDING, MASK_NONE,
                       MASK_REFERENCE_SDPA)
 from .... import _lib
 
@@ -31,7 +31,9 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
                packed: bool = False):
     """q [B,Hq,S,hd], k/v [B,Hkv,S,hd] from the fused projection qkv [B,S,L+2K]
     (CCGQAAttention.forward, attention.py:205-266).  Conv weights are in
-    PyTorch Conv1d layout, or already tap-major when packed=True."""
+    PyTorch Conv1d layout, or already tap-major when packed=True.  With
+    CCGQA_V_TRANSPOSED in flags, v is returned as a [B,Hkv,S,hd] view of a
+    [B,Hkv,hd,S] buffer (the layout the attention kernel stages directly)."""
     _lib.require_gpu("ccgqa_prep", qkv, wq1, wq2, wk1, wk2, temperature, cos, sin)
     B, S, W = qkv.shape
     L, K = n_heads * head_dim, n_kv_heads * head_dim
@@ -63,14 +65,16 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
         sin = sin[:S].float().contiguous()
     q = torch.empty((B, n_heads, S, head_dim), dtype=dt, device=qkv.device)
     k = torch.empty((B, n_kv_heads, S, head_dim), dtype=dt, device=qkv.device)
-    v = torch.empty((B, n_kv_heads, S, head_dim), dtype=dt, device=qkv.device)
+    vt = bool(flags & CCGQA_V_TRANSPOSED)
+    v = torch.empty((B, n_kv_heads, head_dim, S) if vt else (B, n_kv_heads, S, head_dim),
+                    dtype=dt, device=qkv.device)
     with torch.cuda.device(qkv.device):
         _lib.call("hydra_ccgqa_prep_fwd", qkv.data_ptr(), qkv.stride(1), _lib.ptr(wq1),
                   _lib.ptr(wq2), _lib.ptr(wk1), _lib.ptr(wk2), _lib.ptr(temp), _lib.ptr(cos),
                   _lib.ptr(sin), head_dim // 2 if cos is None else cos.stride(0),
                   q.data_ptr(), k.data_ptr(), v.data_ptr(), B, S, n_heads, n_kv_heads,
                   head_dim, flags, _lib.dtype_code(qkv), _lib.stream(qkv))
-    return q, k, v
+    return q, k, (v.transpose(2, 3) if vt else v)
 
 
 def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool,
@@ -90,7 +94,9 @@ def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
         raise ValueError("attention_forward: n_heads must be a multiple of n_kv_heads")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("attention_forward: q, k, v must share a dtype")
-    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    q, k = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k))
+    if v.stride(-1) != 1 and v.stride(-2) != 1:
+        v = v.contiguous()
     if out is None:
         out = torch.empty((B, Hq, S, hd), dtype=q.dtype, device=q.device)
     elif out.shape != q.shape or out.stride(-1) != 1:

@@ -7,9 +7,11 @@
 // 341-429).
 //
 // bf16 path (attn_fwd_mfma_kernel): v_mfma_f32_32x32x16_bf16.
-//  * A workgroup is 4 waves that share one (batch, kv-head) and one staged
-//    K/V tile in LDS; wave w takes task 4*wg+w, task t -> (32-row query block
-//    t/G, query head kvh*G + t%G), so GQA heads reuse the same K/V tile.
+//  * A workgroup is NW waves (4, or 2 when that is needed to give the
+//    dispatcher enough workgroups to balance the causal triangle) that share
+//    one (batch, kv-head) and one staged K/V tile in LDS; wave w takes task
+//    NW*wg+w, task t -> (32-row query block t/G, query head kvh*G + t%G), so
+//    GQA heads reuse the same K/V tile.
 //  * Scores are computed transposed, S^T = K Q^T, so lane l owns query
 //    (l%32) and the online softmax needs no cross-lane traffic except one
 //    swap between the two half-waves.
@@ -27,6 +29,7 @@
 // math, any element type, even head_dim <= 256.
 #include "common.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace hydra {
@@ -42,9 +45,18 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+constexpr uint32_t kOnesBf16x2 = 0x3f803f80u;  // (1.0, 1.0) in bf16
 
-template <int HD, bool CAUSAL, int MASK>
-__global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
+// acc + a.lo*b.lo + a.hi*b.hi on packed bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+
+template <int HD, bool CAUSAL, int MASK, bool VT, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
     int S, int Hq, int Hkv, int G, int ntasks, int nwg,
@@ -52,14 +64,18 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
     int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2,
     int64_t os0, int64_t os1, int64_t os2, float scale_log2) {
+  // VT: V is stored transposed ([.., hd, S], keys contiguous, row stride
+  // vs2 between d rows) and is staged with plain 16-byte copies; otherwise
+  // V is [.., S, hd] and is transposed while staged.
   constexpr int BN = 64;                // keys per tile
   constexpr int KSTEPS = HD / 16;       // k-steps of S^T = K Q^T
   constexpr int DT = (HD + 31) / 32;    // 32-row d tiles of O^T
   constexpr int KROW = HD + 8;          // padded LDS row of K (elements)
   constexpr int VROW = BN + 4;          // padded LDS row of V^T (elements)
   constexpr int DC = HD / 8;            // 16-byte chunks per K/V row
-  constexpr int KCH = (BN * DC + 255) / 256;        // K chunks per thread
-  constexpr int VCH = ((BN / 2) * DC + 255) / 256;  // V key-pair units per thread
+  constexpr int NT = 64 * NW;                       // threads per workgroup
+  constexpr int KCH = (BN * DC + NT - 1) / NT;      // K chunks per thread
+  constexpr int VCH = ((BN / 2) * DC + NT - 1) / NT;  // V key-pair units per thread
   constexpr int KBUF = BN * KROW, VBUF = DT * 32 * VROW;
   // Lazy rescaling: the running max used for exp2 only moves when a score
   // exceeds it by more than this (log2 units), so P stays <= 2^8.
@@ -82,13 +98,13 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
   const int wg = nwg - 1 - rank / BH;
   const int bk = rank - (rank / BH) * BH;
   const int b = bk / Hkv, kvh = bk - b * Hkv;
-  const int task = wg * 4 + wave;
+  const int task = wg * NW + wave;
   const bool active = task < ntasks;
   const int qb = task / G;
   const int h = kvh * G + (task - qb * G);
   const int q0 = qb * 32;
   const int qi = q0 + n;
-  const int last_task = min(wg * 4 + 3, ntasks - 1);
+  const int last_task = min(wg * NW + NW - 1, ntasks - 1);
   const int wg_qmax = (last_task / G) * 32 + 31;
   const int kend = (CAUSAL && MASK != 2) ? min(S, wg_qmax + 1) : S;
   const int nkb = (kend + BN - 1) / BN;
@@ -97,7 +113,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
   const bf16* vbase = v + b * vs0 + kvh * vs1;
 
   if (DT * 32 > HD) {  // zero the padding rows of both V^T buffers once
-    for (int i = tid; i < (DT * 32 - HD) * VROW; i += 256) {
+    for (int i = tid; i < (DT * 32 - HD) * VROW; i += NT) {
       Vt[HD * VROW + i] = 0;
       Vt[VBUF + HD * VROW + i] = 0;
     }
@@ -119,53 +135,90 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
   // MFMA of every iteration wait for the next tile's prefetch as well.
   __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
 
+  constexpr int VTCH = (HD * (BN / 8) + NT - 1) / NT;  // V^T 16-byte chunks per thread
   uint4 kreg[KCH];
-  uint4 vreg[VCH][2];
-  auto fetch = [&](int key0) {
+  uint4 vreg[VT ? VTCH : VCH][2];
+  // Global -> registers for the tile at key0.  FULL tiles (key0 + BN <= S)
+  // skip the per-row bounds tests.
+  auto fetch = [&](int key0, auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + NT * j;
       const int key = c / DC, dc = c - key * DC;
-      kreg[j] = make_uint4(0, 0, 0, 0);
-      if (c < BN * DC && key0 + key < S)
+      if (FULL && (BN * DC) % NT == 0) {
         kreg[j] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key0 + key) * ks2 + dc * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < VCH; ++j) {
-      const int u = tid + 256 * j;
-      const int kp = u / DC, dc = u - kp * DC;
-      const int key = key0 + 2 * kp;
-      vreg[j][0] = make_uint4(0, 0, 0, 0);
-      vreg[j][1] = make_uint4(0, 0, 0, 0);
-      if (u < (BN / 2) * DC) {
-        if (key < S) vreg[j][0] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * vs2 + dc * 8);
-        if (key + 1 < S) vreg[j][1] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key + 1) * vs2 + dc * 8);
+      } else {
+        kreg[j] = make_uint4(0, 0, 0, 0);
+        if (c < BN * DC && (FULL || key0 + key < S))
+          kreg[j] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key0 + key) * ks2 + dc * 8);
       }
     }
+    if constexpr (VT) {
+#pragma unroll
+      for (int j = 0; j < VTCH; ++j) {
+        const int c = tid + NT * j;
+        const int d = c / (BN / 8), kc = c - d * (BN / 8);
+        vreg[j][0] = make_uint4(0, 0, 0, 0);
+        // S % 8 == 0 on this path, so a chunk is either fully in or out
+        if (c < HD * (BN / 8) && (FULL || key0 + 8 * kc < S))
+          vreg[j][0] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(d) * vs2 + key0 + 8 * kc);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VCH; ++j) {
+        const int u = tid + NT * j;
+        const int kp = u / DC, dc = u - kp * DC;
+        const int key = key0 + 2 * kp;
+        vreg[j][0] = make_uint4(0, 0, 0, 0);
+        vreg[j][1] = make_uint4(0, 0, 0, 0);
+        if (u < (BN / 2) * DC) {
+          if (FULL || key < S) vreg[j][0] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * vs2 + dc * 8);
+          if (FULL || key + 1 < S) vreg[j][1] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key + 1) * vs2 + dc * 8);
+        }
+      }
+    }
+  };
+  auto fetch_tile = [&](int key0) {
+    if (key0 + BN <= S) fetch(key0, std::true_type());
+    else fetch(key0, std::false_type());
   };
   auto stage = [&](int buf) {
     uint16_t* kd = Ks + buf * KBUF;
     uint16_t* vd = Vt + buf * VBUF;
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + NT * j;
       const int key = c / DC, dc = c - key * DC;
       if (c < BN * DC) *reinterpret_cast<uint4*>(&kd[key * KROW + dc * 8]) = kreg[j];
     }
+    if constexpr (VT) {
 #pragma unroll
-    for (int j = 0; j < VCH; ++j) {
-      const int u = tid + 256 * j;
-      const int kp = u / DC, dc = u - kp * DC;
-      if (u < (BN / 2) * DC) {
-        const uint32_t a[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
-        const uint32_t c2[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
+      for (int j = 0; j < VTCH; ++j) {
+        const int c = tid + NT * j;
+        const int d = c / (BN / 8), kc = c - d * (BN / 8);
+        if (c < HD * (BN / 8)) {
+          // VROW*2 bytes is a multiple of 8, not of 16: two 8-byte stores
+          *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc]) = make_uint2(vreg[j][0].x, vreg[j][0].y);
+          *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc + 4]) = make_uint2(vreg[j][0].z, vreg[j][0].w);
+        }
+      }
+    } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
-          const uint32_t lo = __builtin_amdgcn_perm(c2[e], a[e], 0x05040100u);
-          const uint32_t hi = __builtin_amdgcn_perm(c2[e], a[e], 0x07060302u);
-          *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
-          *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
+      for (int j = 0; j < VCH; ++j) {
+        const int u = tid + NT * j;
+        const int kp = u / DC, dc = u - kp * DC;
+        if (u < (BN / 2) * DC) {
+          const uint32_t a[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
+          const uint32_t c2[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
+            const uint32_t lo = __builtin_amdgcn_perm(c2[e], a[e], 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(c2[e], a[e], 0x07060302u);
+            *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
+            *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
+          }
         }
       }
     }
@@ -236,26 +289,31 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
       m_i = m_new;
     }
     const float m_use = m_i == -INFINITY ? 0.f : m_i;
+    // P in bf16, and its row sum from the same rounded values (v_dot2 with
+    // (1, 1)), so the normalisation uses exactly the P of the PV product.
+    uint4 pk[4];
     float rs = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int mt = s2 >> 1, rb = 8 * (s2 & 1);
+      float p[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(st[mt][r], scale_log2, -m_use));
-        st[mt][r] = p;
-        rs += p;
-      }
+      for (int e = 0; e < 8; ++e)
+        p[e] = __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
+      pk[s2].x = pack2<bf16>(p[0], p[1]);
+      pk[s2].y = pack2<bf16>(p[2], p[3]);
+      pk[s2].z = pack2<bf16>(p[4], p[5]);
+      pk[s2].w = pack2<bf16>(p[6], p[7]);
+      rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
+      rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
+      rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
+      rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
+    }
     l_i += rs + __shfl_xor(rs, 32);
     // O^T += V^T P^T over 4 k-steps of 16 keys.
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) {
-      const int mt = s2 >> 1, rb = 8 * (s2 & 1);
-      uint4 praw;
-      praw.x = pack2<bf16>(st[mt][rb + 0], st[mt][rb + 1]);
-      praw.y = pack2<bf16>(st[mt][rb + 2], st[mt][rb + 3]);
-      praw.z = pack2<bf16>(st[mt][rb + 4], st[mt][rb + 5]);
-      praw.w = pack2<bf16>(st[mt][rb + 6], st[mt][rb + 7]);
-      const bf16x8_t pf = as_bf16x8(praw);
+      const bf16x8_t pf = as_bf16x8(pk[s2]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const uint16_t* vr = &vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
@@ -269,19 +327,19 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
 
   // Tiles [0, nfull) are in bounds and at or below the diagonal of every
   // wave of the workgroup; the rest need the mask.
-  const int wg_qmin = ((wg * 4) / G) * 32;
+  const int wg_qmin = ((wg * NW) / G) * 32;
   int nfull = 0;
   if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
   nfull = min(nfull, nkb);
 
   if (nkb > 0) {
-    fetch(0);
+    fetch_tile(0);
     stage(0);
   }
   __syncthreads();
   int kb = 0;
   for (; kb < nfull; ++kb) {
-    if (kb + 1 < nkb) fetch((kb + 1) * BN);
+    if (kb + 1 < nkb) fetch_tile((kb + 1) * BN);
     if (active) tile(kb, std::false_type());
     // The next tile goes into the other buffer, which every wave finished
     // reading before the barrier that ended the previous iteration.
@@ -289,7 +347,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(
     __syncthreads();
   }
   for (; kb < nkb; ++kb) {
-    if (kb + 1 < nkb) fetch((kb + 1) * BN);
+    if (kb + 1 < nkb) fetch_tile((kb + 1) * BN);
     const bool live = active && !(CAUSAL && MASK != 2 && kb * BN > q0 + 31);
     if (live) tile(kb, std::true_type());
     if (kb + 1 < nkb) stage((kb & 1) ^ 1);
@@ -324,7 +382,7 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
     T* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
     int B, int S, int Hq, int Hkv, int hd, int causal, int mask_mode,
     int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
-    int64_t vs0, int64_t vs1, int64_t vs2, int64_t os0, int64_t os1, int64_t os2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t vs3, int64_t os0, int64_t os1, int64_t os2,
     float scale) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (gid >= static_cast<int64_t>(B) * Hq * S) return;
@@ -358,7 +416,7 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
     const float p = expf(x - m);
     l += p;
     const T* vr = vb + static_cast<int64_t>(t) * vs2;
-    for (int d = 0; d < hd; ++d) acc[d] = fmaf(p, to_f32(vr[d]), acc[d]);
+    for (int d = 0; d < hd; ++d) acc[d] = fmaf(p, to_f32(vr[d * vs3]), acc[d]);
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   T* orow = o + b * os0 + h * os1 + static_cast<int64_t>(s) * os2;
@@ -372,28 +430,52 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
                        int64_t Hkv, int64_t S, const int64_t* qs, const int64_t* ks,
                        const int64_t* vs, const int64_t* os, bool causal, float scale,
                        hipStream_t st) {
+  // V with unit stride along the keys is read as V^T rows (vs[3] apart).
+  const bool vt = vs[2] == 1 && vs[3] != 1;
   const int G = static_cast<int>(Hq / Hkv);
   const int nqb = static_cast<int>((S + 31) / 32);
   const int ntasks = G * nqb;
-  const int nwg = (ntasks + 3) / 4;
+  // Four-wave workgroups share each staged K/V tile between four query
+  // blocks; two-wave ones (HYDRA_ATTN_NW=2) halve that reuse and measured
+  // slower even where they double the workgroup count.
+  int nw = 4;
+  if (const char* e = getenv("HYDRA_ATTN_NW")) nw = atoi(e) == 2 ? 2 : 4;
+  const int nwg = (ntasks + nw - 1) / nw;
   const dim3 grid(static_cast<unsigned>(nwg * B * Hkv));
   const float sl2 = scale * kLog2e;
   auto Q = static_cast<const bf16*>(q);
   auto K = static_cast<const bf16*>(k);
   auto V = static_cast<const bf16*>(v);
   auto O = static_cast<bf16*>(o);
-#define HYDRA_ATTN_LAUNCH(C, M)                                                      \
-  attn_fwd_mfma_kernel<HD, C, M><<<grid, 256, 0, st>>>(                              \
-      Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, nwg, qs[0], qs[1], \
-      qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], sl2)
+  auto go = [&](auto c_tag, auto m_tag, auto nw_tag) {
+    constexpr bool C = decltype(c_tag)::value;
+    constexpr int M = decltype(m_tag)::value;
+    constexpr int NW = decltype(nw_tag)::value;
+    if (vt)
+      attn_fwd_mfma_kernel<HD, C, M, true, NW><<<grid, 64 * NW, 0, st>>>(
+          Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, nwg, qs[0], qs[1],
+          qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[3], os[0], os[1], os[2], sl2);
+    else
+      attn_fwd_mfma_kernel<HD, C, M, false, NW><<<grid, 64 * NW, 0, st>>>(
+          Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, nwg, qs[0], qs[1],
+          qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], sl2);
+  };
+  auto by_nw = [&](auto c_tag, auto m_tag) {
+    if (nw == 2) go(c_tag, m_tag, std::integral_constant<int, 2>());
+    else go(c_tag, m_tag, std::integral_constant<int, 4>());
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using M0 = std::integral_constant<int, 0>;
+  using M1 = std::integral_constant<int, 1>;
+  using M2 = std::integral_constant<int, 2>;
   // The reference-SDPA mask mode opens keys above the diagonal, so it walks
   // every key tile (no causal tile skipping).
-  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) HYDRA_ATTN_LAUNCH(false, 2);
-  else if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) HYDRA_ATTN_LAUNCH(true, 1);
-  else if (causal) HYDRA_ATTN_LAUNCH(true, 0);
-  else if (mask_mode == HYDRA_MASK_KEY_PADDING) HYDRA_ATTN_LAUNCH(false, 1);
-  else HYDRA_ATTN_LAUNCH(false, 0);
-#undef HYDRA_ATTN_LAUNCH
+  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) by_nw(F_(), M2());
+  else if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) by_nw(T_(), M1());
+  else if (causal) by_nw(T_(), M0());
+  else if (mask_mode == HYDRA_MASK_KEY_PADDING) by_nw(F_(), M1());
+  else by_nw(F_(), M0());
   return check_launch("attn_fwd_mfma_kernel");
 }
 
@@ -412,7 +494,7 @@ static int launch_generic(const void* q, const void* k, const void* v, void* o, 
 #define HYDRA_GEN_LAUNCH(MAXHD)                                                       \
   attn_fwd_generic_kernel<T, MAXHD><<<grid, 256, 0, st>>>(                            \
       Q, K, V, O, lse, kmask, (int)B, (int)S, (int)Hq, (int)Hkv, (int)hd, causal ? 1 : 0, \
-      mask_mode, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],  \
+      mask_mode, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], vs[3], os[0], \
       os[1], os[2], scale)
   if (hd <= 32) HYDRA_GEN_LAUNCH(32);
   else if (hd <= 64) HYDRA_GEN_LAUNCH(64);
@@ -435,8 +517,10 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_fwd: bad size");
   HYDRA_REQUIRE(Hq % Hkv == 0, "attn_fwd: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(qs && ks && vs && os, "attn_fwd: null stride array");
-  HYDRA_REQUIRE(qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1,
-                "attn_fwd: head_dim must have unit stride");
+  HYDRA_REQUIRE(qs[3] == 1 && ks[3] == 1 && os[3] == 1,
+                "attn_fwd: q, k and o must have unit stride along head_dim");
+  HYDRA_REQUIRE(vs[3] == 1 || vs[2] == 1,
+                "attn_fwd: v needs unit stride along head_dim or along the sequence");
   HYDRA_REQUIRE(hd <= 256, "attn_fwd: head_dim must be <= 256");
   HYDRA_REQUIRE(mask_mode >= HYDRA_MASK_NONE && mask_mode <= HYDRA_MASK_REFERENCE_SDPA,
                 "attn_fwd: unknown mask mode");
@@ -454,7 +538,12 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   const bool mfma_shape = (hd == 16 || hd == 32 || hd == 64 || hd == 128);
   bool strides8 = true;
   for (int i = 0; i < 3; ++i)
-    strides8 = strides8 && qs[i] % 8 == 0 && ks[i] % 8 == 0 && vs[i] % 8 == 0 && os[i] % 4 == 0;
+    strides8 = strides8 && qs[i] % 8 == 0 && ks[i] % 8 == 0 && os[i] % 4 == 0;
+  if (vs[3] == 1) {
+    strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[2] % 8 == 0;
+  } else {  // V^T rows: 16-byte chunks of 8 keys, so S must be a multiple of 8
+    strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[3] % 8 == 0 && S % 8 == 0;
+  }
   if (dtype == HYDRA_BF16 && mfma_shape && strides8 && aligned16(q) && aligned16(k) &&
       aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0) {
     switch (hd) {

@@ -187,7 +187,10 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
       val = xb[static_cast<int64_t>(s) * qkv_rs + L + K + c];
     }
     const int j = c / hd, d = c - j * hd;
-    vo[((static_cast<int64_t>(b) * Hkv + j) * S + s) * hd + d] = val;
+    if (flags & HYDRA_CCGQA_V_TRANSPOSED)
+      vo[((static_cast<int64_t>(b) * Hkv + j) * hd + d) * S + s] = val;
+    else
+      vo[((static_cast<int64_t>(b) * Hkv + j) * S + s) * hd + d] = val;
   }
 }
 
@@ -458,20 +461,42 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
     store16<bf16>(dst, v);
   }
 
-  // ---- v (value shift), 16-byte copies -------------------------------------
+  // ---- v (value shift) ----------------------------------------------------
   const int k8 = K / 8;
-  for (int i = tid; i < TT * k8; i += kPrepThreads) {
-    const int r = i / k8, c = (i - r * k8) * 8;
-    const int s = s0 + r;
-    if (s >= S) continue;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (vshift && c >= K / 2) {
-      if (s > 0) val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s - 1) * qkv_rs + L + K + c);
-    } else {
-      val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + c);
+  if (flags & HYDRA_CCGQA_V_TRANSPOSED) {
+    // v^T [B, Hkv, hd, S]: each item packs 8 consecutive tokens of one channel
+    // into one 16-byte store (tokens come from the L2-resident qkv rows).
+    for (int i = tid; i < K * (TT / 8); i += kPrepThreads) {
+      const int c = i / (TT / 8), t8 = (i - c * (TT / 8)) * 8;
+      const bool prev = vshift && c >= K / 2;
+      float vals[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int s = s0 + t8 + e;
+        const int src = prev ? s - 1 : s;
+        vals[e] = (s < S && src >= 0)
+                      ? to_f32(xb[static_cast<int64_t>(src) * qkv_rs + L + K + c])
+                      : 0.f;
+      }
+      if (s0 + t8 < S) {
+        const int j = c / HD, d = c - j * HD;
+        store16<bf16>(vo + ((static_cast<int64_t>(b) * Hkv + j) * HD + d) * S + s0 + t8, vals);
+      }
     }
-    const int j = c / HD, d = c - j * HD;
-    *reinterpret_cast<uint4*>(vo + ((static_cast<int64_t>(b) * Hkv + j) * S + s) * HD + d) = val;
+  } else {
+    for (int i = tid; i < TT * k8; i += kPrepThreads) {
+      const int r = i / k8, c = (i - r * k8) * 8;
+      const int s = s0 + r;
+      if (s >= S) continue;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (vshift && c >= K / 2) {
+        if (s > 0) val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s - 1) * qkv_rs + L + K + c);
+      } else {
+        val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + c);
+      }
+      const int j = c / HD, d = c - j * HD;
+      *reinterpret_cast<uint4*>(vo + ((static_cast<int64_t>(b) * Hkv + j) * S + s) * HD + d) = val;
+    }
   }
 }
 
@@ -542,7 +567,7 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 2, "ccgqa_prep: bad size");
   HYDRA_REQUIRE(Hq % Hkv == 0, "ccgqa_prep: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(hd % 2 == 0, "ccgqa_prep: head_dim must be even");
-  HYDRA_REQUIRE((flags & ~31) == 0, "ccgqa_prep: unknown flag bits");
+  HYDRA_REQUIRE((flags & ~63) == 0, "ccgqa_prep: unknown flag bits");
   const int64_t L = Hq * hd, K = Hkv * hd;
   HYDRA_REQUIRE(!(flags & HYDRA_CCGQA_VALUE_SHIFT) || K % 2 == 0,
                 "ccgqa_prep: kv_dim must be even for the value shift");
@@ -564,7 +589,8 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
       aligned16(v_out) &&
       (!(flags & HYDRA_CCGQA_CONVS) || (aligned16(wq1) && aligned16(wq2) && aligned16(wk1) &&
                                         aligned16(wk2))) &&
-      (!rope || (cs_rs % 4 == 0 && aligned16(cos) && aligned16(sin)));
+      (!rope || (cs_rs % 4 == 0 && aligned16(cos) && aligned16(sin))) &&
+      (!(flags & HYDRA_CCGQA_V_TRANSPOSED) || S % 8 == 0);
   if (mfma_ok) {
     int dev = 0, max_lds = 65536;
     if (hipGetDevice(&dev) == hipSuccess)

@@ -57,10 +57,33 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // Elements of T in one 16-byte vector.
 template <typename T> struct Vec { static constexpr int N = 16 / sizeof(T); };
 
-// 16-byte load / store of N elements of T, converted to / from fp32.
+// 16-byte load / store of N elements of T, converted to / from fp32.  NT
+// marks the access non-temporal (streamed once: no allocation in L2/MALL),
+// which gains ~7% of HBM bandwidth on pure streaming kernels on gfx950.
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_nt;
+
+template <bool NT>
+__device__ __forceinline__ uint4 ld16raw(const void* p) {
+  if constexpr (NT) {
+    const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ void st16raw(void* p, uint4 v) {
+  if constexpr (NT) {
+    const u32x4_nt w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4_nt*>(p));
+  } else {
+    *reinterpret_cast<uint4*>(p) = v;
+  }
+}
+
 template <typename T>
-__device__ __forceinline__ void load16(const T* p, float* out) {
-  const uint4 raw = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ void unpack16(const uint4 raw, float* out) {
   if constexpr (sizeof(T) == 4) {
     out[0] = __uint_as_float(raw.x); out[1] = __uint_as_float(raw.y);
     out[2] = __uint_as_float(raw.z); out[3] = __uint_as_float(raw.w);
@@ -78,18 +101,26 @@ __device__ __forceinline__ void load16(const T* p, float* out) {
 }
 
 template <typename T>
-__device__ __forceinline__ void store16(T* p, const float* in) {
+__device__ __forceinline__ uint4 pack16(const float* in) {
   uint4 raw;
   if constexpr (sizeof(T) == 4) {
     raw.x = __float_as_uint(in[0]); raw.y = __float_as_uint(in[1]);
     raw.z = __float_as_uint(in[2]); raw.w = __float_as_uint(in[3]);
   } else {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = pack2<T>(in[2 * i], in[2 * i + 1]);
-    raw.x = w[0]; raw.y = w[1]; raw.z = w[2]; raw.w = w[3];
+    raw.x = pack2<T>(in[0], in[1]); raw.y = pack2<T>(in[2], in[3]);
+    raw.z = pack2<T>(in[4], in[5]); raw.w = pack2<T>(in[6], in[7]);
   }
-  *reinterpret_cast<uint4*>(p) = raw;
+  return raw;
+}
+
+template <typename T, bool NT = false>
+__device__ __forceinline__ void load16(const T* p, float* out) {
+  unpack16<T>(ld16raw<NT>(p), out);
+}
+
+template <typename T, bool NT = false>
+__device__ __forceinline__ void store16(T* p, const float* in) {
+  st16raw<NT>(p, pack16<T>(in));
 }
 
 // ---- wave64 reductions ---------------------------------------------------

@@ -10,44 +10,59 @@ constexpr int kBlock = 256;  // 4 waves
 
 // ===========================================================================
 // RMSNorm   (reference: _fused_rms_norm_kernel, fused_ops.py:969-1007)
-// One wave per row.  The row stays in registers as raw 16-byte vectors, so
-// HBM sees exactly one read of x and one write of y.
+// LPR lanes per row, CPL 16-byte chunks per lane, RI row groups per wave:
+// every lane issues RI*CPL independent 16-byte loads before it reduces, so
+// each wave keeps several KB in flight (the kernel is latency- not
+// issue-bound otherwise).  The row stays in registers: one read of x, one
+// write of y.
 // ===========================================================================
-template <typename T, int VPL>
+template <typename T, int LPR, int CPL, int RI>
 __global__ __launch_bounds__(kBlock) void rms_norm_vec_kernel(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
     int64_t rows, int nvec, int dim, int64_t x_rs, int64_t y_rs, float eps) {
   constexpr int E = Vec<T>::N;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const T* xr = x + row * x_rs;
-  uint4 raw[VPL];
-  float ss = 0.f;
+  constexpr int RPW = 64 / LPR;                 // rows per wave per group
+  constexpr int RPB = (kBlock / 64) * RPW * RI;  // rows per block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, l = lane % LPR;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB + (wave * RI) * RPW + sub;
+  uint4 raw[RI][CPL];
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) {
-    const int vi = lane + 64 * v;
-    if (vi < nvec) {
-      raw[v] = *reinterpret_cast<const uint4*>(xr + vi * E);
+  for (int g = 0; g < RI; ++g) {
+    const int64_t row = row0 + g * RPW;
+#pragma unroll
+    for (int v = 0; v < CPL; ++v) {
+      const int vi = l + LPR * v;
+      raw[g][v] = make_uint4(0, 0, 0, 0);
+      if (row < rows && vi < nvec)
+        raw[g][v] = ld16raw<true>(x + row * x_rs + vi * E);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < RI; ++g) {
+    const int64_t row = row0 + g * RPW;
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < CPL; ++v) {
       float f[E];
-      load16<T>(reinterpret_cast<const T*>(&raw[v]), f);
+      load16<T>(reinterpret_cast<const T*>(&raw[g][v]), f);
 #pragma unroll
       for (int e = 0; e < E; ++e) ss = fmaf(f[e], f[e], ss);
     }
-  }
-  ss = wave_sum(ss);
-  const float rinv = rsqrtf(ss / static_cast<float>(dim) + eps);
-  T* yr = y + row * y_rs;
+    ss = wave_sum<LPR>(ss);
+    const float rinv = rsqrtf(ss / static_cast<float>(dim) + eps);
+    if (row >= rows) continue;
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) {
-    const int vi = lane + 64 * v;
-    if (vi < nvec) {
-      float f[E], g[E];
-      load16<T>(reinterpret_cast<const T*>(&raw[v]), f);
-      load16<T>(w + vi * E, g);
+    for (int v = 0; v < CPL; ++v) {
+      const int vi = l + LPR * v;
+      if (vi < nvec) {
+        float f[E], gw[E];
+        load16<T>(reinterpret_cast<const T*>(&raw[g][v]), f);
+        load16<T>(w + vi * E, gw);
 #pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = f[e] * rinv * g[e];
-      store16<T>(yr + vi * E, f);
+        for (int e = 0; e < E; ++e) f[e] = f[e] * rinv * gw[e];
+        store16<T, true>(y + row * y_rs + vi * E, f);
+      }
     }
   }
 }
@@ -73,32 +88,47 @@ __global__ __launch_bounds__(kBlock) void rms_norm_scalar_kernel(
   }
 }
 
+template <typename T, int LPR, int CPL>
+static int launch_rms_vec(const T* X, const T* W, T* Y, int64_t rows, int nvec, int64_t dim,
+                          int64_t x_rs, int64_t y_rs, float eps, hipStream_t st) {
+  constexpr int RI = CPL >= 4 ? 1 : (CPL >= 2 ? 2 : 4);
+  constexpr int RPB = (kBlock / 64) * (64 / LPR) * RI;
+  const dim3 grid(static_cast<unsigned>((rows + RPB - 1) / RPB));
+  rms_norm_vec_kernel<T, LPR, CPL, RI><<<grid, kBlock, 0, st>>>(X, W, Y, rows, nvec, (int)dim,
+                                                               x_rs, y_rs, eps);
+  return check_launch("rms_norm_vec_kernel");
+}
+
 template <typename T>
 static int launch_rms_norm(const void* x, const void* w, void* y, int64_t rows,
                            int64_t dim, int64_t x_rs, int64_t y_rs, float eps,
                            hipStream_t st) {
   constexpr int E = Vec<T>::N;
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   const bool vec_ok = dim % E == 0 && x_rs % E == 0 && y_rs % E == 0 &&
                       aligned16(x) && aligned16(w) && aligned16(y);
   const int nvec = static_cast<int>(dim / E);
-  const int vpl = (nvec + 63) / 64;
   auto X = static_cast<const T*>(x);
   auto W = static_cast<const T*>(w);
   auto Y = static_cast<T*>(y);
-  if (vec_ok && vpl <= 16) {
-#define HYDRA_RMS_CASE(V)                                                      \
-  if (vpl <= V) {                                                              \
-    rms_norm_vec_kernel<T, V><<<grid, kBlock, 0, st>>>(X, W, Y, rows, nvec,    \
-                                                       (int)dim, x_rs, y_rs, eps); \
-    return check_launch("rms_norm_vec_kernel");                                \
-  }
-    HYDRA_RMS_CASE(1) HYDRA_RMS_CASE(2) HYDRA_RMS_CASE(3) HYDRA_RMS_CASE(4)
-    HYDRA_RMS_CASE(8) HYDRA_RMS_CASE(16)
+  if (vec_ok && nvec <= 64 * 8) {
+    // Lanes per row: the largest power of two <= 64 that leaves no idle lane
+    // slot (nvec % LPR == 0) with at most 8 chunks per lane; else 64 lanes.
+    int lpr = 64;
+    for (int cand : {64, 32, 16, 8, 4}) {
+      if (nvec % cand == 0 && nvec / cand <= 8) { lpr = cand; break; }
+    }
+    const int cpl = (nvec + lpr - 1) / lpr;
+#define HYDRA_RMS_CASE(LP, CP) \
+  if (lpr == LP && cpl <= CP) return launch_rms_vec<T, LP, CP>(X, W, Y, rows, nvec, dim, x_rs, y_rs, eps, st);
+    HYDRA_RMS_CASE(4, 1) HYDRA_RMS_CASE(4, 2) HYDRA_RMS_CASE(4, 4) HYDRA_RMS_CASE(4, 8)
+    HYDRA_RMS_CASE(8, 1) HYDRA_RMS_CASE(8, 2) HYDRA_RMS_CASE(8, 4) HYDRA_RMS_CASE(8, 8)
+    HYDRA_RMS_CASE(16, 1) HYDRA_RMS_CASE(16, 2) HYDRA_RMS_CASE(16, 4) HYDRA_RMS_CASE(16, 6) HYDRA_RMS_CASE(16, 8)
+    HYDRA_RMS_CASE(32, 1) HYDRA_RMS_CASE(32, 2) HYDRA_RMS_CASE(32, 3) HYDRA_RMS_CASE(32, 4) HYDRA_RMS_CASE(32, 6) HYDRA_RMS_CASE(32, 8)
+    HYDRA_RMS_CASE(64, 1) HYDRA_RMS_CASE(64, 2) HYDRA_RMS_CASE(64, 3) HYDRA_RMS_CASE(64, 4) HYDRA_RMS_CASE(64, 6) HYDRA_RMS_CASE(64, 8)
 #undef HYDRA_RMS_CASE
   }
-  rms_norm_scalar_kernel<T><<<grid, kBlock, 0, st>>>(X, W, Y, rows, (int)dim,
-                                                     x_rs, y_rs, eps);
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  rms_norm_scalar_kernel<T><<<grid, kBlock, 0, st>>>(X, W, Y, rows, (int)dim, x_rs, y_rs, eps);
   return check_launch("rms_norm_scalar_kernel");
 }
 
@@ -107,32 +137,43 @@ static int launch_rms_norm(const void* x, const void* w, void* y, int64_t rows,
 // blockIdx.y = b*H + h; each thread rotates one 16-byte chunk (E/2 pairs).
 // Output is the contiguous [B,H,S,D] tensor; x may be any strided view.
 // ===========================================================================
-template <typename T, typename C>
+template <typename T, typename C, int CH>
 __global__ __launch_bounds__(kBlock) void rope_vec_kernel(
     const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
     T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
     int64_t cs_rs) {
+  // Each thread rotates CH chunks of the same column, in rows kBlock/cpr
+  // apart, issuing all CH loads first.
   constexpr int E = Vec<T>::N;
   const int cpr = D / E;  // chunks per row
   const int bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
-  const int t = blockIdx.x * kBlock + threadIdx.x;
-  const int s = t / cpr;
-  if (s >= S) return;
-  const int c = t - s * cpr;
-  float f[E];
-  load16<T>(x + b * xb + h * xh + static_cast<int64_t>(s) * xsr + c * E, f);
-  const C* cr = cs + static_cast<int64_t>(s) * cs_rs + c * (E / 2);
-  const C* sr = sn + static_cast<int64_t>(s) * cs_rs + c * (E / 2);
-  float o[E];
+  const int t = blockIdx.x * kBlock * CH + threadIdx.x;
+  const int c = threadIdx.x % cpr;
+  const int rstep = kBlock / cpr;
+  const int s0 = t / cpr;
+  float f[CH][E];
 #pragma unroll
-  for (int p = 0; p < E / 2; ++p) {
-    const float cv = to_f32(cr[p]), sv = to_f32(sr[p]);
-    const float x1 = f[2 * p], x2 = f[2 * p + 1];
-    o[2 * p] = x1 * cv - x2 * sv;
-    o[2 * p + 1] = x1 * sv + x2 * cv;
+  for (int j = 0; j < CH; ++j) {
+    const int s = s0 + j * rstep;
+    if (s < S) load16<T, true>(x + b * xb + h * xh + static_cast<int64_t>(s) * xsr + c * E, f[j]);
   }
-  store16<T>(out + (static_cast<int64_t>(bh) * S + s) * D + c * E, o);
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int s = s0 + j * rstep;
+    if (s >= S) continue;
+    const C* cr = cs + static_cast<int64_t>(s) * cs_rs + c * (E / 2);
+    const C* sr = sn + static_cast<int64_t>(s) * cs_rs + c * (E / 2);
+    float o[E];
+#pragma unroll
+    for (int p = 0; p < E / 2; ++p) {
+      const float cv = to_f32(cr[p]), sv = to_f32(sr[p]);
+      const float x1 = f[j][2 * p], x2 = f[j][2 * p + 1];
+      o[2 * p] = x1 * cv - x2 * sv;
+      o[2 * p + 1] = x1 * sv + x2 * cv;
+    }
+    store16<T, true>(out + (static_cast<int64_t>(bh) * S + s) * D + c * E, o);
+  }
 }
 
 template <typename T, typename C>
@@ -168,12 +209,14 @@ static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
   const bool vec_ok = xs[3] == 1 && D % E == 0 && xs[0] % E == 0 &&
                       xs[1] % E == 0 && xs[2] % E == 0 && aligned16(x) &&
                       aligned16(out);
-  if (vec_ok) {
+  // The multi-chunk path needs whole rows per block (kBlock % cpr == 0).
+  if (vec_ok && (kBlock % (D / E)) == 0) {
+    constexpr int CH = 4;
     const int64_t threads = S * (D / E);
-    const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock),
+    const dim3 grid(static_cast<unsigned>((threads + kBlock * CH - 1) / (kBlock * CH)),
                     static_cast<unsigned>(B * H));
-    rope_vec_kernel<T, C><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S,
-                                                   (int)D, xs[0], xs[1], xs[2], cs_rs);
+    rope_vec_kernel<T, C, CH><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S, (int)D,
+                                                       xs[0], xs[1], xs[2], cs_rs);
     return check_launch("rope_vec_kernel");
   }
   const int64_t threads = S * (D / 2);
@@ -206,8 +249,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_vec_kernel(
     rr[j] = idx / cpr;
     cc[j] = idx - rr[j] * cpr;
     if (idx < total) {
-      load16<T>(g + rr[j] * g_rs + cc[j] * E, gf[j]);
-      load16<T>(u + rr[j] * u_rs + cc[j] * E, uf[j]);
+      load16<T, true>(g + rr[j] * g_rs + cc[j] * E, gf[j]);
+      load16<T, true>(u + rr[j] * u_rs + cc[j] * E, uf[j]);
     }
   }
 #pragma unroll
@@ -217,7 +260,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_vec_kernel(
       float of[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) of[e] = silu_f32(gf[j][e]) * uf[j][e];
-      store16<T>(o + rr[j] * o_rs + cc[j] * E, of);
+      store16<T, true>(o + rr[j] * o_rs + cc[j] * E, of);
     }
   }
 }

@@ -90,6 +90,7 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
 #define HYDRA_CCGQA_VALUE_SHIFT 4
 #define HYDRA_CCGQA_QK_NORM     8
 #define HYDRA_CCGQA_ROPE        16
+#define HYDRA_CCGQA_V_TRANSPOSED 32 /* write v as [B, Hkv, hd, S] */
 
 /* Everything of CCGQAAttention.forward between the qkv GEMM and the attention
  * core, in one pass over token tiles: split of the fused projection, value
@@ -107,7 +108,9 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
  *       (unused and may be NULL without HYDRA_CCGQA_CONVS).
  * temp: key temperature, 1 element of `dtype` (NULL without QK_NORM).
  * cos/sin: fp32 [S, hd/2] row stride cs_rs (NULL without ROPE).
- * q_out: [B, Hq, S, hd]; k_out, v_out: [B, Hkv, S, hd]; all contiguous.
+ * q_out: [B, Hq, S, hd]; k_out: [B, Hkv, S, hd]; v_out: [B, Hkv, S, hd], or
+ * [B, Hkv, hd, S] with HYDRA_CCGQA_V_TRANSPOSED (the layout hydra_attn_fwd
+ * stages without a transpose); all contiguous.
  * bf16 with hd in {32, 64, 128} runs both convs on MFMA (up to ~100 KB of LDS
  * per workgroup at L+K = 320); other cases run on the VALU. */
 int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
@@ -138,7 +141,10 @@ int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
  * Replaces ccgqa_attention_fused (kernels/fused_attention.py:826-840, kernels
  * _fwd_gqa_kernel :14-110 and _fwd_kernel :341-429) and the SDPA call of
  * CCGQAAttention.forward (attention.py:268-327).
- * q: [B,Hq,S,hd], k/v: [B,Hkv,S,hd], element strides qs/ks/vs[4] (last = 1);
+ * q: [B,Hq,S,hd], k/v: [B,Hkv,S,hd], element strides qs/ks/vs[4]; q and k
+ *    need unit stride along hd; v needs it along hd or along S (the strides
+ *    of a [B,Hkv,hd,S] buffer, which the bf16 path stages without a
+ *    transpose; then S must be a multiple of 8);
  * o: element strides os[4] (last = 1) -- pass the strides of a [B,S,Hq,hd]
  *    buffer to write the merged-heads layout directly;
  * lse: optional fp32 [B,Hq,S] natural-log sum-exp of the scaled scores.

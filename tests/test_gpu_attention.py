@@ -147,3 +147,31 @@ def test_attention_deterministic(cuda):
     a, _ = attention_forward(q, k, v, causal=True)
     b, _ = attention_forward(q, k, v, causal=True)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("case", [(4, 4, 1, 512, 64), (2, 8, 2, 256, 16), (1, 4, 4, 136, 32), (1, 2, 1, 64, 128)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_v_transposed_layout(cuda, case, causal):
+    """V handed over as [B,Hkv,hd,S] (keys contiguous): the bf16 kernel stages
+    it without a transpose; results equal the row-major V path."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    B, Hq, Hkv, S, hd = case
+    q, k, v = _qkv(*case, seed=31)
+    qd, kd = q.to(cuda, torch.bfloat16), k.to(cuda, torch.bfloat16)
+    vt = v.transpose(2, 3).contiguous().to(cuda, torch.bfloat16)  # [B,Hkv,hd,S]
+    out_t, _ = attention_forward(qd, kd, vt.transpose(2, 3), causal=causal)
+    out_r, _ = attention_forward(qd, kd, v.to(cuda, torch.bfloat16), causal=causal)
+    assert max_rel_err(out_t.cpu(), occ.attention(q, k, v, causal=causal)) < 2e-2
+    assert torch.equal(out_t.cpu(), out_r.cpu())
+
+
+def test_attention_v_transposed_odd_length_generic(cuda):
+    """S not a multiple of 8 with transposed V goes to the generic kernel."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    q, k, v = _qkv(1, 4, 1, 37, 64, seed=32)
+    vt = v.transpose(2, 3).contiguous().to(cuda, torch.bfloat16)
+    out, _ = attention_forward(q.to(cuda, torch.bfloat16), k.to(cuda, torch.bfloat16),
+                               vt.transpose(2, 3), causal=True)
+    assert max_rel_err(out.cpu(), occ.attention(q, k, v, causal=True)) < 2e-2

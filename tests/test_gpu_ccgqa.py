@@ -72,8 +72,19 @@ def test_prep_kernel(cuda, case, dtype):
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     for got, want in zip((q, k, v), ref):
         assert max_rel_err(got.cpu(), want) < tol
-    if dtype == torch.float32:
-        assert torch.equal(v.cpu(), ref[2])  # the value shift is a pure copy
+    assert torch.equal(v.cpu().float(), ref[2].to(dtype).float())  # the value shift is a copy
+    # V^T output layout: the same values, transposed in memory
+    from hydra_amd._lib import CCGQA_V_TRANSPOSED
+
+    if S % 8 == 0 or dtype == torch.float32:
+        q2, k2, v2 = ccgqa_prep(qkv.to(cuda), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                flags | CCGQA_V_TRANSPOSED,
+                                *[None if w is None else w.to(cuda) for w in conv],
+                                temperature=params["key_temperature"].to(cuda),
+                                cos=cos.to(cuda), sin=sin.to(cuda))
+        assert v2.stride(-2) == 1
+        assert torch.equal(v2.cpu(), v.cpu())
+        assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(k2.cpu(), k.cpu())
 
 
 def _bench_case(dim, n_heads, n_kv_heads, B, S, dtype, temperature, seed):
