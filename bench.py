@@ -8,8 +8,10 @@ full module forward: qkv GEMM -> fused prep kernel -> attention kernel ->
 o_proj GEMM, inputs resident in HBM.
 
 Also reported on the same line:
-  roofline      the attention kernel (dominant), algorithmic FLOPs / its
-                average duration from HIP events over the timed steps;
+  roofline      the attention op (dominant: the attention kernel and, when
+                the stream-K schedule splits items, its merge kernel),
+                algorithmic FLOPs / its average duration from HIP events
+                recorded on the launch stream over the timed steps;
   stages        per-stage average durations of the step;
   fused_ops     config 2 RMSNorm / RoPE / SwiGLU in HBM GB/s and % of peak
                 (buffers rotated over > 512 MB so the 256 MB MALL cannot
@@ -102,10 +104,25 @@ class C3Step:
         return y
 
 
-def c3_flops(B=4, S=4096, dim=1024, Hq=4, Hkv=1, comp=4):
-    from oracle.ccgqa import CCGQAConfig, flops
-
-    return flops(CCGQAConfig(dim=dim, n_heads=Hq, n_kv_heads=Hkv, compression_factor=comp), B, S)
+def c3_flops(B=4, S=4096, dim=1024, Hq=4, Hkv=1, comp=4, ks=3):
+    """Algorithmic FLOPs of one config-3 forward (multiply-add = 2).  The
+    latent is dim/comp wide, split into Hq heads of hd = latent/Hq; K and V
+    are Hkv*hd wide.  Each conv sequence is a grouped k=3 conv (hd inputs
+    per output channel) followed by a dense k=3 conv; the attention core is
+    causal QK^T + PV over S(S+1)/2 (query, key) pairs per head."""
+    L = dim // comp
+    hd = L // Hq
+    K = Hkv * hd
+    N = B * S
+    f = {
+        "qkv_proj": 2 * N * dim * (L + 2 * K),
+        "q_conv": 2 * N * ks * (L * hd + L * L),
+        "k_conv": 2 * N * ks * (K * hd + K * K),
+        "core": 4 * B * Hq * hd * S * (S + 1) // 2,
+        "o_proj": 2 * N * L * dim,
+    }
+    f["total"] = sum(f.values())
+    return f
 
 
 def bench_c3(dev, steps, warmup):
@@ -330,7 +347,7 @@ def main():
         "config": {"workload": "config 3: CCGQA attention forward, dim 1024, latent 256, 4q/1kv heads "
                                "x hd 64, causal conv k=3, QK-mean, QK-norm tau 1.0, B4 x S4096, bf16",
                    "global_batch": step.B, "seq_len": step.S, "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "attn_fwd_mfma_kernel<64,causal>", "bound": "mfma",
+        "roofline": {"kernel": "attn_fwd_mfma_kernel<64,causal> + attn_merge_kernel<64>", "bound": "mfma",
                      "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS,
                      "traffic": measured_traffic("attn_fwd_mfma_kernel<64,true,0>"),

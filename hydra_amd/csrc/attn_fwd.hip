@@ -29,7 +29,11 @@
 // math, any element type, even head_dim <= 256.
 #include "common.h"
 
+#include <algorithm>
+#include <cstdio>
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 namespace hydra {
@@ -54,12 +58,126 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          __builtin_bit_cast(bf16x2_t, b), acc, false);
 }
 
+constexpr int kAttnBN = 64;  // keys per tile of the bf16 kernel
+
+// Key tiles item wg walks: all of them, or (causal) up to its last query.
+template <int NW>
+__host__ __device__ __forceinline__ int attn_tiles(int wg, int S, int G, int ntasks, bool causal) {
+  const int last_task = min(wg * NW + NW - 1, ntasks - 1);
+  const int kend = causal ? min(S, (last_task / G) * 32 + 32) : S;
+  return (kend + kAttnBN - 1) / kAttnBN;
+}
+
+// Item order.  Stream-K (alt): long and short items alternate (positions
+// 0, 2, 4, .. take items nwg-1, nwg-2, ..; positions 1, 3, .. take items
+// 0, 1, ..), so any contiguous run of tiles holds a similar number of item
+// starts.  One item per workgroup (!alt): longest first, so the hardware
+// dispatcher's greedy placement ends with the short items.
+__host__ __device__ __forceinline__ int attn_pos_item(int p, int nwg, bool alt) {
+  return (alt && (p & 1)) ? (p >> 1) : nwg - 1 - (alt ? (p >> 1) : p);
+}
+
+// Where tile v of the stream-K sequence lies.  The sequence walks positions
+// p = 0.., and within a position the BH (batch, kv-head) pairs, each with
+// the item's key tiles in order.  Wave-level: a lane-parallel prefix sum
+// over positions; every output is wave-uniform.  Requires 0 <= v < total.
+struct AttnLoc {
+  int wg, bk, kb, nkb, start;  // item, pair, tile within item, item tiles, v of its tile 0
+};
+template <int NW>
+__device__ __forceinline__ AttnLoc attn_locate(int v, int lane, int nwg, int BH, int S, int G,
+                                               int ntasks, bool walk, bool alt) {
+  const int per = (nwg + 63) / 64;
+  int cnt = 0;
+  for (int i = 0; i < per; ++i) {
+    const int p = lane * per + i;
+    if (p < nwg) cnt += attn_tiles<NW>(attn_pos_item(p, nwg, alt), S, G, ntasks, walk);
+  }
+  cnt *= BH;
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  const int L = __ffsll(static_cast<unsigned long long>(__ballot(v < incl))) - 1;
+  int base = __shfl(incl - cnt, L);
+  int p = L * per, nt = 1;
+  for (int i = 0; i < per; ++i, ++p) {
+    nt = attn_tiles<NW>(attn_pos_item(p, nwg, alt), S, G, ntasks, walk);
+    if (v < base + nt * BH) break;
+    base += nt * BH;
+  }
+  AttnLoc r;
+  r.wg = __builtin_amdgcn_readfirstlane(attn_pos_item(p, nwg, alt));
+  r.nkb = __builtin_amdgcn_readfirstlane(nt);
+  const int local = __builtin_amdgcn_readfirstlane(v - base);
+  r.bk = local / r.nkb;
+  r.kb = local - r.bk * r.nkb;
+  r.start = __builtin_amdgcn_readfirstlane(base) + r.bk * r.nkb;
+  return r;
+}
+
+// First tile of item w = p*BH + bk in the (!alt) sequence, and its length.
+template <int NW>
+__device__ __forceinline__ int2 attn_item_range(int w, int lane, int nwg, int BH, int S, int G,
+                                                int ntasks, bool walk) {
+  const int p = w / BH, bk = w - (w / BH) * BH;
+  int part = 0;
+  for (int i = lane; i < p; i += 64) part += attn_tiles<NW>(attn_pos_item(i, nwg, false), S, G, ntasks, walk);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+  const int nt = attn_tiles<NW>(attn_pos_item(p, nwg, false), S, G, ntasks, walk);
+  const int start = __builtin_amdgcn_readfirstlane(part * BH + bk * nt);
+  return make_int2(start, start + nt);
+}
+
+// First tile of workgroup w's range when T tiles are shared by P workgroups.
+__host__ __device__ __forceinline__ int attn_range_begin(int w, int T, int P) {
+  return static_cast<int>(static_cast<int64_t>(w) * T / P);
+}
+
+// x combined with its copy in the other half of the wave (lane l ^ 32),
+// through v_permlane32_swap: a = (x[0..31], x[0..31]), b = (x[32..63],
+// x[32..63]), so max(a, b) and a + b hold the pair's max and sum in every
+// lane (both halves get the same bits: + is commutative).
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Writes one query row of O (bf16) from the MFMA accumulator layout, with
+// the softmax normaliser 1/l, and its log-sum-exp (m is in log2 units).
+template <int HD>
+__device__ __forceinline__ void attn_store_row(bf16* orow, const f32x16_t* acc, float m, float l,
+                                               int hf, float* lse) {
+  constexpr int DT = (HD + 31) / 32;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * dt + 8 * g4 + 4 * hf;
+      if (d < HD) {
+        uint2 w;
+        w.x = pack2<bf16>(acc[dt][4 * g4 + 0] * inv, acc[dt][4 * g4 + 1] * inv);
+        w.y = pack2<bf16>(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d) = w;
+      }
+    }
+  if (lse && hf == 0) *lse = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+}
 
 template <int HD, bool CAUSAL, int MASK, bool VT, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
-    int S, int Hq, int Hkv, int G, int ntasks, int nwg,
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int T, int per_item,
+    float* __restrict__ ws, int4* __restrict__ desc,
     int64_t qs0, int64_t qs1, int64_t qs2,
     int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2,
@@ -67,7 +185,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   // VT: V is stored transposed ([.., hd, S], keys contiguous, row stride
   // vs2 between d rows) and is staged with plain 16-byte copies; otherwise
   // V is [.., S, hd] and is transposed while staged.
-  constexpr int BN = 64;                // keys per tile
+  constexpr int BN = kAttnBN;           // keys per tile
   constexpr int KSTEPS = HD / 16;       // k-steps of S^T = K Q^T
   constexpr int DT = (HD + 31) / 32;    // 32-row d tiles of O^T
   constexpr int KROW = HD + 8;          // padded LDS row of K (elements)
@@ -87,30 +205,28 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, hf = lane >> 5;
-  // Causal balance: workgroups are ranked by work (longest first) and the
-  // second half of the grid takes the ranks in reverse, so the two
-  // workgroups that share a CU carry complementary amounts of work.
-  const int BH = gridDim.x / nwg;
-  const int total = gridDim.x;
-  const int half = (total + 1) / 2;
-  const int pos = blockIdx.x;
-  const int rank = pos < half ? pos : total - 1 - (pos - half);
-  const int wg = nwg - 1 - rank / BH;
-  const int bk = rank - (rank / BH) * BH;
-  const int b = bk / Hkv, kvh = bk - b * Hkv;
-  const int task = wg * NW + wave;
-  const bool active = task < ntasks;
-  const int qb = task / G;
-  const int h = kvh * G + (task - qb * G);
-  const int q0 = qb * 32;
-  const int qi = q0 + n;
-  const int last_task = min(wg * NW + NW - 1, ntasks - 1);
-  const int wg_qmax = (last_task / G) * 32 + 31;
-  const int kend = (CAUSAL && MASK != 2) ? min(S, wg_qmax + 1) : S;
-  const int nkb = (kend + BN - 1) / BN;
-
-  const bf16* kbase = k + b * ks0 + kvh * ks1;
-  const bf16* vbase = v + b * vs0 + kvh * vs1;
+  // Stream-K schedule: the grid is one resident wave of workgroups, and
+  // workgroup w takes tiles [T*w/P, T*(w+1)/P) of the sequence of all
+  // (item, key tile) pairs, so every workgroup gets the same number of key
+  // tiles however uneven the causal items are.  An item that lies whole in
+  // the range is written out directly; a piece of one (a chunk) stores its
+  // (m, l, unnormalised O) in partial slot 2w (the range's first chunk) or
+  // 2w+1 (its last), for attn_merge_kernel.  The workgroup whose range holds
+  // tile 0 of a split item records it in desc[w]; desc[w].y = 0 otherwise.
+  // With per_item set, the grid has one workgroup per item instead (longest
+  // first) and nothing is split.
+  const int P = gridDim.x;
+  const bool walk = CAUSAL && MASK != 2;
+  const bool alt = per_item == 0;
+  int v_begin, v_end;
+  if (alt) {
+    v_begin = attn_range_begin(blockIdx.x, T, P);
+    v_end = attn_range_begin(blockIdx.x + 1, T, P);
+  } else {
+    const int2 r = attn_item_range<NW>(blockIdx.x, lane, nwg, BH, S, G, ntasks, walk);
+    v_begin = r.x;
+    v_end = r.y;
+  }
 
   if (DT * 32 > HD) {  // zero the padding rows of both V^T buffers once
     for (int i = tid; i < (DT * 32 - HD) * VROW; i += NT) {
@@ -119,260 +235,408 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     }
   }
 
-  // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7].
-  bf16x8_t qf[KSTEPS];
-  {
-    const bf16* qrow = q + b * qs0 + h * qs1 + static_cast<int64_t>(qi) * qs2;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (active && qi < S) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
-      qf[s] = as_bf16x8(raw);
-    }
-  }
-
-  // Retire the Q loads here: otherwise the in-order vmcnt makes the first
-  // MFMA of every iteration wait for the next tile's prefetch as well.
-  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
-
   constexpr int VTCH = (HD * (BN / 8) + NT - 1) / NT;  // V^T 16-byte chunks per thread
-  uint4 kreg[KCH];
-  uint4 vreg[VT ? VTCH : VCH][2];
-  // Global -> registers for the tile at key0.  FULL tiles (key0 + BN <= S)
-  // skip the per-row bounds tests.
-  auto fetch = [&](int key0, auto full_tag) {
-    constexpr bool FULL = decltype(full_tag)::value;
+  // Global loads go through buffer descriptors: each thread's byte offsets
+  // within a tile are fixed (computed once, 32-bit), and a tile only moves
+  // the descriptor base, in scalar registers.  num_records ends at the last
+  // valid K (or row-major V) row, so rows at or past S read as zero with no
+  // per-row test.  Chunks past the end of a tile's K rows (small HD) get an
+  // offset beyond num_records for the same effect.
+  constexpr int kRsrcFlags = 0x00020000;  // raw (untyped) access, gfx9 family
+  constexpr uint32_t kOob = 0x80000000u;
+  uint32_t koff[KCH];
 #pragma unroll
-    for (int j = 0; j < KCH; ++j) {
-      const int c = tid + NT * j;
-      const int key = c / DC, dc = c - key * DC;
-      if (FULL && (BN * DC) % NT == 0) {
-        kreg[j] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key0 + key) * ks2 + dc * 8);
+  for (int j = 0; j < KCH; ++j) {
+    const int c = tid + NT * j;
+    const int key = c / DC, dc = c - key * DC;
+    koff[j] = c < BN * DC ? static_cast<uint32_t>((key * ks2 + dc * 8) * 2) : kOob;
+  }
+  constexpr int VOFFS = VT ? VTCH : VCH;
+  uint32_t voff[VOFFS];
+#pragma unroll
+  for (int j = 0; j < VOFFS; ++j) {
+    const int c = tid + NT * j;
+    if constexpr (VT) {
+      const int d = c / (BN / 8), kc = c - d * (BN / 8);
+      voff[j] = c < HD * (BN / 8) ? static_cast<uint32_t>((d * vs2 + 8 * kc) * 2) : kOob;
+    } else {
+      const int kp = c / DC, dc = c - kp * DC;
+      voff[j] = c < (BN / 2) * DC ? static_cast<uint32_t>((2 * kp * vs2 + dc * 8) * 2) : kOob;
+    }
+  }
+  const uint32_t vrow_bytes = static_cast<uint32_t>(vs2 * 2);
+
+  bool started = false;
+  int chunk_no = 0;
+  for (int vcur = v_begin; vcur < v_end; ++chunk_no) {
+    const AttnLoc loc = attn_locate<NW>(vcur, lane, nwg, BH, S, G, ntasks, walk, alt);
+    const int wg = loc.wg, bk = loc.bk, nkb = loc.nkb;
+    const int kb0 = loc.kb, kb1 = min(nkb, kb0 + (v_end - vcur));
+    vcur += kb1 - kb0;
+    const int b = bk / Hkv, kvh = bk - b * Hkv;
+    const int task = wg * NW + wave;
+    const bool active = task < ntasks;
+    const int qb = task / G;
+    const int h = kvh * G + (task - qb * G);
+    const int q0 = qb * 32;
+    const int qi = q0 + n;
+    const bf16* kbase = k + b * ks0 + kvh * ks1;
+    const bf16* vbase = v + b * vs0 + kvh * vs1;
+
+    // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7].
+    bf16x8_t qf[KSTEPS];
+    {
+      const bf16* qrow = q + b * qs0 + h * qs1 + static_cast<int64_t>(qi) * qs2;
+  #pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (active && qi < S) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
+        qf[s] = as_bf16x8(raw);
+      }
+    }
+
+    // Retire the Q loads here: otherwise the in-order vmcnt makes the first
+    // MFMA of every iteration wait for the next tile's prefetch as well.
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+
+    uint4 kreg[KCH];
+    uint4 vreg[VT ? VTCH : VCH][2];
+    auto fetch_tile = [&](int key0) {
+      const int rows = min(BN, S - key0);  // valid keys in this tile (>= 1)
+      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<bf16*>(kbase + static_cast<int64_t>(key0) * ks2), 0,
+          static_cast<int>((rows - 1) * ks2 * 2 + HD * 2), kRsrcFlags);
+  #pragma unroll
+      for (int j = 0; j < KCH; ++j)
+        kreg[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[j], 0, 0));
+      if constexpr (VT) {
+        // Keys past S inside a d row are in memory (the next row's keys, or
+        // the row padding); stage() zeroes them.  num_records stops the last
+        // row at S.
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16*>(vbase + key0), 0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2), kRsrcFlags);
+  #pragma unroll
+        for (int j = 0; j < VTCH; ++j)
+          vreg[j][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j], 0, 0));
       } else {
-        kreg[j] = make_uint4(0, 0, 0, 0);
-        if (c < BN * DC && (FULL || key0 + key < S))
-          kreg[j] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key0 + key) * ks2 + dc * 8);
-      }
-    }
-    if constexpr (VT) {
-#pragma unroll
-      for (int j = 0; j < VTCH; ++j) {
-        const int c = tid + NT * j;
-        const int d = c / (BN / 8), kc = c - d * (BN / 8);
-        vreg[j][0] = make_uint4(0, 0, 0, 0);
-        // S % 8 == 0 on this path, so a chunk is either fully in or out
-        if (c < HD * (BN / 8) && (FULL || key0 + 8 * kc < S))
-          vreg[j][0] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(d) * vs2 + key0 + 8 * kc);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < VCH; ++j) {
-        const int u = tid + NT * j;
-        const int kp = u / DC, dc = u - kp * DC;
-        const int key = key0 + 2 * kp;
-        vreg[j][0] = make_uint4(0, 0, 0, 0);
-        vreg[j][1] = make_uint4(0, 0, 0, 0);
-        if (u < (BN / 2) * DC) {
-          if (FULL || key < S) vreg[j][0] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * vs2 + dc * 8);
-          if (FULL || key + 1 < S) vreg[j][1] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key + 1) * vs2 + dc * 8);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16*>(vbase + static_cast<int64_t>(key0) * vs2), 0,
+            static_cast<int>((rows - 1) * vs2 * 2 + HD * 2), kRsrcFlags);
+  #pragma unroll
+        for (int j = 0; j < VCH; ++j) {
+          vreg[j][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j], 0, 0));
+          vreg[j][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j] + vrow_bytes, 0, 0));
         }
       }
-    }
-  };
-  auto fetch_tile = [&](int key0) {
-    if (key0 + BN <= S) fetch(key0, std::true_type());
-    else fetch(key0, std::false_type());
-  };
-  auto stage = [&](int buf) {
-    uint16_t* kd = Ks + buf * KBUF;
-    uint16_t* vd = Vt + buf * VBUF;
-#pragma unroll
-    for (int j = 0; j < KCH; ++j) {
-      const int c = tid + NT * j;
-      const int key = c / DC, dc = c - key * DC;
-      if (c < BN * DC) *reinterpret_cast<uint4*>(&kd[key * KROW + dc * 8]) = kreg[j];
-    }
-    if constexpr (VT) {
-#pragma unroll
-      for (int j = 0; j < VTCH; ++j) {
+    };
+    auto stage = [&](int buf, int key0) {
+      uint16_t* kd = Ks + buf * KBUF;
+      uint16_t* vd = Vt + buf * VBUF;
+  #pragma unroll
+      for (int j = 0; j < KCH; ++j) {
         const int c = tid + NT * j;
-        const int d = c / (BN / 8), kc = c - d * (BN / 8);
-        if (c < HD * (BN / 8)) {
-          // VROW*2 bytes is a multiple of 8, not of 16: two 8-byte stores
-          *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc]) = make_uint2(vreg[j][0].x, vreg[j][0].y);
-          *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc + 4]) = make_uint2(vreg[j][0].z, vreg[j][0].w);
-        }
+        const int key = c / DC, dc = c - key * DC;
+        if ((BN * DC) % NT == 0 || c < BN * DC) *reinterpret_cast<uint4*>(&kd[key * KROW + dc * 8]) = kreg[j];
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < VCH; ++j) {
-        const int u = tid + NT * j;
-        const int kp = u / DC, dc = u - kp * DC;
-        if (u < (BN / 2) * DC) {
-          const uint32_t a[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
-          const uint32_t c2[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
-            const uint32_t lo = __builtin_amdgcn_perm(c2[e], a[e], 0x05040100u);
-            const uint32_t hi = __builtin_amdgcn_perm(c2[e], a[e], 0x07060302u);
-            *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
-            *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
+      if constexpr (VT) {
+        // S % 8 == 0 on this path: a chunk of 8 keys is all in or all out, and
+        // only the last tile of the sequence (a uniform branch) has chunks out.
+        if (key0 + BN > S) {
+  #pragma unroll
+          for (int j = 0; j < VTCH; ++j) {
+            const int kc = (tid + NT * j) % (BN / 8);
+            if (key0 + 8 * kc >= S) vreg[j][0] = make_uint4(0, 0, 0, 0);
+          }
+        }
+  #pragma unroll
+        for (int j = 0; j < VTCH; ++j) {
+          const int c = tid + NT * j;
+          const int d = c / (BN / 8), kc = c - d * (BN / 8);
+          if ((HD * (BN / 8)) % NT == 0 || c < HD * (BN / 8)) {
+            const uint4 x = vreg[j][0];
+            // VROW*2 bytes is a multiple of 8, not of 16: two 8-byte stores
+            *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc]) = make_uint2(x.x, x.y);
+            *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc + 4]) = make_uint2(x.z, x.w);
+          }
+        }
+      } else {
+  #pragma unroll
+        for (int j = 0; j < VCH; ++j) {
+          const int u = tid + NT * j;
+          const int kp = u / DC, dc = u - kp * DC;
+          if (((BN / 2) * DC) % NT == 0 || u < (BN / 2) * DC) {
+            const uint32_t a[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
+            const uint32_t c2[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
+              const uint32_t lo = __builtin_amdgcn_perm(c2[e], a[e], 0x05040100u);
+              const uint32_t hi = __builtin_amdgcn_perm(c2[e], a[e], 0x07060302u);
+              *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e) * VROW + 2 * kp]) = lo;
+              *reinterpret_cast<uint32_t*>(&vd[(dc * 8 + 2 * e + 1) * VROW + 2 * kp]) = hi;
+            }
           }
         }
       }
-    }
-  };
+    };
 
-  float m_i = -INFINITY, l_i = 0.f;
-  f32x16_t acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  // One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is
-  // compile-time, so the tiles that are fully visible to every wave of the
-  // workgroup run with no mask code at all.
-  auto tile = [&](int kb, auto masked_tag) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    const int buf = kb & 1;
-    const int key0 = kb * BN;
-    const uint16_t* kt = Ks + buf * KBUF;
-    const uint16_t* vt = Vt + buf * VBUF;
-    f32x16_t st[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
-        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
-      }
-    if constexpr (MASKED) {
-#pragma unroll
+    float m_i = -INFINITY, l_i = 0.f;
+    f32x16_t acc[DT];
+  #pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+
+    // One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is
+    // compile-time, so the tiles that are fully visible to every wave of the
+    // workgroup run with no mask code at all.
+    auto tile = [&](int kb, auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const int buf = kb & 1;
+      const int key0 = kb * BN;
+      const uint16_t* kt = Ks + buf * KBUF;
+      const uint16_t* vt = Vt + buf * VBUF;
+      f32x16_t st[2];
+  #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
-          bool ok = key < S;
-          if (CAUSAL && MASK != 2) ok = ok && key <= qi;
-          if (MASK != 0) {
-            const bool keep = kmask[static_cast<int64_t>(b) * S + min(key, S - 1)] != 0;
-            ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
-          }
-          st[mt][r] = ok ? st[mt][r] : -INFINITY;
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
+  #pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+  #pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
+          st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
         }
+      if constexpr (MASKED) {
+  #pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
+            bool ok = key < S;
+            if (CAUSAL && MASK != 2) ok = ok && key <= qi;
+            if (MASK != 0) {
+              const bool keep = kmask[static_cast<int64_t>(b) * S + min(key, S - 1)] != 0;
+              ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
+            }
+            st[mt][r] = ok ? st[mt][r] : -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+  #pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+      mx = halves_max(mx) * scale_log2;  // scaled row max of this tile
+      // Move the reference max only when this tile would push P past 2^8; the
+      // test is made wave-uniform so the common case is one skipped branch.
+      if (__any(mx > m_i + kRescale)) {
+        const bool move = mx > m_i + kRescale;
+        // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
+        // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
+        const float m_new = move ? mx : m_i;
+        l_i *= alpha;
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+        m_i = m_new;
+      }
+      const float m_use = m_i == -INFINITY ? 0.f : m_i;
+      // P in bf16, and its row sum from the same rounded values (v_dot2 with
+      // (1, 1)), so the normalisation uses exactly the P of the PV product.
+      uint4 pk[4];
+      float rs = 0.f;
+  #pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int mt = s2 >> 1, rb = 8 * (s2 & 1);
+        float p[8];
+  #pragma unroll
+        for (int e = 0; e < 8; ++e)
+          p[e] = __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
+        pk[s2].x = pack2<bf16>(p[0], p[1]);
+        pk[s2].y = pack2<bf16>(p[2], p[3]);
+        pk[s2].z = pack2<bf16>(p[4], p[5]);
+        pk[s2].w = pack2<bf16>(p[6], p[7]);
+        rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
+        rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
+        rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
+        rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
+      }
+      l_i += halves_sum(rs);
+      // O^T += V^T P^T over 4 k-steps of 16 keys.
+  #pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const bf16x8_t pf = as_bf16x8(pk[s2]);
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint16_t* vr = &vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+          const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
+        }
+      }
+    };
+
+
+    // Tiles [0, nfull) are in bounds and at or below the diagonal of every
+    // wave of the workgroup; the rest need the mask.
+    const int wg_qmin = ((wg * NW) / G) * 32;
+    int nfull = 0;
+    if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
+    nfull = min(nfull, nkb);
+
+    // This chunk's tiles [kb0, kb1): unmasked ones first, then masked.  The
+    // barrier that ended the previous chunk's last tile lets both LDS
+    // buffers be refilled.
+    const int nf = max(kb0, min(nfull, kb1));
+    fetch_tile(kb0 * BN);
+    stage(kb0 & 1, kb0 * BN);
+    __syncthreads();
+    // `active` is wave-uniform: branch on it rather than masking lanes.
+    const bool wave_active = __builtin_amdgcn_readfirstlane(active ? 1 : 0) != 0;
+    int kb = kb0;
+    for (; kb < nf; ++kb) {
+      if (kb + 1 < kb1) fetch_tile((kb + 1) * BN);
+      if (wave_active) tile(kb, std::false_type());
+      // The next tile goes into the other buffer, which every wave finished
+      // reading before the barrier that ended the previous iteration.
+      if (kb + 1 < kb1) stage((kb & 1) ^ 1, (kb + 1) * BN);
+      __syncthreads();
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;  // scaled row max of this tile
-    // Move the reference max only when this tile would push P past 2^8; the
-    // test is made wave-uniform so the common case is one skipped branch.
-    if (__any(mx > m_i + kRescale)) {
-      const bool move = mx > m_i + kRescale;
-      // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
-      // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
-      const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
-      const float m_new = move ? mx : m_i;
-      l_i *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-      m_i = m_new;
+    for (; kb < kb1; ++kb) {
+      if (kb + 1 < kb1) fetch_tile((kb + 1) * BN);
+      const bool live = wave_active && !(CAUSAL && MASK != 2 && kb * BN > q0 + 31);
+      if (live) tile(kb, std::true_type());
+      if (kb + 1 < kb1) stage((kb & 1) ^ 1, (kb + 1) * BN);
+      __syncthreads();
     }
-    const float m_use = m_i == -INFINITY ? 0.f : m_i;
-    // P in bf16, and its row sum from the same rounded values (v_dot2 with
-    // (1, 1)), so the normalisation uses exactly the P of the PV product.
-    uint4 pk[4];
-    float rs = 0.f;
+
+    if (kb0 == 0 && kb1 == nkb) {
+      if (wave_active && qi < S)
+        attn_store_row<HD>(o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2, acc, m_i, l_i, hf,
+                           lse ? lse + (static_cast<int64_t>(b) * Hq + h) * S + qi : nullptr);
+    } else {
+      // ws = [slot][wave][DT*4][64] partial O as 4 bf16 (uint2), then
+      // [slot][wave][64] float2 (m, l), 2P slots.  O is relative to m and
+      // bounded by l * max|v|, so bf16 keeps its range; the merge adds one
+      // bf16 rounding (2^-9 relative) to the result.
+      uint2* wacc = reinterpret_cast<uint2*>(ws);
+      float2* wml = reinterpret_cast<float2*>(ws + static_cast<int64_t>(2 * P) * NW * 64 * DT * 8);
+      const int slot = 2 * blockIdx.x + (chunk_no == 0 ? 0 : 1);
+      const int64_t sw = static_cast<int64_t>(slot) * NW + wave;
+      if (wave_active) {
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      const int mt = s2 >> 1, rb = 8 * (s2 & 1);
-      float p[8];
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        p[e] = __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
-      pk[s2].x = pack2<bf16>(p[0], p[1]);
-      pk[s2].y = pack2<bf16>(p[2], p[3]);
-      pk[s2].z = pack2<bf16>(p[4], p[5]);
-      pk[s2].w = pack2<bf16>(p[6], p[7]);
-      rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
-      rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
-      rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
-      rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
-    }
-    l_i += rs + __shfl_xor(rs, 32);
-    // O^T += V^T P^T over 4 k-steps of 16 keys.
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      const bf16x8_t pf = as_bf16x8(pk[s2]);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const uint16_t* vr = &vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
-        const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
+          for (int g4 = 0; g4 < 4; ++g4)
+            wacc[(sw * DT * 4 + dt * 4 + g4) * 64 + lane] =
+                make_uint2(pack2<bf16>(acc[dt][4 * g4], acc[dt][4 * g4 + 1]),
+                           pack2<bf16>(acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]));
+        wml[sw * 64 + lane] = make_float2(m_i, l_i);
+      }
+      if (kb0 == 0) {
+        started = true;
+        if (tid == 0) desc[blockIdx.x] = make_int4(loc.start, nkb, wg, bk);
       }
     }
-  };
-
-  // Tiles [0, nfull) are in bounds and at or below the diagonal of every
-  // wave of the workgroup; the rest need the mask.
-  const int wg_qmin = ((wg * NW) / G) * 32;
-  int nfull = 0;
-  if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
-  nfull = min(nfull, nkb);
-
-  if (nkb > 0) {
-    fetch_tile(0);
-    stage(0);
   }
-  __syncthreads();
-  int kb = 0;
-  for (; kb < nfull; ++kb) {
-    if (kb + 1 < nkb) fetch_tile((kb + 1) * BN);
-    if (active) tile(kb, std::false_type());
-    // The next tile goes into the other buffer, which every wave finished
-    // reading before the barrier that ended the previous iteration.
-    if (kb + 1 < nkb) stage((kb & 1) ^ 1);
-    __syncthreads();
-  }
-  for (; kb < nkb; ++kb) {
-    if (kb + 1 < nkb) fetch_tile((kb + 1) * BN);
-    const bool live = active && !(CAUSAL && MASK != 2 && kb * BN > q0 + 31);
-    if (live) tile(kb, std::true_type());
-    if (kb + 1 < nkb) stage((kb & 1) ^ 1);
-    __syncthreads();
-  }
+  if (!started && tid == 0) desc[blockIdx.x] = make_int4(0, 0, 0, 0);
+}
 
-  if (!active || qi >= S) return;
-  const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
+// Combines the chunks of split items.  One thread per (w, wave, lane),
+// where w is the workgroup whose range holds the item's tile 0: lane l of a
+// wave holds query l%32 and, for f = 0..DT*4-1, d = 32(f/4) + 8(f%4) +
+// 4(l/32) + 0..3 -- the MFMA accumulator layout the partials were stored
+// in.  The item's chunks are, in key order: workgroup w's last chunk (slot
+// 2w+1, or 2w if the item starts w's range), then the first chunk (slot
+// 2w') of each following workgroup w' whose range starts inside the item.
+// They are folded in that order (online max), so the result is
+// deterministic; the loads of up to four chunks are issued together.
+template <int HD, int NW>
+__global__ __launch_bounds__(256) void attn_merge_kernel(
+    const float* __restrict__ ws, const int4* __restrict__ desc, bf16* __restrict__ o,
+    float* __restrict__ lse, int P, int T, int S, int Hq, int Hkv, int G, int ntasks,
+    int64_t os0, int64_t os1, int64_t os2) {
+  constexpr int DT = (HD + 31) / 32;
+  constexpr int F = DT * 4;  // 4-element groups per lane
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int lane = gid & 63;
+  const int wave = (gid >> 6) % NW;
+  const int w = gid / (64 * NW);
+  if (w >= P) return;
+  const int4 d = desc[w];
+  // one 16-byte load: keep the compiler from splitting it across the exits
+  asm volatile("" ::"v"(d.x), "v"(d.y), "v"(d.z), "v"(d.w));
+  const int v_s = d.x, nkb = d.y, wg = d.z, bk = d.w;
+  if (nkb == 0) return;
+  const int task = wg * NW + wave;
+  if (task >= ntasks) return;
+  const int qb = task / G;
+  const int b = bk / Hkv, kvh = bk - b * Hkv;
+  const int h = kvh * G + (task - qb * G);
+  const int qi = qb * 32 + (lane & 31), hf = lane >> 5;
+  if (qi >= S) return;
+  const uint2* wacc = reinterpret_cast<const uint2*>(ws);
+  const float2* wml = reinterpret_cast<const float2*>(ws + static_cast<int64_t>(2 * P) * NW * 64 * DT * 8);
+  // Range starts floor(w'T/P) compared without a division:
+  // floor(w'T/P) < x  <=>  w'T < xP.
+  const int64_t vend_p = static_cast<int64_t>(v_s + nkb) * P;
+  int nc = 1;
+  while (w + nc < P && static_cast<int64_t>(w + nc) * T < vend_p) ++nc;
+  // the item opens w's range iff floor(wT/P) >= v_s (it cannot start before)
+  const int slot0 = static_cast<int64_t>(w) * T >= static_cast<int64_t>(v_s) * P ? 2 * w : 2 * w + 1;
+  float M = -INFINITY, L = 0.f;
+  float acc[F][4];
+#pragma unroll
+  for (int g = 0; g < F; ++g) acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.f;
+  for (int j0 = 0; j0 < nc; j0 += 4) {
+    float2 ml[4];
+    uint2 a[4][F];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u;
+      const int64_t sj = static_cast<int64_t>(j == 0 ? slot0 : 2 * (w + j)) * NW + wave;
+      ml[u] = j < nc ? wml[sj * 64 + lane] : make_float2(-INFINITY, 0.f);
+#pragma unroll
+      for (int g = 0; g < F; ++g) a[u][g] = j < nc ? wacc[(sj * F + g) * 64 + lane] : make_uint2(0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      // a chunk in which this row saw no key has m = -inf, l = 0, O = 0
+      if (ml[u].x == -INFINITY) continue;
+      const float mn = fmaxf(M, ml[u].x);
+      const float s_old = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
+      const float s_new = __builtin_amdgcn_exp2f(ml[u].x - mn);
+      M = mn;
+      L = fmaf(s_new, ml[u].y, L * s_old);
+#pragma unroll
+      for (int g = 0; g < F; ++g) {
+        acc[g][0] = fmaf(s_new, __uint_as_float(a[u][g].x << 16), acc[g][0] * s_old);
+        acc[g][1] = fmaf(s_new, __uint_as_float(a[u][g].x & 0xffff0000u), acc[g][1] * s_old);
+        acc[g][2] = fmaf(s_new, __uint_as_float(a[u][g].y << 16), acc[g][2] * s_old);
+        acc[g][3] = fmaf(s_new, __uint_as_float(a[u][g].y & 0xffff0000u), acc[g][3] * s_old);
+      }
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
   bf16* orow = o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * dt + 8 * g4 + 4 * hf;
-      if (d < HD) {
-        uint2 w;
-        w.x = pack2<bf16>(acc[dt][4 * g4 + 0] * inv, acc[dt][4 * g4 + 1] * inv);
-        w.y = pack2<bf16>(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + d) = w;
-      }
+  for (int g = 0; g < F; ++g) {
+    const int dcol = 32 * (g >> 2) + 8 * (g & 3) + 4 * hf;
+    if (dcol < HD) {
+      uint2 w2;
+      w2.x = pack2<bf16>(acc[g][0] * inv, acc[g][1] * inv);
+      w2.y = pack2<bf16>(acc[g][2] * inv, acc[g][3] * inv);
+      *reinterpret_cast<uint2*>(orow + dcol) = w2;
     }
-  if (lse && hf == 0) {
-    lse[(static_cast<int64_t>(b) * Hq + h) * S + qi] =
-        l_i > 0.f ? (m_i + __log2f(l_i)) * kLn2 : -INFINITY;
   }
+  if (lse && hf == 0)
+    lse[(static_cast<int64_t>(b) * Hq + h) * S + qi] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
 }
 
 // ---- generic path ---------------------------------------------------------
@@ -424,59 +688,170 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
   if (lse) lse[gid] = l > 0.f ? m + logf(l) : -INFINITY;
 }
 
+// Split-chunk workspace (chunk partials and the merge descriptors), one per
+// device, owned by the library.  It only grows; a buffer it outgrows is kept
+// (never freed), so a HIP graph captured with it stays valid.  Calls that
+// split and run concurrently on one device (different streams) would share
+// it and must not overlap.
+struct AttnWorkspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+static std::mutex g_ws_mu;
+static AttnWorkspace g_ws[64];
+
+static int attn_workspace(size_t bytes, hipStream_t st, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(HYDRA_ERR_LAUNCH, "attn_fwd: no current device");
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  AttnWorkspace& w = g_ws[dev];
+  if (w.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(HYDRA_ERR_UNSUPPORTED,
+                  "attn_fwd: the split workspace must grow, which cannot happen under graph "
+                  "capture; run the same shape once before capturing");
+    const size_t nb = std::max(bytes, 2 * w.bytes);
+    void* p = nullptr;
+    if (hipMalloc(&p, nb) != hipSuccess) return fail(HYDRA_ERR_LAUNCH, "attn_fwd: workspace allocation failed");
+    w.ptr = p;
+    w.bytes = nb;
+  }
+  *out = w.ptr;
+  return HYDRA_OK;
+}
+
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Resident workgroups per CU of a kernel (cached per kernel), from its
+// register and LDS footprint: a SIMD holds 512 VGPRs per lane (allocated in
+// granules of 8) and at most 8 waves, a CU 4 SIMDs and 160 KiB of LDS.
+static int blocks_per_cu(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<const void*, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(kernel);
+  if (it != cache.end()) return it->second;
+  hipFuncAttributes a{};
+  int nb = 1;
+  if (hipFuncGetAttributes(&a, kernel) == hipSuccess) {
+    const int regs = std::max(8, (a.numRegs + 7) / 8 * 8);
+    const int waves_per_simd = std::min(8, 512 / regs);
+    const int waves_per_wg = (threads + 63) / 64;
+    int by_regs = waves_per_simd * 4 / waves_per_wg;
+    const size_t lds = a.sharedSizeBytes;
+    const int by_lds = lds > 0 ? static_cast<int>((160 * 1024) / lds) : by_regs;
+    nb = std::max(1, std::min(by_regs, by_lds));
+  }
+  if (const char* e = getenv("HYDRA_ATTN_DEBUG"))
+    if (atoi(e)) fprintf(stderr, "attn_fwd: %d resident workgroups per CU (regs %d, lds %zu)\n", nb, a.numRegs, a.sharedSizeBytes);
+  cache[kernel] = nb;
+  return nb;
+}
+
 template <int HD>
 static int launch_mfma(const void* q, const void* k, const void* v, void* o, float* lse,
                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t S, const int64_t* qs, const int64_t* ks,
                        const int64_t* vs, const int64_t* os, bool causal, float scale,
                        hipStream_t st) {
+  constexpr int NW = 4;  // waves per workgroup; GQA heads share each staged K/V tile
+  constexpr int DT = (HD + 31) / 32;
   // V with unit stride along the keys is read as V^T rows (vs[3] apart).
   const bool vt = vs[2] == 1 && vs[3] != 1;
   const int G = static_cast<int>(Hq / Hkv);
   const int nqb = static_cast<int>((S + 31) / 32);
   const int ntasks = G * nqb;
-  // Four-wave workgroups share each staged K/V tile between four query
-  // blocks; two-wave ones (HYDRA_ATTN_NW=2) halve that reuse and measured
-  // slower even where they double the workgroup count.
-  int nw = 4;
-  if (const char* e = getenv("HYDRA_ATTN_NW")) nw = atoi(e) == 2 ? 2 : 4;
-  const int nwg = (ntasks + nw - 1) / nw;
-  const dim3 grid(static_cast<unsigned>(nwg * B * Hkv));
+  const int nwg = (ntasks + NW - 1) / NW;
+  const int BH = static_cast<int>(B * Hkv);
+  const int iS = static_cast<int>(S);
+  // The reference-SDPA mask mode opens keys above the diagonal, so it walks
+  // every key tile (no causal tile skipping).
+  const bool walk = causal && mask_mode != HYDRA_MASK_REFERENCE_SDPA;
+  int64_t T64 = 0;
+  for (int w = 0; w < nwg; ++w) T64 += attn_tiles<NW>(w, iS, G, ntasks, walk);
+  T64 *= BH;
+  if (T64 >= (int64_t(1) << 31)) return fail(HYDRA_ERR_ARG, "attn_fwd: too many key tiles");
+  const int T = static_cast<int>(T64);
+
   const float sl2 = scale * kLog2e;
   auto Q = static_cast<const bf16*>(q);
   auto K = static_cast<const bf16*>(k);
   auto V = static_cast<const bf16*>(v);
   auto O = static_cast<bf16*>(o);
-  auto go = [&](auto c_tag, auto m_tag, auto nw_tag) {
+  auto go = [&](auto c_tag, auto m_tag) -> int {
     constexpr bool C = decltype(c_tag)::value;
     constexpr int M = decltype(m_tag)::value;
-    constexpr int NW = decltype(nw_tag)::value;
-    if (vt)
-      attn_fwd_mfma_kernel<HD, C, M, true, NW><<<grid, 64 * NW, 0, st>>>(
-          Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, nwg, qs[0], qs[1],
-          qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[3], os[0], os[1], os[2], sl2);
-    else
-      attn_fwd_mfma_kernel<HD, C, M, false, NW><<<grid, 64 * NW, 0, st>>>(
-          Q, K, V, O, lse, kmask, (int)S, (int)Hq, (int)Hkv, G, ntasks, nwg, qs[0], qs[1],
-          qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], sl2);
-  };
-  auto by_nw = [&](auto c_tag, auto m_tag) {
-    if (nw == 2) go(c_tag, m_tag, std::integral_constant<int, 2>());
-    else go(c_tag, m_tag, std::integral_constant<int, 4>());
+    auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW> : attn_fwd_mfma_kernel<HD, C, M, false, NW>;
+    // Schedule.  With at least two items per resident workgroup slot, one
+    // workgroup per item (longest first) lets the dispatcher balance the
+    // load; with fewer, stream-K: one resident wave of workgroups, each with
+    // an equal share of the key tiles.  HYDRA_ATTN_WGS=n forces stream-K on
+    // n workgroups, HYDRA_ATTN_WGS=0 one workgroup per item.
+    const int64_t slots = static_cast<int64_t>(device_cus()) *
+                          blocks_per_cu(reinterpret_cast<const void*>(kern), 64 * NW);
+    const int64_t items = static_cast<int64_t>(nwg) * BH;
+    int64_t P64 = slots;
+    bool per_item = items >= 2 * slots;
+    if (const char* e = getenv("HYDRA_ATTN_WGS")) {
+      const int64_t x = atoll(e);
+      per_item = x == 0;
+      if (x > 0) P64 = x;
+    }
+    if (per_item) P64 = items;
+    const int P = static_cast<int>(std::min<int64_t>(P64, T));
+    // Does any item straddle two ranges (then the merge kernel runs)?
+    auto range_of = [&](int64_t t) { return ((t + 1) * P + T - 1) / T - 1; };
+    bool split = false;
+    int64_t vpos = 0;
+    for (int p = 0; p < nwg && !split && !per_item; ++p) {
+      const int nt = attn_tiles<NW>(attn_pos_item(p, nwg, true), iS, G, ntasks, walk);
+      for (int bk = 0; bk < BH; ++bk, vpos += nt)
+        if (range_of(vpos) != range_of(vpos + nt - 1)) {
+          split = true;
+          break;
+        }
+    }
+    float* part = nullptr;
+    int4* desc = nullptr;
+    // partial slots (stream-K only), then the merge descriptors
+    const size_t pb = per_item ? 0 : static_cast<size_t>(2 * P) * NW * 64 * (DT * 8 + 2) * sizeof(float);
+    void* w = nullptr;
+    const int rc = attn_workspace(pb + static_cast<size_t>(P) * sizeof(int4), st, &w);
+    if (rc != HYDRA_OK) return rc;
+    part = static_cast<float*>(w);
+    desc = reinterpret_cast<int4*>(static_cast<char*>(w) + pb);
+    kern<<<dim3(static_cast<unsigned>(P)), 64 * NW, 0, st>>>(
+        Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, T, per_item ? 1 : 0, part, desc,
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2);
+    const int rc1 = check_launch("attn_fwd_mfma_kernel");
+    if (rc1 != HYDRA_OK || !split) return rc1;
+    const int64_t threads = static_cast<int64_t>(P) * NW * 64;
+    attn_merge_kernel<HD, NW><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
+        part, desc, O, lse, P, T, iS, (int)Hq, (int)Hkv, G, ntasks, os[0], os[1], os[2]);
+    return check_launch("attn_merge_kernel");
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
   using M0 = std::integral_constant<int, 0>;
   using M1 = std::integral_constant<int, 1>;
   using M2 = std::integral_constant<int, 2>;
-  // The reference-SDPA mask mode opens keys above the diagonal, so it walks
-  // every key tile (no causal tile skipping).
-  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) by_nw(F_(), M2());
-  else if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) by_nw(T_(), M1());
-  else if (causal) by_nw(T_(), M0());
-  else if (mask_mode == HYDRA_MASK_KEY_PADDING) by_nw(F_(), M1());
-  else by_nw(F_(), M0());
-  return check_launch("attn_fwd_mfma_kernel");
+  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) return go(F_(), M2());
+  if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) return go(T_(), M1());
+  if (causal) return go(T_(), M0());
+  if (mask_mode == HYDRA_MASK_KEY_PADDING) return go(F_(), M1());
+  return go(F_(), M0());
 }
 
 template <typename T>
@@ -531,18 +906,22 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   if (B * S == 0) return HYDRA_OK;
   HYDRA_REQUIRE(q && k && v && o, "attn_fwd: null pointer");
   HYDRA_REQUIRE(S < (int64_t(1) << 30), "attn_fwd: sequence too long");
-  HYDRA_REQUIRE(B * Hkv * ((Hq / Hkv) * ((S + 31) / 32) + 3) / 4 < (int64_t(1) << 31),
-                "attn_fwd: too many workgroups");
   const uint8_t* km = mask_mode == HYDRA_MASK_NONE ? nullptr : key_mask;
   auto st = static_cast<hipStream_t>(stream);
   const bool mfma_shape = (hd == 16 || hd == 32 || hd == 64 || hd == 128);
   bool strides8 = true;
   for (int i = 0; i < 3; ++i)
     strides8 = strides8 && qs[i] % 8 == 0 && ks[i] % 8 == 0 && os[i] % 4 == 0;
+  // The bf16 kernel addresses a K/V tile with 32-bit byte offsets from a
+  // per-tile base, and relies on rows that do not overlap.
+  const int64_t lim = int64_t(1) << 30;
+  strides8 = strides8 && ks[2] >= hd && ks[2] * 2 * 64 < lim;
   if (vs[3] == 1) {
-    strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[2] % 8 == 0;
+    strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[2] % 8 == 0 && vs[2] >= hd &&
+               vs[2] * 2 * 64 < lim;
   } else {  // V^T rows: 16-byte chunks of 8 keys, so S must be a multiple of 8
-    strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[3] % 8 == 0 && S % 8 == 0;
+    strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[3] % 8 == 0 && S % 8 == 0 &&
+               vs[3] >= S && hd * vs[3] * 2 < lim;
   }
   if (dtype == HYDRA_BF16 && mfma_shape && strides8 && aligned16(q) && aligned16(k) &&
       aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0) {

@@ -175,3 +175,72 @@ def test_attention_v_transposed_odd_length_generic(cuda):
     out, _ = attention_forward(q.to(cuda, torch.bfloat16), k.to(cuda, torch.bfloat16),
                                vt.transpose(2, 3), causal=True)
     assert max_rel_err(out.cpu(), occ.attention(q, k, v, causal=True)) < 2e-2
+
+
+SPLIT_CASES = [
+    # B, Hq, Hkv, S, hd, causal, mask mode
+    ((2, 8, 2, 512, 16), True, "none"),
+    ((1, 4, 1, 1000, 64), True, "key_padding"),
+    ((2, 4, 4, 300, 32), False, "none"),
+    ((1, 8, 1, 257, 128), True, "none"),
+    ((2, 4, 2, 200, 64), True, "reference"),
+    ((1, 2, 1, 700, 64), False, "key_padding"),
+]
+
+
+@pytest.mark.parametrize("wgs", ["0", "3", "7", "64", "509"])
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[f"{c[0]}-{c[1]}-{c[2]}" for c in SPLIT_CASES])
+def test_attention_split_chunks(cuda, monkeypatch, case, wgs):
+    """The bf16 kernel shares the key tiles of all items equally among
+    `wgs` workgroups (stream-K), so items are cut at arbitrary tiles and
+    merged by a second kernel; wgs=0 runs one workgroup per item.  Every
+    schedule gives the oracle's result, the LSE of the unsplit run (one
+    workgroup), and identical bits on a repeated call."""
+    from hydra_amd.attention.backends.ccgqa.ops import (MASK_KEY_PADDING, MASK_NONE,
+                                                        MASK_REFERENCE_SDPA, attention_forward)
+
+    (B, Hq, Hkv, S, hd), causal, mode = case
+    q, k, v = _qkv(B, Hq, Hkv, S, hd, seed=S + hd)
+    mask = None
+    mm = {"none": MASK_NONE, "key_padding": MASK_KEY_PADDING, "reference": MASK_REFERENCE_SDPA}[mode]
+    if mode != "none":
+        g = torch.Generator().manual_seed(S)
+        mask = (torch.rand(B, S, generator=g) > 0.25).long()
+        mask[:, 0] = 1
+        mask[0, 1:70] = 0  # a run of padding longer than one tile
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    kw = dict(causal=causal, key_mask=None if mask is None else mask.to(cuda), mask_mode=mm, want_lse=True)
+    monkeypatch.setenv("HYDRA_ATTN_WGS", "1")  # one range: no item is split
+    whole, whole_lse = attention_forward(dev(q), dev(k), dev(v), **kw)
+    monkeypatch.setenv("HYDRA_ATTN_WGS", wgs)
+    out, lse = attention_forward(dev(q), dev(k), dev(v), **kw)
+    out2, lse2 = attention_forward(dev(q), dev(k), dev(v), **kw)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    if mode == "key_padding":
+        ref = occ.attention_bruteforce(q, k, v, causal=causal, mask=mask)
+    else:
+        ref = occ.attention(q, k, v, causal=causal, mask=mask)
+    assert max_rel_err(out.cpu(), ref) < 2e-2
+    assert max_rel_err(whole.cpu(), ref) < 2e-2
+    assert max_rel_err(out.cpu(), whole.float().cpu()) < 2e-2
+    fin = torch.isfinite(whole_lse)
+    assert torch.equal(fin, torch.isfinite(lse))
+    # P is rounded to bf16 against a per-chunk running max, so the row sums
+    # agree to the bf16 rounding bound: |d log l| <= 2^-8.
+    assert (lse[fin] - whole_lse[fin]).abs().max().item() < 2 ** -8
+
+
+def test_attention_split_fully_masked_rows(cuda, monkeypatch):
+    """Rows that see no key in any chunk come out as zeros with LSE -inf."""
+    from hydra_amd.attention.backends.ccgqa.ops import MASK_KEY_PADDING, attention_forward
+
+    monkeypatch.setenv("HYDRA_ATTN_WGS", "5")
+    q, k, v = _qkv(1, 4, 1, 400, 64, seed=16)
+    mask = torch.ones(1, 400, dtype=torch.long)
+    mask[0, :150] = 0  # queries 0..149 see no key; later rows span several chunks
+    out, lse = attention_forward(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), causal=True,
+                                 key_mask=mask.to(cuda), mask_mode=MASK_KEY_PADDING, want_lse=True)
+    assert torch.count_nonzero(out[:, :, :150].cpu()) == 0
+    assert torch.isinf(lse[:, :, :150].cpu()).all()
+    ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
+    assert max_rel_err(out[:, :, 150:].cpu(), ref[:, :, 150:]) < 2e-2
