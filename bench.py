@@ -350,7 +350,7 @@ def main():
         "roofline": {"kernel": "attn_fwd_mfma_kernel<64,causal> + attn_merge_kernel<64>", "bound": "mfma",
                      "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS,
-                     "traffic": measured_traffic("attn_fwd_mfma_kernel<64,true,0>"),
+                     "traffic": measured_traffic("attention_op<64,causal>"),
                      "flops_per_launch": fl["core"], "avg_ms": attn_ms},
         "stages_ms": stages,
         "module_tflops": fl["total"] / (ms_step * 1e-3) / 1e12,

@@ -7,24 +7,25 @@
 // 341-429).
 //
 // bf16 path (attn_fwd_mfma_kernel): v_mfma_f32_32x32x16_bf16.
-//  * A workgroup is NW waves (4, or 2 when that is needed to give the
-//    dispatcher enough workgroups to balance the causal triangle) that share
-//    one (batch, kv-head) and one staged K/V tile in LDS; wave w takes task
-//    NW*wg+w, task t -> (32-row query block t/G, query head kvh*G + t%G), so
-//    GQA heads reuse the same K/V tile.
+//  * A workgroup is 4 waves that share one (batch, kv-head) and one staged
+//    K/V tile in LDS; an item is 4 query tasks, task t -> (32-row query
+//    block t/G, query head kvh*G + t%G), so GQA heads reuse the same tile.
 //  * Scores are computed transposed, S^T = K Q^T, so lane l owns query
 //    (l%32) and the online softmax needs no cross-lane traffic except one
-//    swap between the two half-waves.
+//    swap between the two half-waves (v_permlane32_swap).
 //  * O^T = V^T P^T: the bf16 P fragment is taken straight from the score
-//    accumulator registers; V is transposed while it is staged into LDS.
+//    accumulator registers; V is transposed while it is staged into LDS,
+//    or read as V^T rows when the caller stores it keys-contiguous.
 //  * Softmax runs in the exp2 domain with fp32 statistics; the scale is
 //    folded into one FMA per score, and the running max (with the O
 //    rescale it implies) only moves when a tile's max exceeds it by 2^8.
-//  * K/V tiles are double-buffered in LDS: one barrier per key tile, the
-//    global loads of tile j+1 are in flight while tile j is computed.
-//  * Causal: the grid runs the longest query blocks first (with the second
-//    half of the grid in reverse, so co-resident workgroups balance), blocks
-//    above the diagonal are skipped, only diagonal tiles evaluate the mask.
+//  * K/V tiles are buffer-loaded and double-buffered in LDS: one barrier
+//    per key tile, the loads of tile j+1 in flight while tile j computes.
+//  * Causal: tiles above an item's last query are skipped, only tiles that
+//    cross the diagonal evaluate the mask.
+//  * Schedule: stream-K (equal key-tile ranges over one resident wave of
+//    workgroups, split items folded by attn_merge_kernel) when items are
+//    few, else one workgroup per item, longest first.
 // Generic path (attn_fwd_generic_kernel): one thread per query row, fp32
 // math, any element type, even head_dim <= 256.
 #include "common.h"
