@@ -68,13 +68,17 @@ class C3Step:
         self.x = x.to(dev, torch.bfloat16)
         from hydra_amd.attention.backends.ccgqa.ops import prep_flags
 
-        from hydra_amd._lib import CCGQA_V_TRANSPOSED
+        from hydra_amd._lib import CCGQA_V_TRANSPOSED, CCGQA_W_TILED
+        from hydra_amd.attention.backends.ccgqa.ops import tiled_weights_ok
 
         self.flags = prep_flags(True, True, True, True, True) | CCGQA_V_TRANSPOSED
         mm = self.m
+        tiled = tiled_weights_ok(n_heads, n_kv_heads, mm.head_dim, torch.bfloat16)
+        if tiled:
+            self.flags |= CCGQA_W_TILED
         self.convw = mm._packed_conv_weights((mm.q_conv.conv1.weight, mm.q_conv.conv2.weight,
                                               mm.k_conv.conv1.weight, mm.k_conv.conv2.weight),
-                                             torch.bfloat16)
+                                             torch.bfloat16, tiled)
         self.cos = mm.cos_cached[0, 0, :S].float().contiguous()
         self.sin = mm.sin_cached[0, 0, :S].float().contiguous()
         self.out = torch.empty(B, S, mm.latent_dim, dtype=torch.bfloat16, device=dev)

@@ -22,6 +22,7 @@ OK, ERR_ARG, ERR_LAUNCH, ERR_UNSUPPORTED = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
 CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_VALUE_SHIFT, CCGQA_QK_NORM, CCGQA_ROPE = 1, 2, 4, 8, 16
 CCGQA_V_TRANSPOSED = 32
+CCGQA_W_TILED = 64
 MASK_NONE, MASK_KEY_PADDING, MASK_REFERENCE_SDPA = 0, 1, 2
 SCATTER_ADD, SCATTER_REPLACE = 0, 1
 
@@ -43,6 +44,7 @@ SIGNATURES = {
                              _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_attn_fwd": [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64,
                        _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
+    "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
     "hydra_mod_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P],
     "hydra_mod_gather": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_mod_scatter": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
@@ -95,6 +97,11 @@ def call(name: str, *args) -> None:
         if rc == ERR_ARG:
             raise ValueError(f"{name}: {msg}")
         raise HydraError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name: str, *args) -> int:
+    """Call an entry point that returns a value rather than a status."""
+    return int(getattr(load(), name)(*args))
 
 
 def dtype_code(t: torch.Tensor) -> int:

@@ -27,9 +27,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ...._autograd import track
-from ...._lib import CCGQA_V_TRANSPOSED, MASK_KEY_PADDING, MASK_REFERENCE_SDPA
+from ...._lib import CCGQA_V_TRANSPOSED, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_REFERENCE_SDPA
 from .kernels.fused_conv import OptimizedConvSequence
-from .ops import attention_forward, ccgqa_prep, pack_conv_weight, prep_flags
+from .ops import attention_forward, ccgqa_prep, pack_conv_weight, prep_flags, tiled_weights_ok
 
 # Kept for callers that probe these names (attention.py:13-28).
 FUSED_KERNELS_AVAILABLE = True
@@ -116,8 +116,11 @@ class CCGQAAttention(nn.Module):
         convw = ((self.q_conv.conv1.weight, self.q_conv.conv2.weight,
                   self.k_conv.conv1.weight, self.k_conv.conv2.weight)
                  if self.use_convs else ())
+        tiled = self.use_convs and tiled_weights_ok(self.n_heads, self.n_kv_heads, self.head_dim, x.dtype)
+        if tiled:
+            flags |= CCGQA_W_TILED  # conv weights in MFMA-fragment order
         with torch.no_grad():
-            packed = self._packed_conv_weights(convw, x.dtype) if self.use_convs else (None,) * 4
+            packed = self._packed_conv_weights(convw, x.dtype, tiled) if self.use_convs else (None,) * 4
             q, k, v = ccgqa_prep(
                 qkv.detach(), self.n_heads, self.n_kv_heads, self.head_dim, flags, *packed,
                 temperature=self.key_temperature if self.use_qk_norm else None,
@@ -134,13 +137,14 @@ class CCGQAAttention(nn.Module):
             out = out * self.output_scale
         return out
 
-    def _packed_conv_weights(self, convw, dtype):
-        """Tap-major copies of the four conv weights in `dtype`, rebuilt only
-        when a weight changes (tensor version counter) or moves."""
-        key = tuple((w.data_ptr(), w._version, w.device, dtype) for w in convw)
+    def _packed_conv_weights(self, convw, dtype, tiled=False):
+        """Packed copies (tap-major, or MFMA-tiled) of the four conv weights in
+        `dtype`, rebuilt only when a weight changes (tensor version counter)
+        or moves."""
+        key = tuple((w.data_ptr(), w._version, w.device, dtype, tiled) for w in convw)
         cache = getattr(self, "_packed_cache", None)
         if cache is None or cache[0] != key:
-            cache = (key, tuple(pack_conv_weight(w, dtype) for w in convw))
+            cache = (key, tuple(pack_conv_weight(w, dtype, tiled) for w in convw))
             self._packed_cache = cache
         return cache[1]
 

@@ -8,7 +8,7 @@ from typing import Optional
 import torch
 
 from ...._lib import (CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_QK_NORM, CCGQA_ROPE,
-                      CCGQA_V_TRANSPOSED, CCGQA_VALUE_SHIFT, MASK_KEY_PADDING, MASK_NONE,
+                      CCGQA_V_TRANSPOSED, CCGQA_VALUE_SHIFT, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_NONE,
                       MASK_REFERENCE_SDPA)
 from .... import _lib
 
@@ -20,10 +20,25 @@ def prep_flags(use_convs: bool, use_qk_mean: bool, use_value_shift: bool,
             | (CCGQA_QK_NORM if use_qk_norm else 0) | (CCGQA_ROPE if use_rope else 0))
 
 
-def pack_conv_weight(w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+def pack_conv_weight(w: torch.Tensor, dtype: torch.dtype, tiled: bool = False) -> torch.Tensor:
     """Conv1d weight [out, in/groups, k] -> the tap-major [k, out, in/groups]
-    layout the prep kernel reads."""
-    return w.detach().to(dtype).permute(2, 0, 1).contiguous()
+    layout the prep kernel reads, or with `tiled` its MFMA-fragment order
+    [k, out/32, in/16, 2, 32, 8] (CCGQA_W_TILED): element (t, o/32, i/16,
+    (i/8)%2, o%32, i%8), so one 32x16 operand block is contiguous."""
+    t = w.detach().to(dtype).permute(2, 0, 1)
+    if not tiled:
+        return t.contiguous()
+    k, O, I = t.shape
+    return t.reshape(k, O // 32, 32, I // 16, 2, 8).permute(0, 1, 3, 4, 2, 5).contiguous()
+
+
+def tiled_weights_ok(n_heads: int, n_kv_heads: int, head_dim: int, dtype: torch.dtype) -> bool:
+    """Whether the prep kernel takes its MFMA path for this head layout and
+    dtype, i.e. accepts CCGQA_W_TILED weights."""
+    if dtype not in _lib._DTYPE_CODE:
+        return False
+    return _lib.query("hydra_ccgqa_prep_tiled_ok", n_heads, n_kv_heads, head_dim,
+                      _lib._DTYPE_CODE[dtype]) == 1
 
 
 def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, flags: int,
@@ -31,7 +46,8 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
                packed: bool = False):
     """q [B,Hq,S,hd], k/v [B,Hkv,S,hd] from the fused projection qkv [B,S,L+2K]
     (CCGQAAttention.forward, attention.py:205-266).  Conv weights are in
-    PyTorch Conv1d layout, or already tap-major when packed=True.  With
+    PyTorch Conv1d layout, or already packed (pack_conv_weight, tiled when
+    CCGQA_W_TILED is in flags) when packed=True.  With
     CCGQA_V_TRANSPOSED in flags, v is returned as a [B,Hkv,S,hd] view of a
     [B,Hkv,hd,S] buffer (the layout the attention kernel stages directly)."""
     _lib.require_gpu("ccgqa_prep", qkv, wq1, wq2, wk1, wk2, temperature, cos, sin)
@@ -44,11 +60,14 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
     dt = qkv.dtype
     if flags & CCGQA_CONVS:
         ws = (wq1, wq2, wk1, wk2)
+        tiled = bool(flags & CCGQA_W_TILED)
         if packed:
             ws = tuple(w.to(dt).contiguous() for w in ws)
         else:
-            ws = tuple(pack_conv_weight(w, dt) for w in ws)
+            ws = tuple(pack_conv_weight(w, dt, tiled) for w in ws)
         exp = [(3, L, head_dim), (3, L, L), (3, K, head_dim), (3, K, K)]
+        if tiled:
+            exp = [(3, o // 32, i // 16, 2, 32, 8) for _, o, i in exp]
         for w, e in zip(ws, exp):
             if tuple(w.shape) != e:
                 raise ValueError(f"ccgqa_prep: packed conv weight shape {tuple(w.shape)} != {e}")

@@ -138,19 +138,6 @@ __host__ __device__ __forceinline__ int attn_range_begin(int w, int T, int P) {
   return static_cast<int>(static_cast<int64_t>(w) * T / P);
 }
 
-// x combined with its copy in the other half of the wave (lane l ^ 32),
-// through v_permlane32_swap: a = (x[0..31], x[0..31]), b = (x[32..63],
-// x[32..63]), so max(a, b) and a + b hold the pair's max and sum in every
-// lane (both halves get the same bits: + is commutative).
-__device__ __forceinline__ float halves_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float halves_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Writes one query row of O (bf16) from the MFMA accumulator layout, with
 // the softmax normaliser 1/l, and its log-sum-exp (m is in log2 units).
 template <int HD>

@@ -38,6 +38,16 @@ __device__ __forceinline__ float rnd(float v) {
   return to_f32(from_f32<T>(v));
 }
 
+// Eight values rounded to bf16 in place, two per v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void rnd8(float* v) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t p = pack2<bf16>(v[e], v[e + 1]);
+    v[e] = __uint_as_float(p << 16);
+    v[e + 1] = __uint_as_float(p & 0xffff0000u);
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
     const T* __restrict__ qkv, int64_t qkv_rs, const T* __restrict__ wq1,
@@ -199,16 +209,18 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
 // bf16 MFMA variant.
 //
 // LDS (bf16, rows padded by 8 elements): X = qkv q|k columns of tokens
-// [s0-4, s0+TT), Y1 = conv1 output of tokens [s0-2, s0+TT), Y2 = conv2 output
-// of tokens [s0, s0+TT).  Both convs are computed transposed,
+// [s0-4, s0+TT), Y1 = conv1 output of tokens [s0-2, s0+TT), and the RoPE
+// cos/sin rows of the tile (fp32).  Both convs are computed transposed,
 //   Y^T[o, s] = sum_t sum_c W[t][o][c] * In[s + t - 2, c],
-// as 32(out channels) x 32(tokens) tiles: A = weights straight from global
-// (L2-resident, 16-byte loads along c), B = token rows from LDS (16 bytes
-// along c), so lane l owns token l%32 of the tile.  A task is one 32-channel
-// m-tile times all TT/32 token tiles, so each A fragment feeds TT/32 MFMAs.
-// The two halo rows of Y1 (tokens s0-2, s0-1) are computed on the VALU.
-// The epilogue (QK-mean, L2-norm, temperature, RoPE) uses HD/8 lanes per
-// (token, head) row and 16-byte vectors.
+// as 32(out channels) x 32(tokens) MFMA tiles: A = weights straight from
+// global (L2-resident, 16-byte loads along c, a ring of loads in flight),
+// B = token rows from LDS (16 bytes along c), so lane l owns token l%32.
+// A task is one 32-channel m-tile times every token tile (conv1: of the
+// TT+2 rows conv2 needs), so each weight fragment is read once per
+// workgroup and feeds TT/32 (+1) MFMAs; the tasks of both convs are spread
+// over all 8 waves.  conv2's output, rounded to bf16, goes to LDS, and the
+// epilogue (QK-mean, L2-norm with temperature, RoPE) runs on all threads
+// with 8 channels per lane.
 // ===========================================================================
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_p;
 typedef __attribute__((ext_vector_type(16))) float f32x16_p;
@@ -228,12 +240,50 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
 // One MFMA conv task: the 32 output channels of the m-tile (weight rows
 // from wbase, lane row n, k half hf) times all NT token tiles, over 3 taps x
 // CS k-steps of 16 input channels.  A (weights) streams from L2, B (token
-// rows) from LDS at bbase + brow(j, t); row pointers are formed once per tap
-// and the channel loop only adds immediates.
+// rows) from LDS at bbase + brow(j, t).  With CS known at compile time the
+// 3*CS steps are unrolled and the A fragments run through a ring of D
+// registers, so D L2 loads stay in flight behind the MFMAs; otherwise a
+// plain loop.
+template <int NT, int CS, typename BRow>
+__device__ __forceinline__ void conv_task_fixed(const bf16* wbase, int64_t wtap, int wstep,
+                                                const uint16_t* bbase, BRow brow,
+                                                f32x16_p (&acc)[NT]) {
+  constexpr int NSTEP = 3 * CS;
+  constexpr int D = NSTEP < 12 ? NSTEP : 12;  // A steps in flight
+  bf16x8_p ring[D];
+  bf16x8_p bq[2][NT];  // B fragments of this step and the next
+  auto aptr = [&](int st) { return wbase + (st / CS) * wtap + wstep * (st % CS); };
+  auto bload = [&](int st, bf16x8_p* dst) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) dst[j] = ld_bf16x8(bbase + brow(j, st / CS) + 16 * (st % CS));
+  };
+#pragma unroll
+  for (int i = 0; i < D; ++i) ring[i] = ld_bf16x8(aptr(i));
+  bload(0, bq[0]);
+#pragma unroll
+  for (int st = 0; st < NSTEP; ++st) {
+    const bf16x8_p a = ring[st % D];
+    if (st + 1 < NSTEP) bload(st + 1, bq[(st + 1) & 1]);
+    if (st + D < NSTEP) ring[st % D] = ld_bf16x8(aptr(st + D));
+    // Keep the scheduler from sinking the loads next to their use: they
+    // hide L2 and LDS latency only if they really are in flight.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[st & 1][j], acc[j], 0, 0, 0);
+  }
+}
+
 template <int NT, typename BRow>
-__device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int CS,
+__device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int wstep, int CS,
                                           const uint16_t* bbase, BRow brow,
                                           f32x16_p (&acc)[NT]) {
+  switch (CS) {  // CS is uniform: a scalar branch
+    case 2: return conv_task_fixed<NT, 2>(wbase, wtap, wstep, bbase, brow, acc);
+    case 4: return conv_task_fixed<NT, 4>(wbase, wtap, wstep, bbase, brow, acc);
+    case 8: return conv_task_fixed<NT, 8>(wbase, wtap, wstep, bbase, brow, acc);
+    default: break;
+  }
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
     const bf16* wt = wbase + t * wtap;
@@ -242,7 +292,7 @@ __device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int C
     for (int j = 0; j < NT; ++j) bt[j] = bbase + brow(j, t);
 #pragma unroll 8
     for (int c = 0; c < CS; ++c) {
-      const bf16x8_p a = ld_bf16x8(wt + 16 * c);
+      const bf16x8_p a = ld_bf16x8(wt + wstep * c);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const bf16x8_p bb = ld_bf16x8(bt[j] + 16 * c);
@@ -250,6 +300,73 @@ __device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int C
       }
     }
   }
+}
+
+// One conv2 task: the MT m-tiles (32 output channels each) of one head times
+// NG 32-token tiles.  Each step's MT A fragments (weights) and NG B fragments
+// (token rows from LDS, row 32g + n + t for tap t) feed MT x NG MFMAs; A runs
+// through a ring of D steps of loads in flight, B one step ahead.
+template <int MT, int NG, int CS>
+__device__ __forceinline__ void conv2_task_fixed(const bf16* wrow, int64_t wtap, int64_t wmt,
+                                                 int wstep, const uint16_t* brow0, int rs,
+                                                 f32x16_p (&acc)[MT][NG]) {
+  constexpr int NSTEP = 3 * CS;
+  constexpr int DW = (MT * NG >= 8 ? 8 : 16) / MT;  // A steps in flight
+  constexpr int D = NSTEP < DW ? NSTEP : (DW > 0 ? DW : 1);
+  bf16x8_p ring[D][MT];
+  bf16x8_p bq[2][NG];
+  auto aptr = [&](int st, int m) { return wrow + (st / CS) * wtap + m * wmt + wstep * (st % CS); };
+  auto bload = [&](int st, bf16x8_p* dst) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) dst[g] = ld_bf16x8(brow0 + (32 * g + st / CS) * rs + 16 * (st % CS));
+  };
+#pragma unroll
+  for (int i = 0; i < D; ++i)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) ring[i][m] = ld_bf16x8(aptr(i, m));
+  bload(0, bq[0]);
+#pragma unroll
+  for (int st = 0; st < NSTEP; ++st) {
+    bf16x8_p a[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) a[m] = ring[st % D][m];
+    if (st + 1 < NSTEP) bload(st + 1, bq[(st + 1) & 1]);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if (st + D < NSTEP) ring[st % D][m] = ld_bf16x8(aptr(st + D, m));
+    // Keep the scheduler from sinking the loads next to their use: they
+    // hide L2 and LDS latency only if they really are in flight.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+        acc[m][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[m], bq[st & 1][g], acc[m][g], 0, 0, 0);
+  }
+}
+
+template <int MT, int NG>
+__device__ __forceinline__ void conv2_task(const bf16* wrow, int64_t wtap, int64_t wmt, int wstep,
+                                           int CS, const uint16_t* brow0, int rs,
+                                           f32x16_p (&acc)[MT][NG]) {
+  switch (CS) {  // uniform
+    case 2: return conv2_task_fixed<MT, NG, 2>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+    case 4: return conv2_task_fixed<MT, NG, 4>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+    case 8: return conv2_task_fixed<MT, NG, 8>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+    case 16: return conv2_task_fixed<MT, NG, 16>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+    default: break;
+  }
+  for (int t = 0; t < 3; ++t)
+    for (int c = 0; c < CS; ++c) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const bf16x8_p bb = ld_bf16x8(brow0 + (32 * g + t) * rs + 16 * c);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          acc[m][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              ld_bf16x8(wrow + t * wtap + m * wmt + wstep * c), bb, acc[m][g], 0, 0, 0);
+      }
+    }
 }
 
 // 8 waves: two per SIMD, so one wave's VALU work and L2 latency overlap
@@ -264,13 +381,25 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
     int64_t cs_rs, bf16* __restrict__ qo, bf16* __restrict__ ko, bf16* __restrict__ vo, int S,
     int Hq, int Hkv, int flags) {
   constexpr int NT = TT / 32;  // token tiles
-  constexpr int LPR = HD / 8;  // epilogue lanes per (token, head) row
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   uint16_t* sm = reinterpret_cast<uint16_t*>(smem_raw);
   const int L = Hq * HD, K = Hkv * HD, CW = L + K, RS = CW + 8;
+  const int G = Hq / Hkv;
+  // QK-mean terms per token: one per head when G == 1 ((q0_h + k0_h) / 2),
+  // else one for the q heads (mean of the k heads) and one for the k heads.
+  const int NQA = G == 1 ? Hq : 2;
   uint16_t* X = sm;                   // row r <-> token s0 - 4 + r
   uint16_t* Y1 = X + (TT + 4) * RS;   // row r <-> token s0 - 2 + r
-  uint16_t* Y2 = Y1 + (TT + 2) * RS;  // row r <-> token s0 + r
+  // RoPE cos | sin of the tile's tokens, fp32 [TT][CSR] each; rows padded
+  // by 2 floats so the 32 tokens of a half-wave read distinct banks.
+  constexpr int CSR = HD / 2 + 2;
+  float* CSl = reinterpret_cast<float*>(Y1 + (TT + 2) * RS);
+  float* SNl = CSl + TT * CSR;
+  uint16_t* QA = reinterpret_cast<uint16_t*>(SNl + TT * CSR);  // bf16 [TT][NQA][HD]
+  // v columns of tokens [s0-1, s0+TT), row r <-> token s0 - 1 + r (the
+  // value shift reads the previous token), rows padded by 8 elements
+  const int VR = K + 8;
+  uint16_t* Vs = QA + TT * NQA * HD;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, hf = lane >> 5;
   const int b = blockIdx.y;
@@ -280,9 +409,14 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
   const bool vshift = flags & HYDRA_CCGQA_VALUE_SHIFT;
   const bool qk_norm = flags & HYDRA_CCGQA_QK_NORM;
   const bool rope = flags & HYDRA_CCGQA_ROPE;
+  // Weight layout: tap-major rows ([3][O][I], a fragment is 32 rows x 32
+  // bytes) or MFMA-tiled ([3][O/32][I/16][64 lanes][8], a fragment is one
+  // contiguous 1 KB block).  Both have tap stride O*I and m-tile stride 32*I.
+  const bool tiled = flags & HYDRA_CCGQA_W_TILED;
+  const int wstep = tiled ? 512 : 16;  // elements between k-steps
   const bf16* xb = qkv + static_cast<int64_t>(b) * S * qkv_rs;
 
-  // ---- stage q0|k0 rows --------------------------------------------------
+  // ---- stage q0|k0 rows, RoPE angles ---------------------------------------
   const int cw8 = CW / 8;
   for (int i = tid; i < (TT + 4) * cw8; i += kPrepThreads) {
     const int r = i / cw8, c = (i - r * cw8) * 8;
@@ -291,213 +425,253 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
     if (s >= 0 && s < S) v = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + c);
     *reinterpret_cast<uint4*>(X + r * RS + c) = v;
   }
+  for (int i = tid; i < (TT + 1) * (K / 8); i += kPrepThreads) {
+    const int r = i / (K / 8), c = (i - r * (K / 8)) * 8;
+    const int s = s0 - 1 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (s >= 0 && s < S) v = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + c);
+    *reinterpret_cast<uint4*>(Vs + r * VR + c) = v;
+  }
+  if (rope) {
+    constexpr int Q4 = HD / 8;  // float4 chunks per cos (or sin) row
+    for (int i = tid; i < 2 * TT * Q4; i += kPrepThreads) {
+      const int which = i / (TT * Q4), rem = i - which * (TT * Q4);
+      const int r = rem / Q4, c4 = (rem - r * Q4) * 4;
+      const int s = s0 + r;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (s < S) v = *reinterpret_cast<const float4*>((which ? sn : cs) + static_cast<int64_t>(s) * cs_rs + c4);
+      float* d = (which ? SNl : CSl) + r * CSR + c4;  // 8-byte aligned rows
+      *reinterpret_cast<float2*>(d) = make_float2(v.x, v.y);
+      *reinterpret_cast<float2*>(d + 2) = make_float2(v.z, v.w);
+    }
+  }
   __syncthreads();
 
-  if (convs) {
-    // ---- conv1 halo rows (tokens s0-2, s0-1) on the VALU -------------------
-    for (int i = tid; i < 2 * CW; i += kPrepThreads) {
-      const int r = i / CW, o = i - r * CW;
-      const int s = s0 - 2 + r;
-      float acc = 0.f;
-      if (s >= 0) {
-        const bool is_q = o < L;
-        const int oo = is_q ? o : o - L;
-        const int O = is_q ? L : K;
-        const int col0 = (is_q ? 0 : L) + (oo / HD) * HD;
-        const bf16* w1 = is_q ? wq1 : wk1;
-        for (int t = 0; t < 3; ++t) {
-          const bf16* wr = w1 + (static_cast<int64_t>(t) * O + oo) * HD;
-          const uint16_t* xr = X + (r + t) * RS + col0;
-#pragma unroll 4
-          for (int c = 0; c < HD; c += 8) {
-            const uint4 wv = *reinterpret_cast<const uint4*>(wr + c);
-            const uint4 xv = *reinterpret_cast<const uint4*>(xr + c);
-            acc = dot2_bf16(wv.x, xv.x, acc);
-            acc = dot2_bf16(wv.y, xv.y, acc);
-            acc = dot2_bf16(wv.z, xv.z, acc);
-            acc = dot2_bf16(wv.w, xv.w, acc);
+  // ---- side work: QK-mean terms into QA, and v (value shift) to global ----
+  // Shared by the waves [hw0, 8); they run it while the others still have
+  // MFMA tasks, so it stays off the critical path.
+  auto side_work = [&](int hw0) {
+    const int hl = (wave - hw0) * 64 + lane, nhl = (kPrepThreads / 64 - hw0) * 64;
+    if (qk_mean) {
+      constexpr int C8 = HD / 8;
+      for (int it = hl; it < TT * NQA * C8; it += nhl) {
+        const int r = it / (NQA * C8), rem = it - r * (NQA * C8);
+        const int q = rem / C8, c8 = (rem - q * C8) * 8;
+        const bf16* x0 = reinterpret_cast<const bf16*>(X + (r + 4) * RS);
+        float add[8];
+        if (G == 1) {
+          float a[8], c[8];
+          load16<bf16>(x0 + q * HD + c8, a);
+          load16<bf16>(x0 + L + q * HD + c8, c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(a[e] + c[e]));
+        } else {
+          // term 0 (for q heads): mean of the k heads; term 1: of the q heads
+          const int nh = q ? Hq : Hkv;
+          const bf16* src = x0 + (q ? 0 : L) + c8;
+          float sum[8];
+          load16<bf16>(src, sum);
+          for (int hx = 1; hx < nh; ++hx) {
+            float a[8];
+            load16<bf16>(src + hx * HD, a);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum[e] += a[e];
           }
+          const float inv = 1.f / static_cast<float>(nh);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(sum[e] * inv));
+        }
+        store16<bf16>(reinterpret_cast<bf16*>(QA + (r * NQA + q) * HD + c8), add);
+      }
+    }
+    // v from the staged rows: channels of the second half take the previous
+    // token with the value shift (row r of token s, row r+1 otherwise)
+    if (flags & HYDRA_CCGQA_V_TRANSPOSED) {
+      // v^T [B, Hkv, hd, S]: 8 consecutive tokens of one channel per
+      // 16-byte store
+      for (int i = hl; i < K * (TT / 8); i += nhl) {
+        const int c = i / (TT / 8), t8 = (i - c * (TT / 8)) * 8;
+        const int dr = (vshift && c >= K / 2) ? 0 : 1;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = static_cast<uint32_t>(Vs[(t8 + 2 * e + dr) * VR + c]) |
+                 (static_cast<uint32_t>(Vs[(t8 + 2 * e + 1 + dr) * VR + c]) << 16);
+        if (s0 + t8 < S) {
+          const int j = c / HD, d = c - j * HD;
+          *reinterpret_cast<uint4*>(vo + ((static_cast<int64_t>(b) * Hkv + j) * HD + d) * S + s0 + t8) =
+              make_uint4(w[0], w[1], w[2], w[3]);
         }
       }
-      Y1[r * RS + o] = from_f32<bf16>(acc).bits;
+    } else {
+      const int k8 = K / 8;
+      for (int i = hl; i < TT * k8; i += nhl) {
+        const int r = i / k8, c = (i - r * k8) * 8;
+        const int s = s0 + r;
+        if (s >= S) continue;
+        const int dr = (vshift && c >= K / 2) ? 0 : 1;
+        const uint4 val = *reinterpret_cast<const uint4*>(Vs + (r + dr) * VR + c);
+        const int j = c / HD, d = c - j * HD;
+        *reinterpret_cast<uint4*>(vo + ((static_cast<int64_t>(b) * Hkv + j) * S + s) * HD + d) = val;
+      }
     }
-    // ---- conv1 main rows on MFMA ---------------------------------------------
-    for (int mt = wave; mt < CW / 32; mt += kPrepThreads / 64) {
+  };
+
+  if (convs) {
+    // ---- conv1 on MFMA ------------------------------------------------------
+    // Output row i in [0, TT+2) <-> token s0-2+i reads X rows i..i+2.  The
+    // rows are covered by NT+1 token tiles; the last holds the two rows past
+    // TT (its other lanes read clamped rows and are discarded).  Rows of
+    // tokens < 0 come out 0 (their X rows are 0): conv2's causal padding.
+    constexpr int NT1 = NT + 1;
+    const int nm1 = CW / 32;
+    for (int mt = wave; mt < nm1; mt += kPrepThreads / 64) {
       const int o0 = 32 * mt;
       const bool is_q = o0 < L;
       const int oo0 = is_q ? o0 : o0 - L;
       const int O = is_q ? L : K;
       const int cbase = (is_q ? 0 : L) + (oo0 / HD) * HD;
-      const bf16* wbase = (is_q ? wq1 : wk1) + static_cast<int64_t>(oo0 + n) * HD + 8 * hf;
-      f32x16_p acc[NT];
+      const bf16* wbase = (is_q ? wq1 : wk1) + static_cast<int64_t>(oo0) * HD +
+                          (tiled ? 8 * lane : n * HD + 8 * hf);
+      f32x16_p acc[NT1];
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-      // output token s0+32j+n, tap t reads token s0+32j+n+t-2 = X row 32j+n+2+t
-      conv_task<NT>(wbase, static_cast<int64_t>(O) * HD, HD / 16, X + cbase + 8 * hf,
-                       [&](int j, int t) { return (32 * j + n + 2 + t) * RS; }, acc);
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          uint2 w;
-          w.x = pack2<bf16>(acc[j][4 * g4 + 0], acc[j][4 * g4 + 1]);
-          w.y = pack2<bf16>(acc[j][4 * g4 + 2], acc[j][4 * g4 + 3]);
-          *reinterpret_cast<uint2*>(Y1 + (2 + 32 * j + n) * RS + o0 + 8 * g4 + 4 * hf) = w;
-        }
-    }
-    __syncthreads();
-    // ---- conv2 on MFMA -------------------------------------------------------
-    for (int mt = wave; mt < CW / 32; mt += kPrepThreads / 64) {
-      const int o0 = 32 * mt;
-      const bool is_q = o0 < L;
-      const int oo0 = is_q ? o0 : o0 - L;
-      const int C = is_q ? L : K;
-      const int cbase = is_q ? 0 : L;
-      const bf16* wbase = (is_q ? wq2 : wk2) + static_cast<int64_t>(oo0 + n) * C + 8 * hf;
-      f32x16_p acc[NT];
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
+      for (int j = 0; j < NT1; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-      // output token s0+32j+n, tap t reads token s0+32j+n+t-2 = Y1 row 32j+n+t
-      conv_task<NT>(wbase, static_cast<int64_t>(C) * C, C / 16, Y1 + cbase + 8 * hf,
-                       [&](int j, int t) { return (32 * j + n + t) * RS; }, acc);
+      conv_task<NT1>(wbase, static_cast<int64_t>(O) * HD, wstep, HD / 16, X + cbase + 8 * hf,
+                     [&](int j, int t) { return min(32 * j + n + t, TT + 3) * RS; }, acc);
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+      for (int j = 0; j < NT1; ++j) {
+        const int i = 32 * j + n;
+        if (j < NT || i < TT + 2) {
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          uint2 w;
-          w.x = pack2<bf16>(acc[j][4 * g4 + 0], acc[j][4 * g4 + 1]);
-          w.y = pack2<bf16>(acc[j][4 * g4 + 2], acc[j][4 * g4 + 3]);
-          *reinterpret_cast<uint2*>(Y2 + (32 * j + n) * RS + o0 + 8 * g4 + 4 * hf) = w;
+          for (int g4 = 0; g4 < 4; ++g4) {
+            uint2 w;
+            w.x = pack2<bf16>(acc[j][4 * g4 + 0], acc[j][4 * g4 + 1]);
+            w.y = pack2<bf16>(acc[j][4 * g4 + 2], acc[j][4 * g4 + 3]);
+            *reinterpret_cast<uint2*>(Y1 + i * RS + o0 + 8 * g4 + 4 * hf) = w;
+          }
         }
+      }
     }
+    // waves with one m-tile fewer take the side work
+    const int extra = nm1 % (kPrepThreads / 64);
+    const int hw0 = extra == 0 ? 0 : extra;
+    if (wave >= hw0) side_work(hw0);
   } else {
-    for (int i = tid; i < TT * cw8; i += kPrepThreads) {
-      const int r = i / cw8, c = (i - r * cw8) * 8;
-      *reinterpret_cast<uint4*>(Y2 + r * RS + c) = *reinterpret_cast<const uint4*>(X + (r + 4) * RS + c);
-    }
+    side_work(0);
   }
   __syncthreads();
 
+  // ---- conv2 on MFMA: one head (HD/32 m-tiles) x all token tiles per task,
+  // so each weight fragment is read once per workgroup and each token-row
+  // fragment feeds HD/32 MFMAs.  Output token s0+32j+n, tap t reads Y1 row
+  // 32j+n+t.  Rounded to bf16 into Y2, which reuses X's rows (conv1 and the
+  // side work are done with X).  Without convs, Y2 is X's rows 4.. as is.
+  uint16_t* Y2 = convs ? X : X + 4 * RS;  // row r <-> token s0 + r
+  if (convs) {
+    constexpr int MT = HD / 32;
+    for (int hh = wave; hh < Hq + Hkv; hh += kPrepThreads / 64) {
+      const bool is_k = hh >= Hq;
+      const int head = is_k ? hh - Hq : hh;
+      const int C = is_k ? K : L;
+      f32x16_p acc[MT][NT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[m][j][r] = 0.f;
+      conv2_task<MT, NT>((is_k ? wk2 : wq2) + static_cast<int64_t>(head * HD) * C +
+                             (tiled ? 8 * lane : n * C + 8 * hf),
+                         static_cast<int64_t>(C) * C, static_cast<int64_t>(32) * C, wstep, C / 16,
+                         Y1 + n * RS + (is_k ? L : 0) + 8 * hf, RS, acc);
+      const int o0 = (is_k ? L : 0) + head * HD;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            uint2 w;
+            w.x = pack2<bf16>(acc[m][j][4 * g4 + 0], acc[m][j][4 * g4 + 1]);
+            w.y = pack2<bf16>(acc[m][j][4 * g4 + 2], acc[m][j][4 * g4 + 3]);
+            *reinterpret_cast<uint2*>(Y2 + (32 * j + n) * RS + o0 + 32 * m + 8 * g4 + 4 * hf) = w;
+          }
+    }
+    __syncthreads();
+  }
+
   // ---- epilogue: QK-mean, L2-norm (+temperature), RoPE, store -------------
-  // The reference divides by the (bf16) norm; here that is one fp32 division
-  // per row and a multiply per element, then the same bf16 roundings.
-  const int G = Hq / Hkv;
+  // HD/8 lanes per (token, head) row, 8 channels each; a wave covers 8 rows,
+  // i.e. the heads of consecutive tokens, so RoPE angles are shared reads
+  // and every row leaves as one contiguous 2*HD-byte store.  Roundings
+  // follow the reference: the QK-mean sum, the norm, the normalised vector,
+  // the temperature product (conv2 output and QK-mean terms are bf16).
+  constexpr int LPR = HD / 8;
   const float tval = (qk_norm && temp) ? to_f32(temp[0]) : 1.f;
-  const float inv_hq = 1.f / static_cast<float>(Hq), inv_hkv = 1.f / static_cast<float>(Hkv);
   const int nheads = Hq + Hkv;
   const int rows = TT * nheads;
   for (int base = 0; base < rows * LPR; base += kPrepThreads) {
     const int i = base + tid;
     const bool live = i < rows * LPR;
-    const int row = i / LPR, c8 = (i % LPR) * 8;
+    const int row = live ? i / LPR : 0, c8 = (i % LPR) * 8;
     const int r = row / nheads, hh = row - r * nheads;
     const int s = s0 + r;
     const bool is_k = hh >= Hq;
     const int head = is_k ? hh - Hq : hh;
-    const int col0 = (is_k ? L : 0) + head * HD;
     float v[8];
-    float ss = 0.f;
-    if (live) {
-      load16<bf16>(reinterpret_cast<const bf16*>(Y2 + r * RS + col0 + c8), v);
-      if (qk_mean) {
-        const bf16* x0 = reinterpret_cast<const bf16*>(X + (r + 4) * RS);
-        float add[8];
-        if (G == 1) {
-          float a[8], c[8];
-          load16<bf16>(x0 + head * HD + c8, a);
-          load16<bf16>(x0 + L + head * HD + c8, c);
+    load16<bf16>(reinterpret_cast<const bf16*>(Y2 + r * RS + (is_k ? L : 0) + head * HD + c8), v);
+    if (qk_mean) {
+      float add[8];
+      const int q = G == 1 ? head : (is_k ? 1 : 0);
+      load16<bf16>(reinterpret_cast<const bf16*>(QA + (r * NQA + q) * HD + c8), add);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(a[e] + c[e]));
-        } else {
-          // k heads take the mean of the q heads, q heads the mean of the k heads
-          const int nh = is_k ? Hq : Hkv;
-          const bf16* src = x0 + (is_k ? 0 : L) + c8;
-          float acc[8];
-          load16<bf16>(src, acc);
-          for (int hx = 1; hx < nh; ++hx) {
-            float a[8];
-            load16<bf16>(src + hx * HD, a);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += a[e];
-          }
-          const float inv = is_k ? inv_hq : inv_hkv;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(acc[e] * inv));
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = rnd<bf16>(v[e] + add[e]);
-      }
+      for (int e = 0; e < 8; ++e) v[e] += add[e];
+      rnd8(v);
+    }
+    if (qk_norm) {
+      float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-    }
-    ss = wave_sum<LPR>(ss);
-    if (!live || s >= S) continue;
-    if (qk_norm) {
+      ss = wave_sum<LPR>(ss);
       const float rinv = 1.f / fmaxf(rnd<bf16>(__builtin_sqrtf(ss)), 1e-12f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v[e] = rnd<bf16>(v[e] * rinv);
-        if (is_k) v[e] = rnd<bf16>(v[e] * tval);
+      for (int e = 0; e < 8; ++e) v[e] *= rinv;
+      rnd8(v);
+      if (is_k) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] *= tval;
+        rnd8(v);
       }
     }
     if (rope) {
-      const float4 cv = *reinterpret_cast<const float4*>(cs + static_cast<int64_t>(s) * cs_rs + c8 / 2);
-      const float4 sv = *reinterpret_cast<const float4*>(sn + static_cast<int64_t>(s) * cs_rs + c8 / 2);
-      const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
-      const float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+      const float* cr = CSl + r * CSR + c8 / 2;
+      const float* sr = SNl + r * CSR + c8 / 2;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const float x1 = v[2 * p], x2 = v[2 * p + 1];
-        v[2 * p] = x1 * cc[p] - x2 * sc[p];
-        v[2 * p + 1] = x1 * sc[p] + x2 * cc[p];
+      for (int p2 = 0; p2 < 2; ++p2) {
+        const float2 cv = *reinterpret_cast<const float2*>(cr + 2 * p2);
+        const float2 sv = *reinterpret_cast<const float2*>(sr + 2 * p2);
+        const float x0 = v[4 * p2 + 0], x1 = v[4 * p2 + 1], x2 = v[4 * p2 + 2], x3 = v[4 * p2 + 3];
+        v[4 * p2 + 0] = x0 * cv.x - x1 * sv.x;
+        v[4 * p2 + 1] = x0 * sv.x + x1 * cv.x;
+        v[4 * p2 + 2] = x2 * cv.y - x3 * sv.y;
+        v[4 * p2 + 3] = x2 * sv.y + x3 * cv.y;
       }
     }
-    bf16* dst = (is_k ? ko : qo) +
-                ((static_cast<int64_t>(b) * (is_k ? Hkv : Hq) + head) * S + s) * HD + c8;
-    store16<bf16>(dst, v);
+    if (live && s < S) {
+      bf16* dst = (is_k ? ko : qo) +
+                  ((static_cast<int64_t>(b) * (is_k ? Hkv : Hq) + head) * S + s) * HD + c8;
+      store16<bf16>(dst, v);
+    }
   }
+}
 
-  // ---- v (value shift) ----------------------------------------------------
-  const int k8 = K / 8;
-  if (flags & HYDRA_CCGQA_V_TRANSPOSED) {
-    // v^T [B, Hkv, hd, S]: each item packs 8 consecutive tokens of one channel
-    // into one 16-byte store (tokens come from the L2-resident qkv rows).
-    for (int i = tid; i < K * (TT / 8); i += kPrepThreads) {
-      const int c = i / (TT / 8), t8 = (i - c * (TT / 8)) * 8;
-      const bool prev = vshift && c >= K / 2;
-      float vals[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int s = s0 + t8 + e;
-        const int src = prev ? s - 1 : s;
-        vals[e] = (s < S && src >= 0)
-                      ? to_f32(xb[static_cast<int64_t>(src) * qkv_rs + L + K + c])
-                      : 0.f;
-      }
-      if (s0 + t8 < S) {
-        const int j = c / HD, d = c - j * HD;
-        store16<bf16>(vo + ((static_cast<int64_t>(b) * Hkv + j) * HD + d) * S + s0 + t8, vals);
-      }
-    }
-  } else {
-    for (int i = tid; i < TT * k8; i += kPrepThreads) {
-      const int r = i / k8, c = (i - r * k8) * 8;
-      const int s = s0 + r;
-      if (s >= S) continue;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (vshift && c >= K / 2) {
-        if (s > 0) val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s - 1) * qkv_rs + L + K + c);
-      } else {
-        val = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + c);
-      }
-      const int j = c / HD, d = c - j * HD;
-      *reinterpret_cast<uint4*>(vo + ((static_cast<int64_t>(b) * Hkv + j) * S + s) * HD + d) = val;
-    }
-  }
+static size_t prep_mfma_lds(int64_t Hq, int64_t Hkv, int64_t hd, int TT) {
+  const int64_t RS = (Hq + Hkv) * hd + 8;
+  const int64_t nqa = Hq == Hkv ? Hq : 2;  // QK-mean terms per token
+  return static_cast<size_t>(2 * TT + 6) * RS * 2 + static_cast<size_t>(TT) * (hd + 4) * 4 +
+         static_cast<size_t>(TT) * nqa * hd * 2 + static_cast<size_t>(TT + 1) * (Hkv * hd + 8) * 2;
 }
 
 template <int HD>
@@ -506,8 +680,7 @@ static int launch_prep_mfma(const void* qkv, int64_t qkv_rs, const void* wq1, co
                             const float* sn, int64_t cs_rs, void* qo, void* ko, void* vo,
                             int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int flags,
                             size_t max_lds, hipStream_t st) {
-  const int64_t RS = (Hq + Hkv) * HD + 8;
-  auto lds_for = [&](int TT) { return static_cast<size_t>(3 * TT + 6) * RS * 2; };
+  auto lds_for = [&](int TT) { return prep_mfma_lds(Hq, Hkv, HD, TT); };
   auto go = [&](auto tt_tag) -> int {
     constexpr int TT = decltype(tt_tag)::value;
     const size_t lds = lds_for(TT);
@@ -558,6 +731,15 @@ static int launch_prep_generic(const void* qkv, int64_t qkv_rs, const void* wq1,
 
 using namespace hydra;
 
+extern "C" int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype) {
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
+  if (dtype != HYDRA_BF16 || !(hd == 32 || hd == 64 || hd == 128)) return 0;
+  int dev = 0, max_lds = 65536;
+  if (hipGetDevice(&dev) == hipSuccess)
+    hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  return prep_mfma_lds(Hq, Hkv, hd, 32) <= static_cast<size_t>(max_lds) ? 1 : 0;
+}
+
 extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void* wq1,
                                     const void* wq2, const void* wk1, const void* wk2,
                                     const void* temp, const float* cos, const float* sin,
@@ -567,7 +749,7 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 2, "ccgqa_prep: bad size");
   HYDRA_REQUIRE(Hq % Hkv == 0, "ccgqa_prep: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(hd % 2 == 0, "ccgqa_prep: head_dim must be even");
-  HYDRA_REQUIRE((flags & ~63) == 0, "ccgqa_prep: unknown flag bits");
+  HYDRA_REQUIRE((flags & ~127) == 0, "ccgqa_prep: unknown flag bits");
   const int64_t L = Hq * hd, K = Hkv * hd;
   HYDRA_REQUIRE(!(flags & HYDRA_CCGQA_VALUE_SHIFT) || K % 2 == 0,
                 "ccgqa_prep: kv_dim must be even for the value shift");
@@ -603,6 +785,10 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
     }
     if (rc >= 0) return rc;
   }
+  if (flags & HYDRA_CCGQA_W_TILED)
+    return fail(HYDRA_ERR_UNSUPPORTED,
+                "ccgqa_prep: MFMA-tiled conv weights need the MFMA path (bf16, head_dim 32/64/128, "
+                "16-byte aligned pointers, S % 8 == 0 with V_TRANSPOSED)");
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     return launch_prep_generic<T>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs,
                                   q_out, k_out, v_out, B, S, Hq, Hkv, hd, flags, st);

@@ -137,6 +137,19 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// x combined with its copy in the other half of the wave (lane l ^ 32),
+// through v_permlane32_swap: a = (x[0..31], x[0..31]), b = (x[32..63],
+// x[32..63]), so max(a, b) and a + b hold the pair's max and sum in every
+// lane (both halves get the same bits: + is commutative).
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---- host-side error plumbing -------------------------------------------
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);

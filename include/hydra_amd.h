@@ -91,6 +91,7 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
 #define HYDRA_CCGQA_QK_NORM     8
 #define HYDRA_CCGQA_ROPE        16
 #define HYDRA_CCGQA_V_TRANSPOSED 32 /* write v as [B, Hkv, hd, S] */
+#define HYDRA_CCGQA_W_TILED     64  /* conv weights in MFMA-fragment order (below) */
 
 /* Everything of CCGQAAttention.forward between the qkv GEMM and the attention
  * core, in one pass over token tiles: split of the fused projection, value
@@ -106,6 +107,10 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
  *       PyTorch's [out, in/groups, 3] permuted (2, 0, 1):
  *       wq1 [3][L][hd], wq2 [3][L][L], wk1 [3][K][hd], wk2 [3][K][K]
  *       (unused and may be NULL without HYDRA_CCGQA_CONVS).
+ *       With HYDRA_CCGQA_W_TILED each tap-major weight [3][O][I] is instead
+ *       given as [3][O/32][I/16][2][32][8]: element (t, o/32, i/16, (i/8)%2,
+ *       o%32, i%8), so one 32x16 MFMA operand block is 1 KB contiguous; only
+ *       the MFMA path reads it (HYDRA_ERR_UNSUPPORTED otherwise).
  * temp: key temperature, 1 element of `dtype` (NULL without QK_NORM).
  * cos/sin: fp32 [S, hd/2] row stride cs_rs (NULL without ROPE).
  * q_out: [B, Hq, S, hd]; k_out: [B, Hkv, S, hd]; v_out: [B, Hkv, S, hd], or
@@ -121,6 +126,13 @@ int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
                          void* q_out, void* k_out, void* v_out,
                          int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
                          int64_t hd, int flags, int dtype, void* stream);
+
+/* 1 when hydra_ccgqa_prep_fwd takes its MFMA path for these heads and
+ * dtype on the current device (given 16-byte aligned pointers and, with
+ * V_TRANSPOSED, S % 8 == 0), i.e. when HYDRA_CCGQA_W_TILED weights are
+ * accepted; 0 otherwise.  No counterpart in the reference: it tells the
+ * host which conv-weight layout to pack. */
+int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype);
 
 /* Key-mask modes of hydra_attn_fwd (key_mask: uint8 [B,S], nonzero = keep).
  * KEY_PADDING: key t is visible to query s iff key_mask[b,t] != 0 (and t <= s

@@ -65,6 +65,11 @@ def test_abi_version_and_error_path():
                   st, st, st, st, 1, ctypes.c_float(0.25), 1, None)
     with pytest.raises(ValueError, match="unknown flag"):
         _lib.call("hydra_ccgqa_prep_fwd", None, 48, None, None, None, None, None, None, None, 0,
-                  None, None, None, 1, 4, 2, 1, 16, 64, 1, None)
+                  None, None, None, 1, 4, 2, 1, 16, 128, 1, None)
+    # the tiled conv-weight layout is offered for bf16 MFMA head dims only
+    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 64, _lib.BF16) == 1
+    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 64, _lib.F32) == 0
+    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 48, _lib.BF16) == 0
+    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 3, 64, _lib.BF16) == 0
     # empty work is a no-op success
     _lib.call("hydra_swiglu_fwd", None, None, None, 0, 8, 8, 8, 8, 1, None)

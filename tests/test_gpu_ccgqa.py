@@ -45,6 +45,10 @@ PREP_CASES = [
     dict(dim=256, n_heads=4, n_kv_heads=2, compression_factor=4, B=1, S=9, use_convs=False),
     dict(dim=256, n_heads=4, n_kv_heads=2, compression_factor=4, B=1, S=40, use_qk_norm=False,
          use_rope=False, use_value_shift=False, use_qk_mean=False),
+    # head_dim 128 on the MFMA path (4 m-tiles per head), GQA 2
+    dict(dim=2048, n_heads=4, n_kv_heads=2, compression_factor=4, B=1, S=200),
+    # head_dim 32, one q head per kv head (QK-mean (q0 + k0) / 2), no convs
+    dict(dim=512, n_heads=4, n_kv_heads=4, compression_factor=4, B=2, S=96, use_convs=False),
 ]
 
 
@@ -85,6 +89,17 @@ def test_prep_kernel(cuda, case, dtype):
         assert v2.stride(-2) == 1
         assert torch.equal(v2.cpu(), v.cpu())
         assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(k2.cpu(), k.cpu())
+    # MFMA-tiled conv weights: the same operands in a different memory order
+    from hydra_amd._lib import CCGQA_W_TILED
+    from hydra_amd.attention.backends.ccgqa.ops import tiled_weights_ok
+
+    if cfg.use_convs and tiled_weights_ok(cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, dtype):
+        q3, k3, v3 = ccgqa_prep(qkv.to(cuda), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                flags | CCGQA_W_TILED, *[w.to(cuda) for w in conv],
+                                temperature=params["key_temperature"].to(cuda),
+                                cos=cos.to(cuda), sin=sin.to(cuda))
+        assert torch.equal(q3.cpu(), q.cpu()) and torch.equal(k3.cpu(), k.cpu())
+        assert torch.equal(v3.cpu(), v.cpu())
 
 
 def _bench_case(dim, n_heads, n_kv_heads, B, S, dtype, temperature, seed):
