@@ -67,8 +67,9 @@ def test_abi_version_and_error_path():
         _lib.call("hydra_ccgqa_prep_fwd", None, 48, None, None, None, None, None, None, None, 0,
                   None, None, None, 1, 4, 2, 1, 16, 128, 1, None)
     # the tiled conv-weight layout is offered for bf16 MFMA head dims only
-    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 64, _lib.BF16) == 1
-    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 64, _lib.F32) == 0
+    # (a layout small enough for the 64 KB LDS assumed without a device)
+    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 32, _lib.BF16) == 1
+    assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 32, _lib.F32) == 0
     assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 48, _lib.BF16) == 0
     assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 3, 64, _lib.BF16) == 0
     # empty work is a no-op success
