@@ -138,6 +138,12 @@ __host__ __device__ __forceinline__ int attn_range_begin(int w, int T, int P) {
   return static_cast<int>(static_cast<int64_t>(w) * T / P);
 }
 
+// Buffer load of 16 bytes per lane straight into LDS: lane l's bytes land
+// at lds + 16*l (lds must be wave-uniform), whatever its global offset.
+__device__ __forceinline__ void load16_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
 // Writes one query row of O (bf16) from the MFMA accumulator layout, with
 // the softmax normaliser 1/l, and its log-sum-exp (m is in log2 units).
 template <int HD>
@@ -176,13 +182,21 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   constexpr int BN = kAttnBN;           // keys per tile
   constexpr int KSTEPS = HD / 16;       // k-steps of S^T = K Q^T
   constexpr int DT = (HD + 31) / 32;    // 32-row d tiles of O^T
-  constexpr int KROW = HD + 8;          // padded LDS row of K (elements)
-  constexpr int VROW = BN + 4;          // padded LDS row of V^T (elements)
+  // LDS rows are padded by one 16-byte slot (8 elements) so that the MFMA
+  // operand reads of 16 consecutive rows hit distinct banks.  K (and V^T
+  // when V comes keys-contiguous) is loaded straight into LDS: a wave's
+  // buffer load writes 64 consecutive slots, one per lane, and the lanes
+  // that land on a pad slot load nothing (an offset past num_records).
   constexpr int DC = HD / 8;            // 16-byte chunks per K/V row
+  constexpr int KSL = DC + 1;           // LDS slots per K row
+  constexpr int KROW = 8 * KSL;         // padded LDS row of K (elements)
+  constexpr int VSL = BN / 8 + 1;       // LDS slots per V^T row (direct path)
+  constexpr int VROW = VT ? 8 * VSL : BN + 4;  // padded LDS row of V^T (elements)
   constexpr int NT = 64 * NW;                       // threads per workgroup
-  constexpr int KCH = (BN * DC + NT - 1) / NT;      // K chunks per thread
   constexpr int VCH = ((BN / 2) * DC + NT - 1) / NT;  // V key-pair units per thread
-  constexpr int KBUF = BN * KROW, VBUF = DT * 32 * VROW;
+  constexpr int VINS = (HD * VSL + 63) / 64;        // V^T load instructions per tile
+  constexpr int KBUF = BN * KROW;                   // = 64 * KSL slots: KSL instructions
+  constexpr int VBUF = (VT && VINS * 512 > DT * 32 * VROW) ? VINS * 512 : DT * 32 * VROW;
   // Lazy rescaling: the running max used for exp2 only moves when a score
   // exceeds it by more than this (log2 units), so P stays <= 2^8.
   constexpr float kRescale = 8.f;
@@ -223,31 +237,49 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     }
   }
 
-  constexpr int VTCH = (HD * (BN / 8) + NT - 1) / NT;  // V^T 16-byte chunks per thread
   // Global loads go through buffer descriptors: each thread's byte offsets
   // within a tile are fixed (computed once, 32-bit), and a tile only moves
   // the descriptor base, in scalar registers.  num_records ends at the last
   // valid K (or row-major V) row, so rows at or past S read as zero with no
-  // per-row test.  Chunks past the end of a tile's K rows (small HD) get an
-  // offset beyond num_records for the same effect.
+  // per-row test.
   constexpr int kRsrcFlags = 0x00020000;  // raw (untyped) access, gfx9 family
   constexpr uint32_t kOob = 0x80000000u;
-  uint32_t koff[KCH];
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  // With V^T rows (VT), K and V^T go straight to LDS: instruction j (of
+  // KSL) fills K slots [64j, 64j+64); wave w issues j = w, w+NW, ..  With
+  // row-major V, whose transpose needs registers anyway, K is staged through
+  // registers too (KCH 16-byte chunks per thread): that variant stays under
+  // the register budget of three waves per SIMD.
+  constexpr int KIPW = VT ? (KSL + NW - 1) / NW : 1;
+  constexpr int KCH = VT ? 1 : (BN * DC + NT - 1) / NT;
+  uint32_t koffs[VT ? KIPW : KCH];
 #pragma unroll
-  for (int j = 0; j < KCH; ++j) {
-    const int c = tid + NT * j;
-    const int key = c / DC, dc = c - key * DC;
-    koff[j] = c < BN * DC ? static_cast<uint32_t>((key * ks2 + dc * 8) * 2) : kOob;
-  }
-  constexpr int VOFFS = VT ? VTCH : VCH;
-  uint32_t voff[VOFFS];
-#pragma unroll
-  for (int j = 0; j < VOFFS; ++j) {
-    const int c = tid + NT * j;
+  for (int i = 0; i < (VT ? KIPW : KCH); ++i) {
     if constexpr (VT) {
-      const int d = c / (BN / 8), kc = c - d * (BN / 8);
-      voff[j] = c < HD * (BN / 8) ? static_cast<uint32_t>((d * vs2 + 8 * kc) * 2) : kOob;
+      const int j = wv + NW * i, P = 64 * j + lane;
+      const int r = P / KSL, c = P - r * KSL;
+      koffs[i] = (j < KSL && c < DC) ? static_cast<uint32_t>((r * ks2 + c * 8) * 2) : kOob;
     } else {
+      const int c = tid + NT * i;
+      const int key = c / DC, dc = c - key * DC;
+      koffs[i] = c < BN * DC ? static_cast<uint32_t>((key * ks2 + dc * 8) * 2) : kOob;
+    }
+  }
+  // V^T rows (direct path): slot P <-> (d = P / VSL, 8-key chunk P % VSL)
+  constexpr int VIPW = VT ? (VINS + NW - 1) / NW : 1;
+  uint32_t vtoffs[VIPW];
+#pragma unroll
+  for (int i = 0; i < VIPW; ++i) {
+    const int j = wv + NW * i, P = 64 * j + lane;
+    const int d = P / VSL, c = P - d * VSL;
+    vtoffs[i] = (VT && j < VINS && d < HD && c < BN / 8) ? static_cast<uint32_t>((d * vs2 + 8 * c) * 2) : kOob;
+  }
+  // row-major V: transposed through registers while staged
+  uint32_t voff[VT ? 1 : VCH];
+  if constexpr (!VT) {
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+      const int c = tid + NT * j;
       const int kp = c / DC, dc = c - kp * DC;
       voff[j] = c < (BN / 2) * DC ? static_cast<uint32_t>((2 * kp * vs2 + dc * 8) * 2) : kOob;
     }
@@ -287,75 +319,68 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     // MFMA of every iteration wait for the next tile's prefetch as well.
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
 
-    uint4 kreg[KCH];
-    uint4 vreg[VT ? VTCH : VCH][2];
-    auto fetch_tile = [&](int key0) {
+    uint4 vreg[VT ? 1 : VCH][2];
+    uint4 kreg[VT ? 1 : KCH];
+    // Issue the loads of the tile at key0 into LDS buffer buf (K, and V^T
+    // on the direct path) or registers (row-major V).
+    auto fetch_tile = [&](int key0, int buf) {
       const int rows = min(BN, S - key0);  // valid keys in this tile (>= 1)
       const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<bf16*>(kbase + static_cast<int64_t>(key0) * ks2), 0,
           static_cast<int>((rows - 1) * ks2 * 2 + HD * 2), kRsrcFlags);
-  #pragma unroll
-      for (int j = 0; j < KCH; ++j)
-        kreg[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[j], 0, 0));
+      if constexpr (VT) {
+#pragma unroll
+        for (int i = 0; i < KIPW; ++i) {
+          const int j = wv + NW * i;
+          if (j < KSL) load16_to_lds(kr, Ks + buf * KBUF + 512 * j, koffs[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i)
+          kreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, koffs[i], 0, 0));
+      }
       if constexpr (VT) {
         // Keys past S inside a d row are in memory (the next row's keys, or
-        // the row padding); stage() zeroes them.  num_records stops the last
-        // row at S.
+        // the row padding): zero_tail() clears them in LDS.  num_records
+        // stops the last row at S.
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<bf16*>(vbase + key0), 0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2), kRsrcFlags);
-  #pragma unroll
-        for (int j = 0; j < VTCH; ++j)
-          vreg[j][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j], 0, 0));
+#pragma unroll
+        for (int i = 0; i < VIPW; ++i) {
+          const int j = wv + NW * i;
+          if (j < VINS)
+            load16_to_lds(vr, Vt + buf * VBUF + 512 * j, vtoffs[i]);
+        }
       } else {
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<bf16*>(vbase + static_cast<int64_t>(key0) * vs2), 0,
             static_cast<int>((rows - 1) * vs2 * 2 + HD * 2), kRsrcFlags);
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < VCH; ++j) {
           vreg[j][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j], 0, 0));
           vreg[j][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j] + vrow_bytes, 0, 0));
         }
       }
     };
-    auto stage = [&](int buf, int key0) {
-      uint16_t* kd = Ks + buf * KBUF;
-      uint16_t* vd = Vt + buf * VBUF;
-  #pragma unroll
-      for (int j = 0; j < KCH; ++j) {
-        const int c = tid + NT * j;
-        const int key = c / DC, dc = c - key * DC;
-        if ((BN * DC) % NT == 0 || c < BN * DC) *reinterpret_cast<uint4*>(&kd[key * KROW + dc * 8]) = kreg[j];
-      }
-      if constexpr (VT) {
-        // S % 8 == 0 on this path: a chunk of 8 keys is all in or all out, and
-        // only the last tile of the sequence (a uniform branch) has chunks out.
-        if (key0 + BN > S) {
-  #pragma unroll
-          for (int j = 0; j < VTCH; ++j) {
-            const int kc = (tid + NT * j) % (BN / 8);
-            if (key0 + 8 * kc >= S) vreg[j][0] = make_uint4(0, 0, 0, 0);
-          }
+    // Row-major V: K rows and the transposed V from registers into buffer buf.
+    auto stage = [&](int buf) {
+      if constexpr (!VT) {
+        uint16_t* kd = Ks + buf * KBUF;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+          const int c = tid + NT * i;
+          const int key = c / DC, dc = c - key * DC;
+          if ((BN * DC) % NT == 0 || c < BN * DC) *reinterpret_cast<uint4*>(&kd[key * KROW + dc * 8]) = kreg[i];
         }
-  #pragma unroll
-        for (int j = 0; j < VTCH; ++j) {
-          const int c = tid + NT * j;
-          const int d = c / (BN / 8), kc = c - d * (BN / 8);
-          if ((HD * (BN / 8)) % NT == 0 || c < HD * (BN / 8)) {
-            const uint4 x = vreg[j][0];
-            // VROW*2 bytes is a multiple of 8, not of 16: two 8-byte stores
-            *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc]) = make_uint2(x.x, x.y);
-            *reinterpret_cast<uint2*>(&vd[d * VROW + 8 * kc + 4]) = make_uint2(x.z, x.w);
-          }
-        }
-      } else {
-  #pragma unroll
+        uint16_t* vd = Vt + buf * VBUF;
+#pragma unroll
         for (int j = 0; j < VCH; ++j) {
           const int u = tid + NT * j;
           const int kp = u / DC, dc = u - kp * DC;
           if (((BN / 2) * DC) % NT == 0 || u < (BN / 2) * DC) {
             const uint32_t a[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
             const uint32_t c2[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
-  #pragma unroll
+#pragma unroll
             for (int e = 0; e < 4; ++e) {
               // d = dc*8 + 2e (low halves) and d+1 (high halves); keys 2kp, 2kp+1
               const uint32_t lo = __builtin_amdgcn_perm(c2[e], a[e], 0x05040100u);
@@ -367,7 +392,24 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
         }
       }
     };
-
+    // Wait for this wave's loads (LDS writes included), then for every wave.
+    auto land = [&]() {
+      __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+      __syncthreads();
+    };
+    // Direct V^T path, last tile of the sequence: zero the keys at or past S
+    // (a uniform branch; S % 8 == 0 here).  Follows land(), ends with a barrier.
+    auto zero_tail = [&](int key0, int buf) {
+      if (VT && key0 + BN > S) {
+        const int valid = S - key0, w = BN - valid;
+        uint16_t* vd = Vt + buf * VBUF;
+        for (int i = tid; i < HD * w; i += NT) {
+          const int d = i / w;
+          vd[d * VROW + valid + (i - d * w)] = 0;
+        }
+        __syncthreads();
+      }
+    };
 
     float m_i = -INFINITY, l_i = 0.f;
     f32x16_t acc[DT];
@@ -482,26 +524,29 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     // barrier that ended the previous chunk's last tile lets both LDS
     // buffers be refilled.
     const int nf = max(kb0, min(nfull, kb1));
-    fetch_tile(kb0 * BN);
-    stage(kb0 & 1, kb0 * BN);
-    __syncthreads();
+    fetch_tile(kb0 * BN, kb0 & 1);
+    stage(kb0 & 1);
+    land();
+    zero_tail(kb0 * BN, kb0 & 1);
     // `active` is wave-uniform: branch on it rather than masking lanes.
     const bool wave_active = __builtin_amdgcn_readfirstlane(active ? 1 : 0) != 0;
     int kb = kb0;
     for (; kb < nf; ++kb) {
-      if (kb + 1 < kb1) fetch_tile((kb + 1) * BN);
-      if (wave_active) tile(kb, std::false_type());
       // The next tile goes into the other buffer, which every wave finished
       // reading before the barrier that ended the previous iteration.
-      if (kb + 1 < kb1) stage((kb & 1) ^ 1, (kb + 1) * BN);
-      __syncthreads();
+      if (kb + 1 < kb1) fetch_tile((kb + 1) * BN, (kb & 1) ^ 1);
+      if (wave_active) tile(kb, std::false_type());
+      if (kb + 1 < kb1) stage((kb & 1) ^ 1);
+      land();
+      if (kb + 1 < kb1) zero_tail((kb + 1) * BN, (kb & 1) ^ 1);
     }
     for (; kb < kb1; ++kb) {
-      if (kb + 1 < kb1) fetch_tile((kb + 1) * BN);
+      if (kb + 1 < kb1) fetch_tile((kb + 1) * BN, (kb & 1) ^ 1);
       const bool live = wave_active && !(CAUSAL && MASK != 2 && kb * BN > q0 + 31);
       if (live) tile(kb, std::true_type());
-      if (kb + 1 < kb1) stage((kb & 1) ^ 1, (kb + 1) * BN);
-      __syncthreads();
+      if (kb + 1 < kb1) stage((kb & 1) ^ 1);
+      land();
+      if (kb + 1 < kb1) zero_tail((kb + 1) * BN, (kb & 1) ^ 1);
     }
 
     if (kb0 == 0 && kb1 == nkb) {
