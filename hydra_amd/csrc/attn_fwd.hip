@@ -138,10 +138,41 @@ __host__ __device__ __forceinline__ int attn_range_begin(int w, int T, int P) {
   return static_cast<int>(static_cast<int64_t>(w) * T / P);
 }
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor (base, stride 0, num_records, untyped access) as four
+// wave-uniform words.
+__device__ __forceinline__ i32x4_t raw_rsrc(const void* base, int num_records) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a)));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xffffu));
+  r.z = __builtin_amdgcn_readfirstlane(num_records);
+  r.w = 0x00020000;
+  return r;
+}
+
 // Buffer load of 16 bytes per lane straight into LDS: lane l's bytes land
-// at lds + 16*l (lds must be wave-uniform), whatever its global offset.
-__device__ __forceinline__ void load16_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+// at lds + 16*l (lds must be wave-uniform), whatever its global offset; an
+// offset at or past num_records writes zeros.  Written as inline assembly
+// so that the compiler, which cannot tell which LDS bytes the transfer
+// writes, does not make every later LDS read wait for it (a vmcnt(0) at the
+// top of each tile, which would expose the prefetch's whole latency): the
+// caller waits with vmcnt(0) and a barrier before reading the destination.
+// M0 is written here and in no compiler-generated code of this file (the
+// compiler sets M0 right before each instruction that reads it, and only
+// these transfers do), so the clobber loses nothing.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void load16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
 
 // Writes one query row of O (bf16) from the MFMA accumulator layout, with
@@ -181,6 +212,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   // V is [.., S, hd] and is transposed while staged.
   constexpr int BN = kAttnBN;           // keys per tile
   constexpr int KSTEPS = HD / 16;       // k-steps of S^T = K Q^T
+  constexpr int MT = BN / 32;           // 32-key row tiles of S^T
+  constexpr int PS = BN / 16;           // 16-key k-steps of O^T = V^T P^T
   constexpr int DT = (HD + 31) / 32;    // 32-row d tiles of O^T
   // LDS rows are padded by one 16-byte slot (8 elements) so that the MFMA
   // operand reads of 16 consecutive rows hit distinct banks.  K (and V^T
@@ -195,7 +228,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   constexpr int NT = 64 * NW;                       // threads per workgroup
   constexpr int VCH = ((BN / 2) * DC + NT - 1) / NT;  // V key-pair units per thread
   constexpr int VINS = (HD * VSL + 63) / 64;        // V^T load instructions per tile
-  constexpr int KBUF = BN * KROW;                   // = 64 * KSL slots: KSL instructions
+  constexpr int KBUF = BN * KROW;                   // BN * KSL slots
+  constexpr int KINS = BN * KSL / 64;               // K load instructions per tile
   constexpr int VBUF = (VT && VINS * 512 > DT * 32 * VROW) ? VINS * 512 : DT * 32 * VROW;
   // Lazy rescaling: the running max used for exp2 only moves when a score
   // exceeds it by more than this (log2 units), so P stays <= 2^8.
@@ -246,11 +280,11 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   constexpr uint32_t kOob = 0x80000000u;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   // With V^T rows (VT), K and V^T go straight to LDS: instruction j (of
-  // KSL) fills K slots [64j, 64j+64); wave w issues j = w, w+NW, ..  With
+  // KINS) fills K slots [64j, 64j+64); wave w issues j = w, w+NW, ..  With
   // row-major V, whose transpose needs registers anyway, K is staged through
   // registers too (KCH 16-byte chunks per thread): that variant stays under
   // the register budget of three waves per SIMD.
-  constexpr int KIPW = VT ? (KSL + NW - 1) / NW : 1;
+  constexpr int KIPW = VT ? (KINS + NW - 1) / NW : 1;
   constexpr int KCH = VT ? 1 : (BN * DC + NT - 1) / NT;
   uint32_t koffs[VT ? KIPW : KCH];
 #pragma unroll
@@ -258,7 +292,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     if constexpr (VT) {
       const int j = wv + NW * i, P = 64 * j + lane;
       const int r = P / KSL, c = P - r * KSL;
-      koffs[i] = (j < KSL && c < DC) ? static_cast<uint32_t>((r * ks2 + c * 8) * 2) : kOob;
+      koffs[i] = (j < KINS && c < DC) ? static_cast<uint32_t>((r * ks2 + c * 8) * 2) : kOob;
     } else {
       const int c = tid + NT * i;
       const int key = c / DC, dc = c - key * DC;
@@ -285,6 +319,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     }
   }
   const uint32_t vrow_bytes = static_cast<uint32_t>(vs2 * 2);
+  const uint32_t ks_lds = lds_addr(Ks), vt_lds = lds_addr(Vt);
 
   bool started = false;
   int chunk_no = 0;
@@ -325,16 +360,17 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     // on the direct path) or registers (row-major V).
     auto fetch_tile = [&](int key0, int buf) {
       const int rows = min(BN, S - key0);  // valid keys in this tile (>= 1)
-      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<bf16*>(kbase + static_cast<int64_t>(key0) * ks2), 0,
-          static_cast<int>((rows - 1) * ks2 * 2 + HD * 2), kRsrcFlags);
+      const bf16* kt0 = kbase + static_cast<int64_t>(key0) * ks2;
+      const int krec = static_cast<int>((rows - 1) * ks2 * 2 + HD * 2);
       if constexpr (VT) {
+        const i32x4_t kr = raw_rsrc(kt0, krec);
 #pragma unroll
         for (int i = 0; i < KIPW; ++i) {
           const int j = wv + NW * i;
-          if (j < KSL) load16_to_lds(kr, Ks + buf * KBUF + 512 * j, koffs[i]);
+          if (j < KINS) load16_to_lds(kr, ks_lds + (buf * KBUF + 512 * j) * 2, koffs[i]);
         }
       } else {
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(kt0), 0, krec, kRsrcFlags);
 #pragma unroll
         for (int i = 0; i < KCH; ++i)
           kreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, koffs[i], 0, 0));
@@ -343,13 +379,12 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
         // Keys past S inside a d row are in memory (the next row's keys, or
         // the row padding): zero_tail() clears them in LDS.  num_records
         // stops the last row at S.
-        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<bf16*>(vbase + key0), 0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2), kRsrcFlags);
+        const i32x4_t vr = raw_rsrc(vbase + key0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2));
 #pragma unroll
         for (int i = 0; i < VIPW; ++i) {
           const int j = wv + NW * i;
           if (j < VINS)
-            load16_to_lds(vr, Vt + buf * VBUF + 512 * j, vtoffs[i]);
+            load16_to_lds(vr, vt_lds + (buf * VBUF + 512 * j) * 2, vtoffs[i]);
         }
       } else {
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
@@ -427,21 +462,21 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       const int key0 = kb * BN;
       const uint16_t* kt = Ks + buf * KBUF;
       const uint16_t* vt = Vt + buf * VBUF;
-      f32x16_t st[2];
+      f32x16_t st[MT];
   #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
   #pragma unroll
         for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
   #pragma unroll
       for (int s = 0; s < KSTEPS; ++s)
   #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
           const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
           st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
         }
       if constexpr (MASKED) {
   #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
   #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
@@ -456,7 +491,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       }
       float mx = -INFINITY;
   #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
   #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
       mx = halves_max(mx) * scale_log2;  // scaled row max of this tile
@@ -478,10 +513,10 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       const float m_use = m_i == -INFINITY ? 0.f : m_i;
       // P in bf16, and its row sum from the same rounded values (v_dot2 with
       // (1, 1)), so the normalisation uses exactly the P of the PV product.
-      uint4 pk[4];
+      uint4 pk[PS];
       float rs = 0.f;
   #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
+      for (int s2 = 0; s2 < PS; ++s2) {
         const int mt = s2 >> 1, rb = 8 * (s2 & 1);
         float p[8];
   #pragma unroll
@@ -497,9 +532,9 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
         rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
       }
       l_i += halves_sum(rs);
-      // O^T += V^T P^T over 4 k-steps of 16 keys.
+      // O^T += V^T P^T over PS k-steps of 16 keys.
   #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
+      for (int s2 = 0; s2 < PS; ++s2) {
         const bf16x8_t pf = as_bf16x8(pk[s2]);
   #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
