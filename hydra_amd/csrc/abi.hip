@@ -1,6 +1,12 @@
 // Error plumbing and version query of the C ABI.
 #include "common.h"
 
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <mutex>
+
 namespace hydra {
 
 static thread_local std::string g_last_error;
@@ -32,6 +38,45 @@ int dtype_size(int dtype) {
     case HYDRA_F16: return 2;
     default: return 0;
   }
+}
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// From the kernel's register and LDS footprint: a SIMD holds 512 VGPRs per
+// lane (allocated in granules of 8) and at most 8 waves, a CU 4 SIMDs and
+// 160 KiB of LDS.  (The runtime's occupancy query over-counted for these
+// kernels.)
+int blocks_per_cu(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<const void*, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(kernel);
+  if (it != cache.end()) return it->second;
+  hipFuncAttributes a{};
+  int nb = 1;
+  if (hipFuncGetAttributes(&a, kernel) == hipSuccess) {
+    const int regs = std::max(8, (a.numRegs + 7) / 8 * 8);
+    const int waves_per_simd = std::min(8, 512 / regs);
+    const int waves_per_wg = (threads + 63) / 64;
+    const int by_regs = waves_per_simd * 4 / waves_per_wg;
+    const size_t lds = a.sharedSizeBytes;
+    const int by_lds = lds > 0 ? static_cast<int>((160 * 1024) / lds) : by_regs;
+    nb = std::max(1, std::min(by_regs, by_lds));
+  }
+  if (const char* e = getenv("HYDRA_OCC_DEBUG"))
+    if (atoi(e)) fprintf(stderr, "hydra_amd: %d resident workgroups per CU (regs %d, lds %zu)\n", nb, a.numRegs, a.sharedSizeBytes);
+  cache[kernel] = nb;
+  return nb;
 }
 
 }  // namespace hydra

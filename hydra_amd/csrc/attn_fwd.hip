@@ -29,6 +29,7 @@
 // Generic path (attn_fwd_generic_kernel): one thread per query row, fp32
 // math, any element type, even head_dim <= 256.
 #include "common.h"
+#include "lds_dma.h"
 
 #include <algorithm>
 #include <cstdio>
@@ -138,42 +139,6 @@ __host__ __device__ __forceinline__ int attn_range_begin(int w, int T, int P) {
   return static_cast<int>(static_cast<int64_t>(w) * T / P);
 }
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor (base, stride 0, num_records, untyped access) as four
-// wave-uniform words.
-__device__ __forceinline__ i32x4_t raw_rsrc(const void* base, int num_records) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4_t r;
-  r.x = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a)));
-  r.y = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xffffu));
-  r.z = __builtin_amdgcn_readfirstlane(num_records);
-  r.w = 0x00020000;
-  return r;
-}
-
-// Buffer load of 16 bytes per lane straight into LDS: lane l's bytes land
-// at lds + 16*l (lds must be wave-uniform), whatever its global offset; an
-// offset at or past num_records writes zeros.  Written as inline assembly
-// so that the compiler, which cannot tell which LDS bytes the transfer
-// writes, does not make every later LDS read wait for it (a vmcnt(0) at the
-// top of each tile, which would expose the prefetch's whole latency): the
-// caller waits with vmcnt(0) and a barrier before reading the destination.
-// M0 is written here and in no compiler-generated code of this file (the
-// compiler sets M0 right before each instruction that reads it, and only
-// these transfers do), so the clobber loses nothing.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void load16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// LDS byte address of a pointer into shared memory.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
 
 // Writes one query row of O (bf16) from the MFMA accumulator layout, with
 // the softmax normaliser 1/l, and its log-sum-exp (m is in log2 units).
@@ -788,44 +753,6 @@ static int attn_workspace(size_t bytes, hipStream_t st, void** out) {
   }
   *out = w.ptr;
   return HYDRA_OK;
-}
-
-static int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
-// Resident workgroups per CU of a kernel (cached per kernel), from its
-// register and LDS footprint: a SIMD holds 512 VGPRs per lane (allocated in
-// granules of 8) and at most 8 waves, a CU 4 SIMDs and 160 KiB of LDS.
-static int blocks_per_cu(const void* kernel, int threads) {
-  static std::mutex mu;
-  static std::map<const void*, int> cache;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find(kernel);
-  if (it != cache.end()) return it->second;
-  hipFuncAttributes a{};
-  int nb = 1;
-  if (hipFuncGetAttributes(&a, kernel) == hipSuccess) {
-    const int regs = std::max(8, (a.numRegs + 7) / 8 * 8);
-    const int waves_per_simd = std::min(8, 512 / regs);
-    const int waves_per_wg = (threads + 63) / 64;
-    int by_regs = waves_per_simd * 4 / waves_per_wg;
-    const size_t lds = a.sharedSizeBytes;
-    const int by_lds = lds > 0 ? static_cast<int>((160 * 1024) / lds) : by_regs;
-    nb = std::max(1, std::min(by_regs, by_lds));
-  }
-  if (const char* e = getenv("HYDRA_ATTN_DEBUG"))
-    if (atoi(e)) fprintf(stderr, "attn_fwd: %d resident workgroups per CU (regs %d, lds %zu)\n", nb, a.numRegs, a.sharedSizeBytes);
-  cache[kernel] = nb;
-  return nb;
 }
 
 template <int HD>

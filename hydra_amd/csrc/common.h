@@ -156,6 +156,10 @@ int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 bool aligned16(const void* p);
 int dtype_size(int dtype);
+// Compute units of the current device (cached per device).
+int device_cus();
+// Workgroups of `kernel` (launched with `threads`) resident on one CU.
+int blocks_per_cu(const void* kernel, int threads);
 
 }  // namespace hydra
 
