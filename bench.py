@@ -136,10 +136,10 @@ def bench_c3(dev, steps, warmup):
     """The config-3 step timed two ways over rotating inputs (one x per step,
     N_X_SETS sets, so repeats are not served from the memory-side cache):
 
-    - graph: each step captured once per input set into a HIP graph (shared
-      memory pool) and replayed -- the GPU timeline of the step without the
-      host's Python/ctypes launch cost.  This is the reported value: K timed
-      replays after W untimed ones.
+    - graph: the K steps captured into one HIP graph and replayed (after W
+      eager warmup steps and one untimed replay) -- the GPU timeline of the
+      steps without the host's Python/ctypes launch cost, one graph launch
+      for all K.  This is the reported value.
     - eager: the same K steps launched from Python, with HIP events around
       each stage (the stage breakdown; host launch gaps included).
 
@@ -169,7 +169,9 @@ def bench_c3(dev, steps, warmup):
     eager_ms = t0.elapsed_time(t1) / steps
     names = ["qkv_gemm", "prep", "attention", "o_proj_gemm"]
     stages = {n: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, n in enumerate(names)}
-    # graph: one captured step per input set
+    # graph: the K steps (input sets in turn) captured into one HIP graph,
+    # replayed once untimed and once timed -- exactly K steps, one graph
+    # launch for all of them
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -177,24 +179,19 @@ def bench_c3(dev, steps, warmup):
             step(x=xs[i])
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    graphs, pool = [], None
-    for i in range(N_X_SETS):
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr, pool=pool):
-            step(x=xs[i])
-        pool = gr.pool()
-        graphs.append(gr)
-    for i in range(max(warmup, 1)):
-        graphs[i % N_X_SETS].replay()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(x=xs[i % N_X_SETS])
+    graph.replay()
     torch.cuda.synchronize()
     t0, t1 = _events(2)
     t0.record()
-    for i in range(steps):
-        graphs[i % N_X_SETS].replay()
+    graph.replay()
     t1.record()
     torch.cuda.synchronize()
     graph_ms = t0.elapsed_time(t1) / steps
-    del graphs
+    del graph
     # the attention op alone, back to back in a graph
     m = step.m
     with torch.no_grad():
@@ -412,7 +409,7 @@ def main():
                      "frac": achieved / BF16_PEAK_TFLOPS,
                      "traffic": measured_traffic("attention_op<64,causal>"),
                      "flops_per_launch": fl["core"], "avg_ms": attn_ms},
-        "launch": "HIP graph: one captured step per rotating input set (16 x 32 MiB of x)",
+        "launch": "HIP graph of the K steps (16 rotating 32 MiB input sets), one launch",
         "eager_ms_per_step": eager_ms,
         "stages_ms": {"eager_events": stages, "attention_graph": attn_ms},
         "module_tflops": fl["total"] / (ms_step * 1e-3) / 1e12,
