@@ -5,14 +5,18 @@ dim 1024, 4x compression to latent 256, 4 query heads / 1 KV head (hd 64),
 causal conv k=3, QK-mean, QK L2-norm with temperature 1.0, B4 x S4096, bf16,
 random-init N(0, 0.02) weights, N(0,1) activations (seed 0).  A step is one
 full module forward: qkv GEMM -> fused prep kernel -> attention kernel ->
-o_proj GEMM, inputs resident in HBM.
+o_proj GEMM, inputs resident in HBM (16 rotating input sets).  The K timed
+steps are one HIP graph replay between synchronisations, so the graph's
+launch latency (~0.1 ms for K = 100) is inside the timed region, spread
+over the K steps; the eager Python-launched time is reported beside it.
 
 Also reported on the same line:
   roofline      the attention op (dominant: the attention kernel and, when
                 the stream-K schedule splits items, its merge kernel),
                 algorithmic FLOPs / its average duration from HIP events
-                recorded on the launch stream over the timed steps;
-  stages        per-stage average durations of the step;
+                recorded on the launch stream around a graph of
+                back-to-back calls;
+  stages        per-stage average durations of the eager step;
   fused_ops     config 2 RMSNorm / RoPE / SwiGLU in HBM GB/s and % of peak
                 (buffers rotated over > 512 MB so the 256 MB MALL cannot
                 serve repeats);
@@ -364,7 +368,7 @@ def measured_traffic(kernel_key):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip the fused-op and MoD sections")
