@@ -86,6 +86,7 @@ class C3Step:
         self.cos = mm.cos_cached[0, 0, :S].float().contiguous()
         self.sin = mm.sin_cached[0, 0, :S].float().contiguous()
         self.out = torch.empty(B, S, mm.latent_dim, dtype=torch.bfloat16, device=dev)
+        self.bound = mm._score_bound()  # |q.k| bound from QK-norm (temperature 1.0)
 
     @torch.no_grad()
     def __call__(self, ev=None, x=None):
@@ -103,7 +104,7 @@ class C3Step:
         if ev:
             ev[2].record()
         o_view = self.out.view(self.B, self.S, m.n_heads, m.head_dim).transpose(1, 2)
-        attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view)
+        attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view, score_bound=self.bound)
         if ev:
             ev[3].record()
         y = F.linear(self.out, m.o_proj.weight)
@@ -203,7 +204,8 @@ def bench_c3(dev, steps, warmup):
         q, k, v = ccgqa_prep(qkv, m.n_heads, m.n_kv_heads, m.head_dim, step.flags, *step.convw,
                              temperature=m.key_temperature, cos=step.cos, sin=step.sin, packed=True)
     o_view = step.out.view(step.B, step.S, m.n_heads, m.head_dim).transpose(1, 2)
-    attn_ms = _time_rotating(lambda: attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view),
+    attn_ms = _time_rotating(lambda: attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view,
+                                                       score_bound=step.bound),
                              [()], 8 * max(1, steps // 2))
     return step, graph_ms, eager_ms, stages, attn_ms
 

@@ -99,10 +99,12 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
 def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool,
                       scale: Optional[float] = None, key_mask: Optional[torch.Tensor] = None,
                       mask_mode: int = MASK_NONE, out: Optional[torch.Tensor] = None,
-                      want_lse: bool = False):
+                      want_lse: bool = False, score_bound: Optional[float] = None):
     """Softmax attention over [B,H,S,hd] q and [B,Hkv,S,hd] k/v.  `out` may be
     any [B,Hq,S,hd]-indexed view (e.g. a [B,S,Hq,hd] buffer transposed).
-    Returns (out, lse or None)."""
+    score_bound: optional beta >= max |q.k| (before the scale); with one the
+    bf16 kernel takes a fixed reference max instead of a running row max
+    (see qk_norm_score_bound).  Returns (out, lse or None)."""
     _lib.require_gpu("attention_forward", q, k, v, key_mask, out)
     B, Hq, S, hd = q.shape
     Hkv = k.shape[1]
@@ -131,8 +133,17 @@ def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
         _lib.call("hydra_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                   _lib.ptr(lse), _lib.ptr(km), mask_mode, B, Hq, Hkv, S, hd,
                   _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
-                  1 if causal else 0, sc, _lib.dtype_code(q), _lib.stream(q))
+                  1 if causal else 0, sc, float(score_bound or 0.0), _lib.dtype_code(q),
+                  _lib.stream(q))
     return out, lse
+
+
+def qk_norm_score_bound(temperature: float) -> float:
+    """Bound on |q.k| after CCGQAAttention's QK L2-norm (attention.py:260-262):
+    q has unit norm and k the norm |temperature|, RoPE is a rotation, and the
+    bf16 roundings of the norm, the normalised vector, the temperature product
+    and RoPE move a norm by less than 1%; 3% covers it."""
+    return 1.03 * abs(float(temperature))
 
 
 def conv_sequence(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, groups1: int,
@@ -155,4 +166,4 @@ def conv_sequence(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, groups1: 
 
 
 __all__ = ["prep_flags", "pack_conv_weight", "ccgqa_prep", "attention_forward", "conv_sequence",
-           "MASK_NONE", "MASK_KEY_PADDING", "MASK_REFERENCE_SDPA"]
+           "qk_norm_score_bound", "MASK_NONE", "MASK_KEY_PADDING", "MASK_REFERENCE_SDPA"]

@@ -162,7 +162,7 @@ __device__ __forceinline__ void attn_store_row(bf16* orow, const f32x16_t* acc, 
   if (lse && hf == 0) *lse = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
 }
 
-template <int HD, bool CAUSAL, int MASK, bool VT, int NW>
+template <int HD, bool CAUSAL, int MASK, bool VT, int NW, bool FIXED>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     int64_t qs0, int64_t qs1, int64_t qs2,
     int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2,
-    int64_t os0, int64_t os1, int64_t os2, float scale_log2) {
+    int64_t os0, int64_t os1, int64_t os2, float scale_log2, float m_fix) {
   // VT: V is stored transposed ([.., hd, S], keys contiguous, row stride
   // vs2 between d rows) and is staged with plain 16-byte copies; otherwise
   // V is [.., S, hd] and is transposed while staged.
@@ -199,6 +199,11 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   // Lazy rescaling: the running max used for exp2 only moves when a score
   // exceeds it by more than this (log2 units), so P stays <= 2^8.
   constexpr float kRescale = 8.f;
+  // FIXED: the caller bounds |q.k|, so every row takes the fixed reference
+  // max m_fix = beta * scale (log2 units, at most 48: a row whose scores all
+  // sit at -beta still has P >= 2^-96, far from fp32 underflow) -- P <= 1
+  // with no per-tile max and no rescaling.
+  constexpr bool fixed_max = FIXED;
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * KBUF];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2 * VBUF];
@@ -411,7 +416,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       }
     };
 
-    float m_i = -INFINITY, l_i = 0.f;
+    float m_i = fixed_max ? m_fix : -INFINITY, l_i = 0.f;
     f32x16_t acc[DT];
   #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -454,26 +459,28 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
             st[mt][r] = ok ? st[mt][r] : -INFINITY;
           }
       }
-      float mx = -INFINITY;
+      if constexpr (!fixed_max) {
+        float mx = -INFINITY;
   #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
   #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
-      mx = halves_max(mx) * scale_log2;  // scaled row max of this tile
-      // Move the reference max only when this tile would push P past 2^8; the
-      // test is made wave-uniform so the common case is one skipped branch.
-      if (__any(mx > m_i + kRescale)) {
-        const bool move = mx > m_i + kRescale;
-        // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
-        // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
-        const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
-        const float m_new = move ? mx : m_i;
-        l_i *= alpha;
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+        mx = halves_max(mx) * scale_log2;  // scaled row max of this tile
+        // Move the reference max only when this tile would push P past 2^8; the
+        // test is made wave-uniform so the common case is one skipped branch.
+        if (__any(mx > m_i + kRescale)) {
+          const bool move = mx > m_i + kRescale;
+          // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
+          // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
+          const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
+          const float m_new = move ? mx : m_i;
+          l_i *= alpha;
   #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+          for (int dt = 0; dt < DT; ++dt)
   #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-        m_i = m_new;
+            for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+          m_i = m_new;
+        }
       }
       const float m_use = m_i == -INFINITY ? 0.f : m_i;
       // P in bf16, and its row sum from the same rounded values (v_dot2 with
@@ -760,7 +767,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t S, const int64_t* qs, const int64_t* ks,
                        const int64_t* vs, const int64_t* os, bool causal, float scale,
-                       hipStream_t st) {
+                       float score_bound, hipStream_t st) {
   constexpr int NW = 4;  // waves per workgroup; GQA heads share each staged K/V tile
   constexpr int DT = (HD + 31) / 32;
   // V with unit stride along the keys is read as V^T rows (vs[3] apart).
@@ -785,10 +792,15 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   auto K = static_cast<const bf16*>(k);
   auto V = static_cast<const bf16*>(v);
   auto O = static_cast<bf16*>(o);
-  auto go = [&](auto c_tag, auto m_tag) -> int {
+  // A usable bound on |q.k| (and no key mask) selects the fixed-reference
+  // kernel; m_fix is its reference max in log2 units.
+  const float m_fix = score_bound > 0.f ? score_bound * sl2 : INFINITY;
+  const bool use_fixed = mask_mode == HYDRA_MASK_NONE && m_fix <= 48.f;
+  auto go = [&](auto c_tag, auto m_tag, auto f_tag) -> int {
     constexpr bool C = decltype(c_tag)::value;
     constexpr int M = decltype(m_tag)::value;
-    auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW> : attn_fwd_mfma_kernel<HD, C, M, false, NW>;
+    constexpr bool FX = decltype(f_tag)::value;
+    auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX> : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>;
     // Schedule.  With at least two items per resident workgroup slot, one
     // workgroup per item (longest first) lets the dispatcher balance the
     // load; with fewer, stream-K: one resident wave of workgroups, each with
@@ -829,7 +841,8 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     desc = reinterpret_cast<int4*>(static_cast<char*>(w) + pb);
     kern<<<dim3(static_cast<unsigned>(P)), 64 * NW, 0, st>>>(
         Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, T, per_item ? 1 : 0, part, desc,
-        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2);
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2,
+        m_fix);
     const int rc1 = check_launch("attn_fwd_mfma_kernel");
     if (rc1 != HYDRA_OK || !split) return rc1;
     const int64_t threads = static_cast<int64_t>(P) * NW * 64;
@@ -842,11 +855,11 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   using M0 = std::integral_constant<int, 0>;
   using M1 = std::integral_constant<int, 1>;
   using M2 = std::integral_constant<int, 2>;
-  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) return go(F_(), M2());
-  if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) return go(T_(), M1());
-  if (causal) return go(T_(), M0());
-  if (mask_mode == HYDRA_MASK_KEY_PADDING) return go(F_(), M1());
-  return go(F_(), M0());
+  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) return go(F_(), M2(), F_());
+  if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) return go(T_(), M1(), F_());
+  if (mask_mode == HYDRA_MASK_KEY_PADDING) return go(F_(), M1(), F_());
+  if (causal) return use_fixed ? go(T_(), M0(), T_()) : go(T_(), M0(), F_());
+  return use_fixed ? go(F_(), M0(), T_()) : go(F_(), M0(), F_());
 }
 
 template <typename T>
@@ -882,8 +895,8 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
                               float* lse, const uint8_t* key_mask, int mask_mode,
                               int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
                               const int64_t* qs, const int64_t* ks, const int64_t* vs,
-                              const int64_t* os, int causal, float scale, int dtype,
-                              void* stream) {
+                              const int64_t* os, int causal, float scale,
+                              float score_bound, int dtype, void* stream) {
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_fwd: bad size");
   HYDRA_REQUIRE(Hq % Hkv == 0, "attn_fwd: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(qs && ks && vs && os, "attn_fwd: null stride array");
@@ -921,10 +934,10 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   if (dtype == HYDRA_BF16 && mfma_shape && strides8 && aligned16(q) && aligned16(k) &&
       aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0) {
     switch (hd) {
-      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
-      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
-      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
-      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, st);
+      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
+      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
+      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
+      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
     }
   }
   HYDRA_REQUIRE(B * Hq * S / 256 < (int64_t(1) << 31), "attn_fwd: too many rows");

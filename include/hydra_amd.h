@@ -160,14 +160,24 @@ int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype);
  * o: element strides os[4] (last = 1) -- pass the strides of a [B,S,Hq,hd]
  *    buffer to write the merged-heads layout directly;
  * lse: optional fp32 [B,Hq,S] natural-log sum-exp of the scaled scores.
+ * score_bound: beta >= max |q_i . k_j| (before the scale), or <= 0 when no
+ *   bound is known.  When 0 < scale * beta * log2(e) <= 48 and no key mask
+ *   is given, the bf16 kernel uses the fixed reference max scale * beta for
+ *   every row instead of a running row max: no per-tile max and no
+ *   rescaling (the softmax is the same; its exponentials are taken relative
+ *   to another reference).  A beta below the true maximum overflows.  With
+ *   the QK L2-norm of CCGQAAttention (unit-norm q, k of norm |temperature|,
+ *   RoPE a rotation) beta = 1.03 * |temperature| holds: the 3% covers the
+ *   bf16 roundings of the norm, the normalised vector, the temperature
+ *   product and RoPE.
  * A query row with no visible key gets o = 0 (as CPU SDPA) and lse = -inf.
  * bf16 with hd in {16,32,64,128} runs on MFMA; other cases on the VALU. */
 int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
                    float* lse, const uint8_t* key_mask, int mask_mode,
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
                    const int64_t* qs, const int64_t* ks, const int64_t* vs,
-                   const int64_t* os, int causal, float scale, int dtype,
-                   void* stream);
+                   const int64_t* os, int causal, float scale,
+                   float score_bound, int dtype, void* stream);
 
 /* ---- Mixture-of-Depths hard routing (hydra/routing, model/framework) --- */
 

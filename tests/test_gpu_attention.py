@@ -244,3 +244,76 @@ def test_attention_split_fully_masked_rows(cuda, monkeypatch):
     assert torch.isinf(lse[:, :, :150].cpu()).all()
     ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
     assert max_rel_err(out[:, :, 150:].cpu(), ref[:, :, 150:]) < 2e-2
+
+
+def _normed_qkv(B, Hq, Hkv, S, hd, temp, seed):
+    """q of unit norm and k of norm |temp| per row (CCGQAAttention's QK-norm),
+    bf16-representable, as the prep kernel hands them to attention."""
+    g = torch.Generator().manual_seed(seed)
+    nrm = torch.nn.functional.normalize
+    q = nrm(torch.randn(B, Hq, S, hd, generator=g), dim=-1).to(torch.bfloat16).float()
+    k = (nrm(torch.randn(B, Hkv, S, hd, generator=g), dim=-1) * temp).to(torch.bfloat16).float()
+    v = torch.randn(B, Hkv, S, hd, generator=g).to(torch.bfloat16).float()
+    return q, k, v
+
+
+FIXED_CASES = [
+    # B, Hq, Hkv, S, hd, temperature, causal
+    (4, 4, 1, 512, 64, 1.0, True),
+    (2, 8, 2, 300, 16, 4.0, True),
+    (1, 4, 4, 257, 32, 5.66, False),
+    (2, 8, 1, 100, 128, 11.3, True),
+    (1, 2, 1, 64, 64, -8.0, False),
+    (1, 4, 1, 2048, 64, 40.0, True),
+]
+
+
+@pytest.mark.parametrize("wgs", [None, "7"])
+@pytest.mark.parametrize("case", FIXED_CASES, ids=[str(c) for c in FIXED_CASES])
+def test_attention_fixed_reference_max(cuda, monkeypatch, case, wgs):
+    """Given a bound on |q.k| (QK-norm: 1.03 |temperature|), the bf16 kernel
+    takes the fixed reference max instead of a running row max: the output
+    matches the oracle and the online-max kernel, the LSE matches the
+    closed form, also when stream-K cuts the items into chunks."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward, qk_norm_score_bound
+
+    B, Hq, Hkv, S, hd, temp, causal = case
+    if wgs is not None:
+        monkeypatch.setenv("HYDRA_ATTN_WGS", wgs)
+    q, k, v = _normed_qkv(B, Hq, Hkv, S, hd, temp, seed=S + hd)
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    beta = qk_norm_score_bound(temp)
+    out_f, lse_f = attention_forward(dev(q), dev(k), dev(v), causal=causal, want_lse=True,
+                                     score_bound=beta)
+    out_o, lse_o = attention_forward(dev(q), dev(k), dev(v), causal=causal, want_lse=True)
+    ref = occ.attention(q, k, v, causal=causal)
+    assert max_rel_err(out_f.cpu(), ref) < 2e-2
+    assert max_rel_err(out_f.cpu(), out_o.float().cpu()) < 2e-2
+    G = Hq // Hkv
+    logits = (q @ k.repeat_interleave(G, 1).transpose(-1, -2)) / math.sqrt(hd)
+    if causal:
+        logits = logits.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    ref_lse = torch.logsumexp(logits, -1)
+    assert (lse_f.cpu() - ref_lse).abs().max().item() < 2e-2
+    # row sums of bf16 P against two different reference maxima: |d log l| <= 2^-7
+    assert (lse_f - lse_o).abs().max().item() < 2 ** -7
+
+
+def test_attention_score_bound_outside_fixed_range(cuda):
+    """A bound whose reference max would exceed 2^48 relative range (here
+    |q.k| up to 300 at hd 64), or any key mask, keeps the running row max."""
+    from hydra_amd.attention.backends.ccgqa.ops import (MASK_KEY_PADDING, attention_forward,
+                                                        qk_norm_score_bound)
+
+    q, k, v = _normed_qkv(1, 4, 1, 256, 64, 300.0, seed=5)
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    out, _ = attention_forward(dev(q), dev(k), dev(v), causal=True,
+                               score_bound=qk_norm_score_bound(300.0))
+    assert max_rel_err(out.cpu(), occ.attention(q, k, v, causal=True)) < 2e-2
+    q, k, v = _normed_qkv(1, 4, 1, 256, 64, 2.0, seed=6)
+    mask = torch.ones(1, 256, dtype=torch.long)
+    mask[0, 10:90] = 0
+    out, _ = attention_forward(dev(q), dev(k), dev(v), causal=True, key_mask=mask.to(cuda),
+                               mask_mode=MASK_KEY_PADDING, score_bound=qk_norm_score_bound(2.0))
+    ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
+    assert max_rel_err(out.cpu(), ref) < 2e-2
