@@ -171,7 +171,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     int64_t qs0, int64_t qs1, int64_t qs2,
     int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2,
-    int64_t os0, int64_t os1, int64_t os2, float scale_log2, float m_fix) {
+    int64_t os0, int64_t os1, int64_t os2, float scale_log2) {
   // VT: V is stored transposed ([.., hd, S], keys contiguous, row stride
   // vs2 between d rows) and is staged with plain 16-byte copies; otherwise
   // V is [.., S, hd] and is transposed while staged.
@@ -199,10 +199,13 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   // Lazy rescaling: the running max used for exp2 only moves when a score
   // exceeds it by more than this (log2 units), so P stays <= 2^8.
   constexpr float kRescale = 8.f;
-  // FIXED: the caller bounds |q.k|, so every row takes the fixed reference
-  // max m_fix = beta * scale (log2 units, at most 48: a row whose scores all
-  // sit at -beta still has P >= 2^-96, far from fp32 underflow) -- P <= 1
-  // with no per-tile max and no rescaling.
+  // FIXED: the caller bounds |q.k| by beta with beta * scale <= 48 in log2
+  // units, so exp2 of a scaled score lies in [2^-48, 2^48] and needs no
+  // reference max at all (P, l and O stay far inside the bf16 / fp32 range):
+  // Q is scaled by scale * log2(e) as it is loaded, P = exp2 of the MFMA
+  // accumulator with no FMA, and there is no per-tile max or rescaling.  The
+  // scaled Q is rounded to bf16 once (2^-9 relative per element, the size of
+  // Q's own bf16 rounding).
   constexpr bool fixed_max = FIXED;
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * KBUF];
@@ -316,6 +319,14 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       for (int s = 0; s < KSTEPS; ++s) {
         uint4 raw = make_uint4(0, 0, 0, 0);
         if (active && qi < S) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
+        if constexpr (fixed_max) {
+          uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            w[e] = pack2<bf16>(__uint_as_float(w[e] << 16) * scale_log2,
+                               __uint_as_float(w[e] & 0xffff0000u) * scale_log2);
+          raw = make_uint4(w[0], w[1], w[2], w[3]);
+        }
         qf[s] = as_bf16x8(raw);
       }
     }
@@ -416,7 +427,9 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       }
     };
 
-    float m_i = fixed_max ? m_fix : -INFINITY, l_i = 0.f;
+    // l_i: this lane's part of the row sum (its half of the keys); the two
+    // halves of the wave are added once, after the chunk's last tile.
+    float m_i = fixed_max ? 0.f : -INFINITY, l_i = 0.f;
     f32x16_t acc[DT];
   #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -482,7 +495,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
           m_i = m_new;
         }
       }
-      const float m_use = m_i == -INFINITY ? 0.f : m_i;
+      const float m_use = fixed_max || m_i == -INFINITY ? 0.f : m_i;
       // P in bf16, and its row sum from the same rounded values (v_dot2 with
       // (1, 1)), so the normalisation uses exactly the P of the PV product.
       uint4 pk[PS];
@@ -493,7 +506,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
         float p[8];
   #pragma unroll
         for (int e = 0; e < 8; ++e)
-          p[e] = __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
+          p[e] = fixed_max ? __builtin_amdgcn_exp2f(st[mt][rb + e])
+                           : __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
         pk[s2].x = pack2<bf16>(p[0], p[1]);
         pk[s2].y = pack2<bf16>(p[2], p[3]);
         pk[s2].z = pack2<bf16>(p[4], p[5]);
@@ -503,7 +517,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
         rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
         rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
       }
-      l_i += halves_sum(rs);
+      l_i += rs;
       // O^T += V^T P^T over PS k-steps of 16 keys.
   #pragma unroll
       for (int s2 = 0; s2 < PS; ++s2) {
@@ -556,6 +570,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
       if (kb + 1 < kb1) zero_tail((kb + 1) * BN, (kb & 1) ^ 1);
     }
 
+    if (wave_active) l_i = halves_sum(l_i);
     if (kb0 == 0 && kb1 == nkb) {
       if (wave_active && qi < S)
         attn_store_row<HD>(o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2, acc, m_i, l_i, hf,
@@ -792,8 +807,8 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   auto K = static_cast<const bf16*>(k);
   auto V = static_cast<const bf16*>(v);
   auto O = static_cast<bf16*>(o);
-  // A usable bound on |q.k| (and no key mask) selects the fixed-reference
-  // kernel; m_fix is its reference max in log2 units.
+  // A usable bound on |q.k| (and no key mask) selects the kernel without a
+  // reference max; the bound on the scaled scores is in log2 units.
   const float m_fix = score_bound > 0.f ? score_bound * sl2 : INFINITY;
   const bool use_fixed = mask_mode == HYDRA_MASK_NONE && m_fix <= 48.f;
   auto go = [&](auto c_tag, auto m_tag, auto f_tag) -> int {
@@ -841,8 +856,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     desc = reinterpret_cast<int4*>(static_cast<char*>(w) + pb);
     kern<<<dim3(static_cast<unsigned>(P)), 64 * NW, 0, st>>>(
         Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, T, per_item ? 1 : 0, part, desc,
-        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2,
-        m_fix);
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2);
     const int rc1 = check_launch("attn_fwd_mfma_kernel");
     if (rc1 != HYDRA_OK || !split) return rc1;
     const int64_t threads = static_cast<int64_t>(P) * NW * 64;
