@@ -410,7 +410,7 @@ def main():
         "config": {"workload": "config 3: CCGQA attention forward, dim 1024, latent 256, 4q/1kv heads "
                                "x hd 64, causal conv k=3, QK-mean, QK-norm tau 1.0, B4 x S4096, bf16",
                    "global_batch": step.B, "seq_len": step.S, "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "attn_fwd_mfma_kernel<64,causal> + attn_merge_kernel<64>", "bound": "mfma",
+        "roofline": {"kernel": "attn_fwd_kp_kernel<64,causal>", "bound": "mfma",
                      "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS,
                      "traffic": measured_traffic("attention_op<64,causal>"),

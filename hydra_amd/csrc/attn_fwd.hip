@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -162,6 +163,113 @@ __device__ __forceinline__ void attn_store_row(bf16* orow, const f32x16_t* acc, 
   if (lse && hf == 0) *lse = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
 }
 
+// One 64-key tile for one wave (32 query rows of one head): S^T = K Q^T from
+// the staged K rows kt (row pitch KROW), the mask (MASKED: keys past S,
+// causality, the key mask kmrow of the batch row), the softmax update of
+// (m_i, l_i, acc) and O^T += V^T P^T from the staged V^T rows vt (pitch
+// VROW).  Lane (n, hf) owns query row qi; l_i is the lane's half of the row
+// sum.  FIXED: Q was pre-scaled by scale * log2(e) and bounded, P = exp2 of
+// the accumulator with no reference max.
+template <int HD, bool CAUSAL, int MASK, bool FIXED, bool MASKED, int KROW, int VROW>
+__device__ __forceinline__ void attn_tile(const uint16_t* kt, const uint16_t* vt, const bf16x8_t* qf,
+                                          f32x16_t* acc, float& m_i, float& l_i, int key0, int qi,
+                                          int S, int n, int hf, const uint8_t* kmrow, float scale_log2) {
+  constexpr int BN = kAttnBN;
+  constexpr int KSTEPS = HD / 16;
+  constexpr int MT = BN / 32;
+  constexpr int PS = BN / 16;
+  constexpr int DT = (HD + 31) / 32;
+  // Lazy rescaling: the running max used for exp2 only moves when a score
+  // exceeds it by more than this (log2 units), so P stays <= 2^8.
+  constexpr float kRescale = 8.f;
+  f32x16_t st[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
+      st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
+    }
+  if constexpr (MASKED) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
+        bool ok = key < S;
+        if (CAUSAL && MASK != 2) ok = ok && key <= qi;
+        if (MASK != 0) {
+          const bool keep = kmrow[min(key, S - 1)] != 0;
+          ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
+        }
+        st[mt][r] = ok ? st[mt][r] : -INFINITY;
+      }
+  }
+  if constexpr (!FIXED) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+    mx = halves_max(mx) * scale_log2;  // scaled row max of this tile
+    // Move the reference max only when this tile would push P past 2^8; the
+    // test is made wave-uniform so the common case is one skipped branch.
+    if (__any(mx > m_i + kRescale)) {
+      const bool move = mx > m_i + kRescale;
+      // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
+      // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
+      const float m_new = move ? mx : m_i;
+      l_i *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+      m_i = m_new;
+    }
+  }
+  const float m_use = FIXED || m_i == -INFINITY ? 0.f : m_i;
+  // P in bf16, and its row sum from the same rounded values (v_dot2 with
+  // (1, 1)), so the normalisation uses exactly the P of the PV product.
+  uint4 pk[PS];
+  float rs = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < PS; ++s2) {
+    const int mt = s2 >> 1, rb = 8 * (s2 & 1);
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      p[e] = FIXED ? __builtin_amdgcn_exp2f(st[mt][rb + e])
+                   : __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
+    pk[s2].x = pack2<bf16>(p[0], p[1]);
+    pk[s2].y = pack2<bf16>(p[2], p[3]);
+    pk[s2].z = pack2<bf16>(p[4], p[5]);
+    pk[s2].w = pack2<bf16>(p[6], p[7]);
+    rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
+    rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
+    rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
+    rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
+  }
+  l_i += rs;
+  // O^T += V^T P^T over PS k-steps of 16 keys.
+#pragma unroll
+  for (int s2 = 0; s2 < PS; ++s2) {
+    const bf16x8_t pf = as_bf16x8(pk[s2]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint16_t* vr = &vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
+      const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+      const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+      const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
+    }
+  }
+}
+
 template <int HD, bool CAUSAL, int MASK, bool VT, int NW, bool FIXED>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -177,8 +285,6 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   // V is [.., S, hd] and is transposed while staged.
   constexpr int BN = kAttnBN;           // keys per tile
   constexpr int KSTEPS = HD / 16;       // k-steps of S^T = K Q^T
-  constexpr int MT = BN / 32;           // 32-key row tiles of S^T
-  constexpr int PS = BN / 16;           // 16-key k-steps of O^T = V^T P^T
   constexpr int DT = (HD + 31) / 32;    // 32-row d tiles of O^T
   // LDS rows are padded by one 16-byte slot (8 elements) so that the MFMA
   // operand reads of 16 consecutive rows hit distinct banks.  K (and V^T
@@ -196,9 +302,6 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   constexpr int KBUF = BN * KROW;                   // BN * KSL slots
   constexpr int KINS = BN * KSL / 64;               // K load instructions per tile
   constexpr int VBUF = (VT && VINS * 512 > DT * 32 * VROW) ? VINS * 512 : DT * 32 * VROW;
-  // Lazy rescaling: the running max used for exp2 only moves when a score
-  // exceeds it by more than this (log2 units), so P stays <= 2^8.
-  constexpr float kRescale = 8.f;
   // FIXED: the caller bounds |q.k| by beta with beta * scale <= 48 in log2
   // units, so exp2 of a scaled score lies in [2^-48, 2^48] and needs no
   // reference max at all (P, l and O stay far inside the bf16 / fp32 range):
@@ -436,101 +539,14 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   #pragma unroll
       for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-    // One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is
-    // compile-time, so the tiles that are fully visible to every wave of the
-    // workgroup run with no mask code at all.
+    // One key tile.  MASKED is compile-time, so the tiles that are fully
+    // visible to every wave of the workgroup run with no mask code at all.
+    const uint8_t* kmrow = MASK != 0 ? kmask + static_cast<int64_t>(b) * S : nullptr;
     auto tile = [&](int kb, auto masked_tag) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       const int buf = kb & 1;
-      const int key0 = kb * BN;
-      const uint16_t* kt = Ks + buf * KBUF;
-      const uint16_t* vt = Vt + buf * VBUF;
-      f32x16_t st[MT];
-  #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-  #pragma unroll
-        for (int r = 0; r < 16; ++r) st[mt][r] = 0.f;
-  #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-  #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
-          st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
-        }
-      if constexpr (MASKED) {
-  #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-  #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
-            bool ok = key < S;
-            if (CAUSAL && MASK != 2) ok = ok && key <= qi;
-            if (MASK != 0) {
-              const bool keep = kmask[static_cast<int64_t>(b) * S + min(key, S - 1)] != 0;
-              ok = ok && (MASK == 1 ? keep : (key > qi || !keep));
-            }
-            st[mt][r] = ok ? st[mt][r] : -INFINITY;
-          }
-      }
-      if constexpr (!fixed_max) {
-        float mx = -INFINITY;
-  #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-  #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
-        mx = halves_max(mx) * scale_log2;  // scaled row max of this tile
-        // Move the reference max only when this tile would push P past 2^8; the
-        // test is made wave-uniform so the common case is one skipped branch.
-        if (__any(mx > m_i + kRescale)) {
-          const bool move = mx > m_i + kRescale;
-          // alpha = 0 when m_i = -inf; lanes that keep their max (including rows
-          // with no visible key yet, where m_i - m_i would be NaN) keep alpha = 1.
-          const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
-          const float m_new = move ? mx : m_i;
-          l_i *= alpha;
-  #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-  #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-          m_i = m_new;
-        }
-      }
-      const float m_use = fixed_max || m_i == -INFINITY ? 0.f : m_i;
-      // P in bf16, and its row sum from the same rounded values (v_dot2 with
-      // (1, 1)), so the normalisation uses exactly the P of the PV product.
-      uint4 pk[PS];
-      float rs = 0.f;
-  #pragma unroll
-      for (int s2 = 0; s2 < PS; ++s2) {
-        const int mt = s2 >> 1, rb = 8 * (s2 & 1);
-        float p[8];
-  #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          p[e] = fixed_max ? __builtin_amdgcn_exp2f(st[mt][rb + e])
-                           : __builtin_amdgcn_exp2f(fmaf(st[mt][rb + e], scale_log2, -m_use));
-        pk[s2].x = pack2<bf16>(p[0], p[1]);
-        pk[s2].y = pack2<bf16>(p[2], p[3]);
-        pk[s2].z = pack2<bf16>(p[4], p[5]);
-        pk[s2].w = pack2<bf16>(p[6], p[7]);
-        rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
-        rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
-        rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
-        rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
-      }
-      l_i += rs;
-      // O^T += V^T P^T over PS k-steps of 16 keys.
-  #pragma unroll
-      for (int s2 = 0; s2 < PS; ++s2) {
-        const bf16x8_t pf = as_bf16x8(pk[s2]);
-  #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const uint16_t* vr = &vt[(32 * dt + n) * VROW + 16 * s2 + 4 * hf];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
-          const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf, acc[dt], 0, 0, 0);
-        }
-      }
+      attn_tile<HD, CAUSAL, MASK, FIXED, MASKED, KROW, VROW>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i, l_i,
+                                                            kb * BN, qi, S, n, hf, kmrow, scale_log2);
     };
 
 
@@ -601,6 +617,232 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
     }
   }
   if (!started && tid == 0) desc[blockIdx.x] = make_int4(0, 0, 0, 0);
+}
+
+// Key-split workgroups (V^T rows only).  A workgroup of KP x NW waves takes
+// one item whole -- NW tasks, as in attn_fwd_mfma_kernel -- and its KP groups
+// of NW waves walk the item's key tiles in turn (group g: tiles g, g + KP,
+// ..), each group staging its own tiles in LDS, one barrier per step.  At
+// the end, groups 1.. KP-1 leave (O, m, l) in LDS and group 0 folds them in
+// group order and writes the rows.  Every item is one workgroup, longest
+// first: no chunk partials and no merge kernel, and the longest item takes
+// KP-fold fewer steps, which is what balances the causal triangle when
+// there are few items.
+template <int HD, bool CAUSAL, int MASK, int NW, int KP, bool FIXED>
+__global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH,
+    int64_t qs0, int64_t qs1, int64_t qs2,
+    int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2,
+    int64_t os0, int64_t os1, int64_t os2, float scale_log2) {
+  constexpr int BN = kAttnBN;
+  constexpr int KSTEPS = HD / 16;
+  constexpr int DT = (HD + 31) / 32;
+  constexpr int DC = HD / 8;             // 16-byte chunks per K row
+  constexpr int KSL = DC + 1;            // LDS slots per K row (one pad slot)
+  constexpr int KROW = 8 * KSL;
+  constexpr int VSL = BN / 8 + 1;        // LDS slots per V^T row
+  constexpr int VROW = 8 * VSL;
+  constexpr int VINS = (HD * VSL + 63) / 64;
+  constexpr int KBUF = BN * KROW;
+  constexpr int KINS = BN * KSL / 64;
+  constexpr int VBUF = VINS * 512 > DT * 32 * VROW ? VINS * 512 : DT * 32 * VROW;
+  constexpr int KIPW = (KINS + NW - 1) / NW;
+  constexpr int VIPW = (VINS + NW - 1) / NW;
+  constexpr int GBUF = 2 * (KBUF + VBUF);  // a group's double-buffered K and V^T (elements)
+  constexpr int NT = 64 * NW * KP;
+  constexpr int XF = DT * 16 + 2;          // exchanged floats per lane: O, m, l
+  static_assert((KP - 1) * NW * 64 * XF * 4 <= KP * GBUF * 2, "the exchange fits in the tile buffers");
+  constexpr uint32_t kOob = 0x80000000u;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[KP * GBUF];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wv / NW, wq = wv - grp * NW;  // key group, task within the item
+  const int n = lane & 31, hf = lane >> 5;
+  const bool walk = CAUSAL && MASK != 2;
+  const int p = blockIdx.x / BH, bk = blockIdx.x - p * BH;
+  const int wg = attn_pos_item(p, nwg, false);
+  const int nkb = attn_tiles<NW>(wg, S, G, ntasks, walk);
+  const int b = bk / Hkv, kvh = bk - b * Hkv;
+  const int task = wg * NW + wq;
+  const bool active = task < ntasks;
+  const int qb = task / G;
+  const int h = kvh * G + (task - qb * G);
+  const int q0 = qb * 32, qi = q0 + n;
+  const bf16* kbase = k + b * ks0 + kvh * ks1;
+  const bf16* vbase = v + b * vs0 + kvh * vs1;
+  uint16_t* Ks = smem + grp * GBUF;
+  uint16_t* Vt = Ks + 2 * KBUF;
+
+  if constexpr (DT * 32 > HD) {  // zero the padding rows of every V^T buffer once
+    constexpr int PADE = (DT * 32 - HD) * VROW;
+    for (int i = tid; i < KP * 2 * PADE; i += NT) {
+      const int bu = i / PADE, r = i - bu * PADE;
+      smem[(bu >> 1) * GBUF + 2 * KBUF + (bu & 1) * VBUF + HD * VROW + r] = 0;
+    }
+  }
+  // Per-lane byte offsets within a tile (fixed for the kernel): K slot
+  // P = 64j + lane <-> (key row P / KSL, chunk P % KSL); V^T slot P <-> (d row
+  // P / VSL, 8-key chunk P % VSL); pad slots and slots past the tile get an
+  // offset past num_records and load zeros.
+  uint32_t koffs[KIPW];
+#pragma unroll
+  for (int i = 0; i < KIPW; ++i) {
+    const int j = wq + NW * i, P = 64 * j + lane;
+    const int r = P / KSL, c = P - r * KSL;
+    koffs[i] = (j < KINS && c < DC) ? static_cast<uint32_t>((r * ks2 + c * 8) * 2) : kOob;
+  }
+  uint32_t vtoffs[VIPW];
+  int vtkey[VIPW];  // first key of the slot's chunk (BN for pad slots)
+#pragma unroll
+  for (int i = 0; i < VIPW; ++i) {
+    const int j = wq + NW * i, P = 64 * j + lane;
+    const int d = P / VSL, c = P - d * VSL;
+    const bool ok = j < VINS && d < HD && c < BN / 8;
+    vtoffs[i] = ok ? static_cast<uint32_t>((d * vs2 + 8 * c) * 2) : kOob;
+    vtkey[i] = ok ? 8 * c : BN;
+  }
+  const uint32_t ks_lds = lds_addr(Ks), vt_lds = lds_addr(Vt);
+
+  // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7];
+  // FIXED: scaled by scale * log2(e) and rounded to bf16 once.
+  bf16x8_t qf[KSTEPS];
+  {
+    const bf16* qrow = q + b * qs0 + h * qs1 + static_cast<int64_t>(qi) * qs2;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (active && qi < S) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
+      if constexpr (FIXED) {
+        uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack2<bf16>(__uint_as_float(w[e] << 16) * scale_log2,
+                             __uint_as_float(w[e] & 0xffff0000u) * scale_log2);
+        raw = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      qf[s] = as_bf16x8(raw);
+    }
+  }
+
+  // The group's loads of tile kb into its buffer buf.  Keys at or past S
+  // (last tile only; S % 8 == 0 on this path) load as zeros: K rows through
+  // num_records, V^T chunks through the lane's offset.
+  auto fetch = [&](int kb, int buf) {
+    const int key0 = kb * BN;
+    const int rows = min(BN, S - key0);
+    const i32x4_t kr = raw_rsrc(kbase + static_cast<int64_t>(key0) * ks2,
+                                static_cast<int>((rows - 1) * ks2 * 2 + HD * 2));
+#pragma unroll
+    for (int i = 0; i < KIPW; ++i) {
+      const int j = wq + NW * i;
+      if (j < KINS) load16_to_lds(kr, ks_lds + (buf * KBUF + 512 * j) * 2, koffs[i]);
+    }
+    const i32x4_t vr = raw_rsrc(vbase + key0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2));
+    if (key0 + BN <= S) {
+#pragma unroll
+      for (int i = 0; i < VIPW; ++i) {
+        const int j = wq + NW * i;
+        if (j < VINS) load16_to_lds(vr, vt_lds + (buf * VBUF + 512 * j) * 2, vtoffs[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VIPW; ++i) {
+        const int j = wq + NW * i;
+        if (j < VINS)
+          load16_to_lds(vr, vt_lds + (buf * VBUF + 512 * j) * 2, key0 + vtkey[i] < S ? vtoffs[i] : kOob);
+      }
+    }
+  };
+  auto land = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads, LDS writes included
+    __syncthreads();
+  };
+
+  float m_i = FIXED ? 0.f : -INFINITY, l_i = 0.f;
+  f32x16_t acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+
+  // Tiles [0, nfull) are in bounds and at or below the diagonal of every
+  // wave; the rest need the mask.
+  const int wg_qmin = ((wg * NW) / G) * 32;
+  int nfull = 0;
+  if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
+  nfull = min(nfull, nkb);
+  const uint8_t* kmrow = MASK != 0 ? kmask + static_cast<int64_t>(b) * S : nullptr;
+  const int nsteps = (nkb + KP - 1) / KP;
+  // Steps [0, st_full) have every group's tile unmasked; the rest (at most
+  // a few at the end of a causal item) run the masked code for all tiles.
+  // Two loops rather than a per-tile choice: a join of the two tile codes
+  // costs a copy of the accumulators every step.
+  const int st_full = nfull / KP;
+  if (grp < nkb) fetch(grp, 0);
+  land();
+  int st = 0;
+  for (; st < st_full; ++st) {
+    const int kb = st * KP + grp, buf = st & 1;
+    // The group's next tile goes into its other buffer, which the group
+    // finished reading before the barrier that ended the previous step.
+    if (kb + KP < nkb) fetch(kb + KP, buf ^ 1);
+    if (active)
+      attn_tile<HD, CAUSAL, MASK, FIXED, false, KROW, VROW>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i, l_i,
+                                                           kb * BN, qi, S, n, hf, kmrow, scale_log2);
+    land();
+  }
+  for (; st < nsteps; ++st) {
+    const int kb = st * KP + grp, buf = st & 1;
+    if (kb + KP < nkb) fetch(kb + KP, buf ^ 1);
+    if (active && kb < nkb && !(walk && kb * BN > q0 + 31))
+      attn_tile<HD, CAUSAL, MASK, FIXED, true, KROW, VROW>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i, l_i,
+                                                          kb * BN, qi, S, n, hf, kmrow, scale_log2);
+    land();
+  }
+
+  // Fold the groups: the last barrier ended every read of the tile buffers.
+  l_i = halves_sum(l_i);
+  float* xch = reinterpret_cast<float*>(smem);
+  if (grp > 0) {
+    float* xw = xch + static_cast<int64_t>((grp - 1) * NW + wq) * 64 * XF;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xw[(dt * 16 + r) * 64 + lane] = acc[dt][r];
+    xw[(DT * 16) * 64 + lane] = m_i;
+    xw[(DT * 16 + 1) * 64 + lane] = l_i;
+  }
+  __syncthreads();
+  if (grp == 0 && active && qi < S) {
+#pragma unroll
+    for (int g = 1; g < KP; ++g) {
+      const float* xw = xch + static_cast<int64_t>((g - 1) * NW + wq) * 64 * XF;
+      const float m2 = xw[(DT * 16) * 64 + lane], l2 = xw[(DT * 16 + 1) * 64 + lane];
+      if constexpr (FIXED) {
+        l_i += l2;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] += xw[(dt * 16 + r) * 64 + lane];
+      } else if (m2 != -INFINITY) {  // a group that saw no key of this row adds nothing
+        const float mn = fmaxf(m_i, m2);
+        const float s1 = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - mn);
+        const float s2 = __builtin_amdgcn_exp2f(m2 - mn);
+        l_i = fmaf(l2, s2, l_i * s1);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(xw[(dt * 16 + r) * 64 + lane], s2, acc[dt][r] * s1);
+        m_i = mn;
+      }
+    }
+    attn_store_row<HD>(o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2, acc, m_i, l_i, hf,
+                       lse ? lse + (static_cast<int64_t>(b) * Hq + h) * S + qi : nullptr);
+  }
 }
 
 // Combines the chunks of split items.  One thread per (w, wave, lane),
@@ -815,15 +1057,33 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     constexpr bool C = decltype(c_tag)::value;
     constexpr int M = decltype(m_tag)::value;
     constexpr bool FX = decltype(f_tag)::value;
-    auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX> : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>;
     // Schedule.  With at least two items per resident workgroup slot, one
     // workgroup per item (longest first) lets the dispatcher balance the
-    // load; with fewer, stream-K: one resident wave of workgroups, each with
-    // an equal share of the key tiles.  HYDRA_ATTN_WGS=n forces stream-K on
-    // n workgroups, HYDRA_ATTN_WGS=0 one workgroup per item.
+    // load.  With fewer: for V^T rows, key-split workgroups (one item per
+    // workgroup, its key tiles shared by KP groups of waves, no merge pass);
+    // otherwise stream-K, one resident wave of workgroups, each with an
+    // equal share of the key tiles, and a merge pass.  HYDRA_ATTN_SCHED=
+    // streamk or kp forces the V^T choice; HYDRA_ATTN_WGS=n forces stream-K
+    // on n workgroups, HYDRA_ATTN_WGS=0 one workgroup per item.
     const int64_t slots = static_cast<int64_t>(device_cus()) *
-                          blocks_per_cu(reinterpret_cast<const void*>(kern), 64 * NW);
+                          blocks_per_cu(reinterpret_cast<const void*>(
+                                            vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX>
+                                               : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>),
+                                        64 * NW);
     const int64_t items = static_cast<int64_t>(nwg) * BH;
+    const char* sched = getenv("HYDRA_ATTN_SCHED");
+    bool kp = vt && items < 2 * slots;
+    if (sched && strcmp(sched, "streamk") == 0) kp = false;
+    if (sched && strcmp(sched, "kp") == 0) kp = vt;
+    if (getenv("HYDRA_ATTN_WGS")) kp = false;
+    if (kp) {
+      constexpr int KP = HD == 128 ? 2 : 3;  // key groups (LDS: KP double-buffered K/V^T tiles)
+      attn_fwd_kp_kernel<HD, C, M, NW, KP, FX><<<dim3(static_cast<unsigned>(nwg * BH)), 64 * NW * KP, 0, st>>>(
+          Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, qs[0], qs[1], qs[2], ks[0], ks[1],
+          ks[2], vs[0], vs[1], vs[3], os[0], os[1], os[2], sl2);
+      return check_launch("attn_fwd_kp_kernel");
+    }
+    auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX> : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>;
     int64_t P64 = slots;
     bool per_item = items >= 2 * slots;
     if (const char* e = getenv("HYDRA_ATTN_WGS")) {

@@ -175,6 +175,31 @@ def attention_bruteforce(q, k, v, *, causal=True, mask=None, scale=None):
     return out
 
 
+def attention_key_padding(q, k, v, *, causal=True, mask=None, scale=None):
+    """The same masked softmax as `attention_bruteforce` (key t visible to
+    row s iff (not causal or t <= s) and mask[b, t] != 0; a row with no
+    visible key gives 0), vectorised in fp64 for test sizes the triple loop
+    cannot reach.  Pinned against `attention_bruteforce`."""
+    B, Hq, S, hd = q.shape
+    G = Hq // k.shape[1]
+    sc = (1.0 / math.sqrt(hd)) if scale is None else scale
+    kd = k.double().repeat_interleave(G, 1)
+    vd = v.double().repeat_interleave(G, 1)
+    logits = (q.double() @ kd.transpose(-1, -2)) * sc
+    vis = torch.ones(B, 1, S, S, dtype=torch.bool)
+    if causal:
+        vis = vis & torch.ones(S, S, dtype=torch.bool).tril()
+    if mask is not None:
+        vis = vis & (mask != 0).view(B, 1, 1, S)
+    logits = logits.masked_fill(~vis, float("-inf"))
+    mx = logits.amax(-1, keepdim=True)
+    mx = torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx))
+    p = torch.exp(logits - mx)
+    den = p.sum(-1, keepdim=True)
+    p = torch.where(den > 0, p / torch.where(den > 0, den, torch.ones_like(den)), torch.zeros_like(p))
+    return p @ vd
+
+
 def forward(params: dict, x: torch.Tensor, cfg: CCGQAConfig, mask=None):
     """CCGQAAttention.forward (attention.py:201-331)."""
     B, S, _ = x.shape

@@ -93,7 +93,7 @@ def test_attention_key_padding_mode(cuda, dtype):
     mask[:, 0] = 1
     out, _ = attention_forward(*(t.to(cuda, dtype) for t in (q, k, v)), causal=True,
                                key_mask=mask.to(cuda), mask_mode=MASK_KEY_PADDING)
-    ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
+    ref = occ.attention_key_padding(q, k, v, causal=True, mask=mask)
     assert max_rel_err(out.cpu(), ref) < (1e-5 if dtype == torch.float32 else 2e-2)
 
 
@@ -149,13 +149,19 @@ def test_attention_deterministic(cuda):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("sched", [None, "streamk"])
 @pytest.mark.parametrize("case", [(4, 4, 1, 512, 64), (2, 8, 2, 256, 16), (1, 4, 4, 136, 32), (1, 2, 1, 64, 128)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_v_transposed_layout(cuda, case, causal):
+def test_attention_v_transposed_layout(cuda, monkeypatch, case, causal, sched):
     """V handed over as [B,Hkv,hd,S] (keys contiguous): the bf16 kernel stages
-    it without a transpose; results equal the row-major V path."""
+    it without a transpose.  Under the stream-K schedule the result equals
+    the row-major V path bit for bit (same kernel, same order); the default
+    key-split schedule folds the keys in another order, within bf16
+    rounding of it."""
     from hydra_amd.attention.backends.ccgqa.ops import attention_forward
 
+    if sched:
+        monkeypatch.setenv("HYDRA_ATTN_SCHED", sched)
     B, Hq, Hkv, S, hd = case
     q, k, v = _qkv(*case, seed=31)
     qd, kd = q.to(cuda, torch.bfloat16), k.to(cuda, torch.bfloat16)
@@ -163,7 +169,10 @@ def test_attention_v_transposed_layout(cuda, case, causal):
     out_t, _ = attention_forward(qd, kd, vt.transpose(2, 3), causal=causal)
     out_r, _ = attention_forward(qd, kd, v.to(cuda, torch.bfloat16), causal=causal)
     assert max_rel_err(out_t.cpu(), occ.attention(q, k, v, causal=causal)) < 2e-2
-    assert torch.equal(out_t.cpu(), out_r.cpu())
+    if sched == "streamk":
+        assert torch.equal(out_t.cpu(), out_r.cpu())
+    else:
+        assert max_rel_err(out_t.cpu(), out_r.float().cpu()) < 2e-2
 
 
 def test_attention_v_transposed_odd_length_generic(cuda):
@@ -217,7 +226,7 @@ def test_attention_split_chunks(cuda, monkeypatch, case, wgs):
     out2, lse2 = attention_forward(dev(q), dev(k), dev(v), **kw)
     assert torch.equal(out, out2) and torch.equal(lse, lse2)
     if mode == "key_padding":
-        ref = occ.attention_bruteforce(q, k, v, causal=causal, mask=mask)
+        ref = occ.attention_key_padding(q, k, v, causal=causal, mask=mask)
     else:
         ref = occ.attention(q, k, v, causal=causal, mask=mask)
     assert max_rel_err(out.cpu(), ref) < 2e-2
@@ -242,7 +251,7 @@ def test_attention_split_fully_masked_rows(cuda, monkeypatch):
                                  key_mask=mask.to(cuda), mask_mode=MASK_KEY_PADDING, want_lse=True)
     assert torch.count_nonzero(out[:, :, :150].cpu()) == 0
     assert torch.isinf(lse[:, :, :150].cpu()).all()
-    ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
+    ref = occ.attention_key_padding(q, k, v, causal=True, mask=mask)
     assert max_rel_err(out[:, :, 150:].cpu(), ref[:, :, 150:]) < 2e-2
 
 
@@ -315,5 +324,104 @@ def test_attention_score_bound_outside_fixed_range(cuda):
     mask[0, 10:90] = 0
     out, _ = attention_forward(dev(q), dev(k), dev(v), causal=True, key_mask=mask.to(cuda),
                                mask_mode=MASK_KEY_PADDING, score_bound=qk_norm_score_bound(2.0))
-    ref = occ.attention_bruteforce(q, k, v, causal=True, mask=mask)
+    ref = occ.attention_key_padding(q, k, v, causal=True, mask=mask)
     assert max_rel_err(out.cpu(), ref) < 2e-2
+
+
+def _vt_rows(t):
+    """The same values with the keys contiguous ([.., hd, S] storage), the
+    layout CCGQA's prep kernel writes V in."""
+    return t.transpose(2, 3).contiguous().transpose(2, 3)
+
+
+VT_CASES = [
+    # B, Hq, Hkv, S, hd; S % 8 == 0, so V^T rows are read as they are
+    (4, 4, 1, 520, 64),
+    (2, 8, 2, 136, 16),
+    (1, 4, 4, 264, 32),
+    (2, 8, 1, 104, 128),
+    (1, 4, 2, 8, 64),
+    (3, 6, 3, 72, 16),
+    (1, 8, 1, 1000, 64),
+]
+VT_MODES = [(True, "none"), (False, "none"), (True, "key_padding"), (False, "key_padding"),
+            (True, "reference")]
+
+
+@pytest.mark.parametrize("sched", ["kp", "streamk"])
+@pytest.mark.parametrize("mode", VT_MODES, ids=[f"{c}-{m}" for c, m in VT_MODES])
+@pytest.mark.parametrize("case", VT_CASES, ids=[str(c) for c in VT_CASES])
+def test_attention_vt_rows_schedules(cuda, monkeypatch, case, mode, sched):
+    """V given as V^T rows: the key-split workgroups (one per item; kp) and
+    the stream-K schedule both give the oracle's result and LSE, for every
+    mask mode, with S not a multiple of the 64-key tile."""
+    from hydra_amd.attention.backends.ccgqa.ops import (MASK_KEY_PADDING, MASK_NONE,
+                                                        MASK_REFERENCE_SDPA, attention_forward)
+
+    causal, mname = mode
+    B, Hq, Hkv, S, hd = case
+    monkeypatch.setenv("HYDRA_ATTN_SCHED", sched)
+    q, k, v = _qkv(B, Hq, Hkv, S, hd, seed=S + hd + 1)
+    mask = None
+    if mname != "none":
+        g = torch.Generator().manual_seed(S + 1)
+        mask = (torch.rand(B, S, generator=g) > 0.25).long()
+        mask[:, 0] = 1
+        mask[0, 1:70] = 0
+    mm = {"none": MASK_NONE, "key_padding": MASK_KEY_PADDING, "reference": MASK_REFERENCE_SDPA}[mname]
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    out, lse = attention_forward(dev(q), dev(k), _vt_rows(dev(v)), causal=causal,
+                                 key_mask=None if mask is None else mask.to(cuda), mask_mode=mm,
+                                 want_lse=True)
+    out2, lse2 = attention_forward(dev(q), dev(k), _vt_rows(dev(v)), causal=causal,
+                                   key_mask=None if mask is None else mask.to(cuda), mask_mode=mm,
+                                   want_lse=True)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    if mname == "key_padding":
+        ref = occ.attention_key_padding(q, k, v, causal=causal, mask=mask)
+    else:
+        ref = occ.attention(q, k, v, causal=causal, mask=mask)
+    assert max_rel_err(out.cpu(), ref) < 2e-2
+    if mname == "none":
+        G = Hq // Hkv
+        logits = (q @ k.repeat_interleave(G, 1).transpose(-1, -2)) / math.sqrt(hd)
+        if causal:
+            logits = logits.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+        assert (lse.cpu() - torch.logsumexp(logits, -1)).abs().max().item() < 2e-2
+
+
+FIXED_VT_CASES = [
+    # B, Hq, Hkv, S, hd, temperature, causal
+    (4, 4, 1, 512, 64, 1.0, True),
+    (2, 8, 2, 304, 16, 4.0, True),
+    (1, 4, 4, 264, 32, 5.66, False),
+    (2, 8, 1, 104, 128, 11.3, True),
+    (1, 2, 1, 64, 64, -8.0, False),
+    (1, 4, 1, 2048, 64, 40.0, True),
+]
+
+
+@pytest.mark.parametrize("sched", ["kp", "streamk"])
+@pytest.mark.parametrize("case", FIXED_VT_CASES, ids=[str(c) for c in FIXED_VT_CASES])
+def test_attention_fixed_vt_rows(cuda, monkeypatch, case, sched):
+    """Bounded scores with V^T rows, under both schedules: oracle result,
+    online-max result and closed-form LSE."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward, qk_norm_score_bound
+
+    B, Hq, Hkv, S, hd, temp, causal = case
+    monkeypatch.setenv("HYDRA_ATTN_SCHED", sched)
+    q, k, v = _normed_qkv(B, Hq, Hkv, S, hd, temp, seed=S + hd + 2)
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    out_f, lse_f = attention_forward(dev(q), dev(k), _vt_rows(dev(v)), causal=causal, want_lse=True,
+                                     score_bound=qk_norm_score_bound(temp))
+    out_o, lse_o = attention_forward(dev(q), dev(k), _vt_rows(dev(v)), causal=causal, want_lse=True)
+    ref = occ.attention(q, k, v, causal=causal)
+    assert max_rel_err(out_f.cpu(), ref) < 2e-2
+    assert max_rel_err(out_o.cpu(), ref) < 2e-2
+    G = Hq // Hkv
+    logits = (q @ k.repeat_interleave(G, 1).transpose(-1, -2)) / math.sqrt(hd)
+    if causal:
+        logits = logits.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    ref_lse = torch.logsumexp(logits, -1)
+    assert (lse_f.cpu() - ref_lse).abs().max().item() < 2e-2
+    assert (lse_f - lse_o).abs().max().item() < 2 ** -7

@@ -255,6 +255,28 @@ def test_attention_bruteforce(causal, use_mask):
     assert max_rel_err(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("use_mask", [False, True])
+def test_attention_key_padding_vectorised(causal, use_mask):
+    """The vectorised key-padding softmax equals the triple loop, including
+    rows that see no key (zeros)."""
+    g = torch.Generator().manual_seed(8)
+    B, Hq, Hkv, S, hd = 2, 6, 2, 11, 8
+    q = torch.randn(B, Hq, S, hd, generator=g)
+    k = torch.randn(B, Hkv, S, hd, generator=g)
+    v = torch.randn(B, Hkv, S, hd, generator=g)
+    mask = None
+    if use_mask:
+        mask = (torch.rand(B, S, generator=g) > 0.4).long()
+        mask[0, :4] = 0  # causal rows 0..3 of batch 0 see no key
+        mask[1, 0] = 1
+    out = occ.attention_key_padding(q, k, v, causal=causal, mask=mask)
+    ref = occ.attention_bruteforce(q, k, v, causal=causal, mask=mask)
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
+    if use_mask and causal:
+        assert torch.count_nonzero(out[0, :, :4]) == 0
+
+
 def test_attention_gqa_equals_repeat_interleave():
     g = torch.Generator().manual_seed(7)
     q = torch.randn(1, 6, 10, 8, generator=g)
