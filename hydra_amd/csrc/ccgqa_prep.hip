@@ -685,8 +685,9 @@ static int launch_prep_mfma(const void* qkv, int64_t qkv_rs, const void* wq1, co
     constexpr int TT = decltype(tt_tag)::value;
     const size_t lds = lds_for(TT);
     auto kern = ccgqa_prep_mfma_kernel<HD, TT>;
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+      return fail(HYDRA_ERR_LAUNCH, "ccgqa_prep: cannot set the kernel's LDS size");
     const dim3 grid(static_cast<unsigned>((S + TT - 1) / TT), static_cast<unsigned>(B));
     kern<<<grid, kPrepThreads, lds, st>>>(
         static_cast<const bf16*>(qkv), qkv_rs, static_cast<const bf16*>(wq1),
@@ -735,8 +736,9 @@ extern "C" int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, in
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
   if (dtype != HYDRA_BF16 || !(hd == 32 || hd == 64 || hd == 128)) return 0;
   int dev = 0, max_lds = 65536;
-  if (hipGetDevice(&dev) == hipSuccess)
-    hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+    max_lds = 65536;
   return prep_mfma_lds(Hq, Hkv, hd, 32) <= static_cast<size_t>(max_lds) ? 1 : 0;
 }
 
@@ -775,8 +777,9 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
       (!(flags & HYDRA_CCGQA_V_TRANSPOSED) || S % 8 == 0);
   if (mfma_ok) {
     int dev = 0, max_lds = 65536;
-    if (hipGetDevice(&dev) == hipSuccess)
-      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      max_lds = 65536;
     int rc = -1;
     switch (hd) {
       case 32: rc = launch_prep_mfma<32>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;

@@ -329,27 +329,31 @@ extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t 
     using ST = decltype(s_tag);
     constexpr int E = decltype(e_tag)::value;
     auto kern = mod_topk_kernel<ST, E>;
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+      return false;
     kern<<<grid, kTopkThreads, lds, st>>>(static_cast<const ST*>(scores), (int)L, s_rs, (int)k,
                                           idx_desc, idx_sorted, mask, mask_dtype);
+    return true;
   };
-  auto by_ept = [&](auto s_tag) {
+  auto by_ept = [&](auto s_tag) -> bool {
     switch (ept) {
-      case 1: go(s_tag, std::integral_constant<int, 1>()); break;
-      case 2: go(s_tag, std::integral_constant<int, 2>()); break;
-      case 4: go(s_tag, std::integral_constant<int, 4>()); break;
-      case 8: go(s_tag, std::integral_constant<int, 8>()); break;
-      default: go(s_tag, std::integral_constant<int, 16>()); break;
+      case 1: return go(s_tag, std::integral_constant<int, 1>());
+      case 2: return go(s_tag, std::integral_constant<int, 2>());
+      case 4: return go(s_tag, std::integral_constant<int, 4>());
+      case 8: return go(s_tag, std::integral_constant<int, 8>());
+      default: return go(s_tag, std::integral_constant<int, 16>());
     }
   };
+  bool set = false;
   switch (score_dtype) {
-    case HYDRA_F32: by_ept(float()); break;
-    case HYDRA_BF16: by_ept(bf16()); break;
-    case HYDRA_F16: by_ept(f16()); break;
+    case HYDRA_F32: set = by_ept(float()); break;
+    case HYDRA_BF16: set = by_ept(bf16()); break;
+    case HYDRA_F16: set = by_ept(f16()); break;
     default:
       return fail(HYDRA_ERR_ARG, "mod_topk: unknown score dtype code");
   }
+  if (!set) return fail(HYDRA_ERR_LAUNCH, "mod_topk: cannot set the kernel's LDS size");
   return check_launch("mod_topk_kernel");
 }
 
