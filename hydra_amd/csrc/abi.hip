@@ -79,10 +79,44 @@ int blocks_per_cu(const void* kernel, int threads) {
   return nb;
 }
 
+// Library-owned scratch: one buffer per (device, slot), grown on demand and
+// never freed (a buffer it outgrows is kept too), so a HIP graph captured
+// with a pointer from here stays valid.  Growing under stream capture is an
+// error.  Calls that use one slot from several streams of a device at once
+// share the buffer and must not overlap.
+int device_workspace(int slot, size_t bytes, hipStream_t st, void** out) {
+  struct Buf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+  };
+  static std::mutex mu;
+  static Buf bufs[64][kWorkspaceSlots];
+  int dev = 0;
+  if (slot < 0 || slot >= kWorkspaceSlots) return fail(HYDRA_ERR_ARG, "workspace: bad slot");
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(HYDRA_ERR_LAUNCH, "workspace: no current device");
+  std::lock_guard<std::mutex> lock(mu);
+  Buf& w = bufs[dev][slot];
+  if (w.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(HYDRA_ERR_UNSUPPORTED,
+                  "workspace: the library's scratch buffer must grow, which cannot happen under "
+                  "graph capture; run the same shape once before capturing");
+    const size_t nb = std::max(bytes, 2 * w.bytes);
+    void* p = nullptr;
+    if (hipMalloc(&p, nb) != hipSuccess) return fail(HYDRA_ERR_LAUNCH, "workspace: allocation failed");
+    w.ptr = p;
+    w.bytes = nb;
+  }
+  *out = w.ptr;
+  return HYDRA_OK;
+}
+
 }  // namespace hydra
 
 extern "C" const char* hydra_last_error(void) {
   return hydra::g_last_error.c_str();
 }
 
-extern "C" int hydra_abi_version(void) { return 101; }
+extern "C" int hydra_abi_version(void) { return 102; }

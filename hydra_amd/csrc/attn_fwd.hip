@@ -985,40 +985,6 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
   if (lse) lse[gid] = l > 0.f ? m + logf(l) : -INFINITY;
 }
 
-// Split-chunk workspace (chunk partials and the merge descriptors), one per
-// device, owned by the library.  It only grows; a buffer it outgrows is kept
-// (never freed), so a HIP graph captured with it stays valid.  Calls that
-// split and run concurrently on one device (different streams) would share
-// it and must not overlap.
-struct AttnWorkspace {
-  void* ptr = nullptr;
-  size_t bytes = 0;
-};
-static std::mutex g_ws_mu;
-static AttnWorkspace g_ws[64];
-
-static int attn_workspace(size_t bytes, hipStream_t st, void** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return fail(HYDRA_ERR_LAUNCH, "attn_fwd: no current device");
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  AttnWorkspace& w = g_ws[dev];
-  if (w.bytes < bytes) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-      return fail(HYDRA_ERR_UNSUPPORTED,
-                  "attn_fwd: the split workspace must grow, which cannot happen under graph "
-                  "capture; run the same shape once before capturing");
-    const size_t nb = std::max(bytes, 2 * w.bytes);
-    void* p = nullptr;
-    if (hipMalloc(&p, nb) != hipSuccess) return fail(HYDRA_ERR_LAUNCH, "attn_fwd: workspace allocation failed");
-    w.ptr = p;
-    w.bytes = nb;
-  }
-  *out = w.ptr;
-  return HYDRA_OK;
-}
-
 template <int HD>
 static int launch_mfma(const void* q, const void* k, const void* v, void* o, float* lse,
                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
@@ -1110,7 +1076,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     // partial slots (stream-K only), then the merge descriptors
     const size_t pb = per_item ? 0 : static_cast<size_t>(2 * P) * NW * 64 * (DT * 8 + 2) * sizeof(float);
     void* w = nullptr;
-    const int rc = attn_workspace(pb + static_cast<size_t>(P) * sizeof(int4), st, &w);
+    const int rc = device_workspace(kWsAttention, pb + static_cast<size_t>(P) * sizeof(int4), st, &w);
     if (rc != HYDRA_OK) return rc;
     part = static_cast<float*>(w);
     desc = reinterpret_cast<int4*>(static_cast<char*>(w) + pb);

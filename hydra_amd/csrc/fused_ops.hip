@@ -4,6 +4,8 @@
 // scalar path for shapes, strides or alignments the vector path cannot take.
 #include "common.h"
 
+#include <algorithm>
+
 namespace hydra {
 
 constexpr int kBlock = 256;  // 4 waves
@@ -135,11 +137,13 @@ static int launch_rms_norm(const void* x, const void* w, void* y, int64_t rows,
 // ===========================================================================
 // RoPE   (reference: _fused_rope_kernel, fused_ops.py:185-237)
 // Output is the contiguous [B,H,S,D] tensor; x may be any strided view.
+// BWD: the gradient with respect to x of the same rotation (its transpose:
+// sin negated), which the reference's CPU path gets from autograd.
 // 16-byte path (rope_hg_kernel): a thread rotates one chunk (E/2 pairs) of
 // HB heads of one row.  Otherwise (rope_scalar_kernel) blockIdx.y = b*H + h
 // and a thread rotates one pair.
 // ===========================================================================
-template <typename T, typename C>
+template <typename T, typename C, bool BWD>
 __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(
     const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
     T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
@@ -154,7 +158,7 @@ __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(
   const T* xr = x + b * xb + h * xh + static_cast<int64_t>(s) * xsr;
   const float x1 = to_f32(xr[(2 * p) * xd]), x2 = to_f32(xr[(2 * p + 1) * xd]);
   const float cv = to_f32(cs[static_cast<int64_t>(s) * cs_rs + p]);
-  const float sv = to_f32(sn[static_cast<int64_t>(s) * cs_rs + p]);
+  const float sv = BWD ? -to_f32(sn[static_cast<int64_t>(s) * cs_rs + p]) : to_f32(sn[static_cast<int64_t>(s) * cs_rs + p]);
   T* o = out + (static_cast<int64_t>(bh) * S + s) * D;
   o[2 * p] = from_f32<T>(x1 * cv - x2 * sv);
   o[2 * p + 1] = from_f32<T>(x1 * sv + x2 * cv);
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(
 // Thread (b, group of HB heads, s, chunk c): the cos/sin chunk is read once
 // and applied to HB heads, whose loads are all issued first (-4% against one
 // head per thread at C2).
-template <typename T, typename C, int HB>
+template <typename T, typename C, int HB, bool BWD>
 __global__ __launch_bounds__(kBlock) void rope_hg_kernel(
     const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
     T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void rope_hg_kernel(
 #pragma unroll
   for (int p = 0; p < E / 2; ++p) {
     cv[p] = to_f32(cr[p]);
-    sv[p] = to_f32(sr[p]);
+    sv[p] = BWD ? -to_f32(sr[p]) : to_f32(sr[p]);
   }
   T* orow = out + (static_cast<int64_t>(b) * H * S + s) * D + c * E;
 #pragma unroll
@@ -208,7 +212,7 @@ __global__ __launch_bounds__(kBlock) void rope_hg_kernel(
   }
 }
 
-template <typename T, typename C>
+template <typename T, typename C, bool BWD>
 static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
                        int64_t B, int64_t H, int64_t S, int64_t D,
                        const int64_t* xs, int64_t cs_rs, hipStream_t st) {
@@ -223,14 +227,14 @@ static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
   const int64_t nthr = B * ((H + 4 - 1) / 4) * S * (D / E);
   if (vec_ok && (nthr + kBlock - 1) / kBlock < (int64_t(1) << 31)) {
     const dim3 grid(static_cast<unsigned>((nthr + kBlock - 1) / kBlock));
-    rope_hg_kernel<T, C, 4><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S, (int)D,
+    rope_hg_kernel<T, C, 4, BWD><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S, (int)D,
                                                     xs[0], xs[1], xs[2], cs_rs, nthr);
     return check_launch("rope_hg_kernel");
   }
   const int64_t threads = S * (D / 2);
   const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock),
                   static_cast<unsigned>(B * H));
-  rope_scalar_kernel<T, C><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S,
+  rope_scalar_kernel<T, C, BWD><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S,
                                                     (int)D, xs[0], xs[1], xs[2],
                                                     xs[3], cs_rs);
   return check_launch("rope_scalar_kernel");
@@ -402,6 +406,400 @@ static int launch_qk_norm(const void* q, const void* k, void* qo, void* ko,
   return check_launch("qk_norm_scalar_kernel");
 }
 
+// ===========================================================================
+// Backward of the fused ops (reference: the PyTorch backward paths of
+// fused_ops.py, which the Triton backward kernels follow): fp32 math, the
+// +-100 clamp, one rounding to the input dtype on store.
+// ===========================================================================
+
+// RMSNorm backward (reference: _rms_norm_backward_pytorch,
+// fused_ops.py:1251-1281; _fused_rms_norm_backward_kernel :1027-1111).  Per
+// row, r = rsqrt(mean(x^2) + eps), xn = x * r, corr = mean(g * w * xn),
+// grad_x = clamp(g * w * r - xn * corr) -- the reference's correction term,
+// as written.  The weight gradient sum over rows of xn * g is folded into
+// the same pass: each lane keeps the sums of its columns over the block's
+// rows, the block reduces them through LDS and writes one fp32 partial row;
+// rms_norm_bwd_w_kernel adds the partial rows in block order (deterministic)
+// and clamps.  The block walks rows [blockIdx.x * RPB + i * gridDim.x * RPB, ..).
+template <typename T, int LPR, int CPL>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ gy,
+    T* __restrict__ gx, float* __restrict__ part, int64_t rows, int nvec, int dim,
+    int64_t x_rs, int64_t gy_rs, int64_t gx_rs, float eps) {
+  constexpr int E = Vec<T>::N;
+  constexpr int RPW = 64 / LPR;                 // rows per wave
+  constexpr int RPB = (kBlock / 64) * RPW;      // rows per block step
+  __shared__ float red[kBlock / 64][RPW][CPL * E * LPR];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, l = lane % LPR;
+  float wf[CPL][E];
+  float accw[CPL][E];
+#pragma unroll
+  for (int v = 0; v < CPL; ++v) {
+    const int vi = l + LPR * v;
+#pragma unroll
+    for (int e = 0; e < E; ++e) accw[v][e] = 0.f;
+    if (vi < nvec) {
+      load16<T>(w + vi * E, wf[v]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) wf[v][e] = 0.f;
+    }
+  }
+  for (int64_t rb = static_cast<int64_t>(blockIdx.x) * RPB; rb < rows;
+       rb += static_cast<int64_t>(gridDim.x) * RPB) {
+    const int64_t row = rb + wave * RPW + sub;
+    const bool live = row < rows;
+    float xf[CPL][E], gf[CPL][E];
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < CPL; ++v) {
+      const int vi = l + LPR * v;
+      if (live && vi < nvec) {
+        load16<T, true>(x + row * x_rs + vi * E, xf[v]);
+        load16<T, true>(gy + row * gy_rs + vi * E, gf[v]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) xf[v][e] = gf[v][e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) ss = fmaf(xf[v][e], xf[v][e], ss);
+    }
+    ss = wave_sum<LPR>(ss);
+    const float r = rsqrtf(ss / static_cast<float>(dim) + eps);
+    float cs = 0.f;
+#pragma unroll
+    for (int v = 0; v < CPL; ++v)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float xn = xf[v][e] * r;
+        cs = fmaf(gf[v][e] * wf[v][e], xn, cs);
+        accw[v][e] = fmaf(xn, gf[v][e], accw[v][e]);
+      }
+    const float corr = wave_sum<LPR>(cs) / static_cast<float>(dim);
+    if (!live) continue;
+#pragma unroll
+    for (int v = 0; v < CPL; ++v) {
+      const int vi = l + LPR * v;
+      if (vi >= nvec) continue;
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float xn = xf[v][e] * r;
+        o[e] = fminf(fmaxf(gf[v][e] * wf[v][e] * r - xn * corr, -100.f), 100.f);
+      }
+      store16<T, true>(gx + row * gx_rs + vi * E, o);
+    }
+  }
+  // Weight-gradient partial of this block: sum over (wave, sub) in order.
+#pragma unroll
+  for (int v = 0; v < CPL; ++v)
+#pragma unroll
+    for (int e = 0; e < E; ++e) red[wave][sub][(v * LPR + l) * E + e] = accw[v][e];
+  __syncthreads();
+  for (int c = threadIdx.x; c < CPL * E * LPR; c += kBlock) {
+    // c = (v * LPR + l) * E + e  <->  column (l + LPR * v) * E + e
+    const int e = c % E, vl = c / E, v = vl / LPR, ll = vl - v * LPR;
+    const int col = (ll + LPR * v) * E + e;
+    if (col >= dim) continue;
+    float s = 0.f;
+    for (int wv = 0; wv < kBlock / 64; ++wv)
+      for (int sb = 0; sb < RPW; ++sb) s += red[wv][sb][c];
+    part[static_cast<int64_t>(blockIdx.x) * dim + col] = s;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_w_kernel(const float* __restrict__ part,
+                                                                 T* __restrict__ gw, int nblk, int dim) {
+  const int col = blockIdx.x * kBlock + threadIdx.x;
+  if (col >= dim) return;
+  float s = 0.f;
+  for (int b = 0; b < nblk; ++b) s += part[static_cast<int64_t>(b) * dim + col];
+  gw[col] = from_f32<T>(fminf(fmaxf(s, -100.f), 100.f));
+}
+
+// Rows of any width / alignment: one wave per row, scalar columns.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_scalar_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ gy,
+    T* __restrict__ gx, float* __restrict__ part, int64_t rows, int dim, int64_t x_rs,
+    int64_t gy_rs, int64_t gx_rs, float eps) {
+  // part [gridDim.x * 4][dim]: one partial row per wave (wave-private, so
+  // no reduction step); rms_norm_bwd_w_kernel adds them in order.
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  const int64_t nw = static_cast<int64_t>(gridDim.x) * (kBlock / 64);
+  float* pw = part + wid * dim;
+  for (int c = lane; c < dim; c += 64) pw[c] = 0.f;
+  for (int64_t row = wid; row < rows; row += nw) {
+    const T* xr = x + row * x_rs;
+    const T* gr = gy + row * gy_rs;
+    float ss = 0.f;
+    for (int c = lane; c < dim; c += 64) {
+      const float f = to_f32(xr[c]);
+      ss = fmaf(f, f, ss);
+    }
+    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(dim) + eps);
+    float cs = 0.f;
+    for (int c = lane; c < dim; c += 64)
+      cs = fmaf(to_f32(gr[c]) * to_f32(w[c]), to_f32(xr[c]) * r, cs);
+    const float corr = wave_sum(cs) / static_cast<float>(dim);
+    for (int c = lane; c < dim; c += 64) {
+      const float xn = to_f32(xr[c]) * r, g = to_f32(gr[c]);
+      gx[row * gx_rs + c] = from_f32<T>(fminf(fmaxf(g * to_f32(w[c]) * r - xn * corr, -100.f), 100.f));
+      pw[c] = fmaf(xn, g, pw[c]);
+    }
+  }
+}
+
+template <typename T, int LPR, int CPL>
+static int launch_rms_bwd_vec(const T* X, const T* W, const T* GY, T* GX, T* GW, int64_t rows, int nvec,
+                              int dim, int64_t x_rs, int64_t gy_rs, int64_t gx_rs, float eps,
+                              hipStream_t st) {
+  constexpr int RPB = (kBlock / 64) * (64 / LPR);
+  // A fixed number of blocks (from the shape only), so the summation order
+  // of the weight gradient does not depend on the device.
+  const int nblk = static_cast<int>(std::min<int64_t>((rows + RPB - 1) / RPB, 512));
+  void* ws = nullptr;
+  const int rc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(nblk) * dim * sizeof(float), st, &ws);
+  if (rc != HYDRA_OK) return rc;
+  auto part = static_cast<float*>(ws);
+  rms_norm_bwd_kernel<T, LPR, CPL><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, nvec, dim, x_rs,
+                                                                 gy_rs, gx_rs, eps);
+  const int rc1 = check_launch("rms_norm_bwd_kernel");
+  if (rc1 != HYDRA_OK) return rc1;
+  rms_norm_bwd_w_kernel<T><<<dim3((dim + kBlock - 1) / kBlock), kBlock, 0, st>>>(part, GW, nblk, dim);
+  return check_launch("rms_norm_bwd_w_kernel");
+}
+
+template <typename T>
+static int launch_rms_norm_bwd(const void* x, const void* w, const void* gy, void* gx, void* gw,
+                               int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs, int64_t gx_rs,
+                               float eps, hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  auto X = static_cast<const T*>(x);
+  auto W = static_cast<const T*>(w);
+  auto GY = static_cast<const T*>(gy);
+  auto GX = static_cast<T*>(gx);
+  auto GW = static_cast<T*>(gw);
+  const bool vec_ok = dim % E == 0 && x_rs % E == 0 && gy_rs % E == 0 && gx_rs % E == 0 && aligned16(x) &&
+                      aligned16(w) && aligned16(gy) && aligned16(gx);
+  const int nvec = static_cast<int>(dim / E);
+  if (vec_ok && nvec <= 64 * 4) {
+    int lpr = 64;
+    for (int cand : {64, 32, 16, 8, 4}) {
+      if (nvec % cand == 0 && nvec / cand <= 4) {
+        lpr = cand;
+        break;
+      }
+    }
+    const int cpl = (nvec + lpr - 1) / lpr;
+#define HYDRA_RMSB_CASE(LP, CP)                                                                           \
+  if (lpr == LP && cpl <= CP)                                                                             \
+    return launch_rms_bwd_vec<T, LP, CP>(X, W, GY, GX, GW, rows, nvec, (int)dim, x_rs, gy_rs, gx_rs, eps, st);
+    HYDRA_RMSB_CASE(4, 1) HYDRA_RMSB_CASE(4, 2) HYDRA_RMSB_CASE(4, 4)
+    HYDRA_RMSB_CASE(8, 1) HYDRA_RMSB_CASE(8, 2) HYDRA_RMSB_CASE(8, 4)
+    HYDRA_RMSB_CASE(16, 1) HYDRA_RMSB_CASE(16, 2) HYDRA_RMSB_CASE(16, 4)
+    HYDRA_RMSB_CASE(32, 1) HYDRA_RMSB_CASE(32, 2) HYDRA_RMSB_CASE(32, 3) HYDRA_RMSB_CASE(32, 4)
+    HYDRA_RMSB_CASE(64, 1) HYDRA_RMSB_CASE(64, 2) HYDRA_RMSB_CASE(64, 3) HYDRA_RMSB_CASE(64, 4)
+#undef HYDRA_RMSB_CASE
+  }
+  const int nblk = static_cast<int>(std::min<int64_t>((rows + 3) / 4, 128));
+  void* ws = nullptr;
+  const int rc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(nblk) * 4 * dim * sizeof(float), st, &ws);
+  if (rc != HYDRA_OK) return rc;
+  auto part = static_cast<float*>(ws);
+  rms_norm_bwd_scalar_kernel<T><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, (int)dim, x_rs, gy_rs,
+                                                              gx_rs, eps);
+  const int rc1 = check_launch("rms_norm_bwd_scalar_kernel");
+  if (rc1 != HYDRA_OK) return rc1;
+  rms_norm_bwd_w_kernel<T><<<dim3((dim + kBlock - 1) / kBlock), kBlock, 0, st>>>(part, GW, nblk * 4, (int)dim);
+  return check_launch("rms_norm_bwd_w_kernel");
+}
+
+// SwiGLU backward (reference: _swiglu_backward_pytorch, fused_ops.py:926-948;
+// _fused_swiglu_backward_kernel :748-805): s = sigmoid(g),
+// grad_gate = clamp(go * u * s * (1 + g * (1 - s))), grad_up = clamp(go * g * s).
+__device__ __forceinline__ float sigmoid_f32(float g) { return __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
+
+template <typename T, int U>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_vec_kernel(
+    const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ gy, T* __restrict__ gg,
+    T* __restrict__ gu, uint32_t total, uint32_t cpr, int64_t g_rs, int64_t u_rs, int64_t gy_rs,
+    int64_t gg_rs, int64_t gu_rs) {
+  constexpr int E = Vec<T>::N;
+  const uint32_t base = (blockIdx.x * U) * kBlock + threadIdx.x;
+  float gf[U][E], uf[U][E], of[U][E];
+  uint32_t rr[U], cc[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t idx = base + j * kBlock;
+    rr[j] = idx / cpr;
+    cc[j] = idx - rr[j] * cpr;
+    if (idx < total) {
+      load16<T, true>(g + rr[j] * g_rs + cc[j] * E, gf[j]);
+      load16<T, true>(u + rr[j] * u_rs + cc[j] * E, uf[j]);
+      load16<T, true>(gy + rr[j] * gy_rs + cc[j] * E, of[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t idx = base + j * kBlock;
+    if (idx >= total) continue;
+    float a[E], b[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float x = gf[j][e], s = sigmoid_f32(x);
+      a[e] = fminf(fmaxf(of[j][e] * uf[j][e] * (s * (1.f + x * (1.f - s))), -100.f), 100.f);
+      b[e] = fminf(fmaxf(of[j][e] * (x * s), -100.f), 100.f);
+    }
+    store16<T, true>(gg + rr[j] * gg_rs + cc[j] * E, a);
+    store16<T, true>(gu + rr[j] * gu_rs + cc[j] * E, b);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_scalar_kernel(
+    const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ gy, T* __restrict__ gg,
+    T* __restrict__ gu, int64_t total, int64_t hidden, int64_t g_rs, int64_t u_rs, int64_t gy_rs,
+    int64_t gg_rs, int64_t gu_rs) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t r = idx / hidden, c = idx - r * hidden;
+  const float x = to_f32(g[r * g_rs + c]), up = to_f32(u[r * u_rs + c]), o = to_f32(gy[r * gy_rs + c]);
+  const float s = sigmoid_f32(x);
+  gg[r * gg_rs + c] = from_f32<T>(fminf(fmaxf(o * up * (s * (1.f + x * (1.f - s))), -100.f), 100.f));
+  gu[r * gu_rs + c] = from_f32<T>(fminf(fmaxf(o * (x * s), -100.f), 100.f));
+}
+
+template <typename T>
+static int launch_swiglu_bwd(const void* g, const void* u, const void* gy, void* gg, void* gu, int64_t rows,
+                             int64_t hidden, int64_t g_rs, int64_t u_rs, int64_t gy_rs, int64_t gg_rs,
+                             int64_t gu_rs, hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  constexpr int U = 2;
+  auto G = static_cast<const T*>(g);
+  auto Up = static_cast<const T*>(u);
+  auto GY = static_cast<const T*>(gy);
+  auto GG = static_cast<T*>(gg);
+  auto GU = static_cast<T*>(gu);
+  const int64_t cpr = hidden / E;
+  const int64_t total_vec = rows * cpr;
+  const bool vec_ok = hidden % E == 0 && g_rs % E == 0 && u_rs % E == 0 && gy_rs % E == 0 && gg_rs % E == 0 &&
+                      gu_rs % E == 0 && aligned16(g) && aligned16(u) && aligned16(gy) && aligned16(gg) &&
+                      aligned16(gu) && total_vec < (int64_t(1) << 31);
+  if (vec_ok) {
+    const dim3 grid(static_cast<unsigned>((total_vec + U * kBlock - 1) / (U * kBlock)));
+    swiglu_bwd_vec_kernel<T, U><<<grid, kBlock, 0, st>>>(G, Up, GY, GG, GU, (uint32_t)total_vec, (uint32_t)cpr,
+                                                         g_rs, u_rs, gy_rs, gg_rs, gu_rs);
+    return check_launch("swiglu_bwd_vec_kernel");
+  }
+  const int64_t total = rows * hidden;
+  const dim3 grid(static_cast<unsigned>((total + kBlock - 1) / kBlock));
+  swiglu_bwd_scalar_kernel<T><<<grid, kBlock, 0, st>>>(G, Up, GY, GG, GU, total, hidden, g_rs, u_rs, gy_rs,
+                                                       gg_rs, gu_rs);
+  return check_launch("swiglu_bwd_scalar_kernel");
+}
+
+// QK-norm backward (reference: _qk_norm_backward_pytorch, fused_ops.py:638-672;
+// _fused_qk_norm_backward_kernel :389-471): per row n = max(||x||, 1e-6),
+// xn = x / n, grad = clamp(s / n * (g - xn * <xn, g>)), s = scale (q) or
+// scale * temperature (k).  Rows of q then rows of k, contiguous.
+template <typename T, int LPR>
+__global__ __launch_bounds__(kBlock) void qk_norm_bwd_vec_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ gqo, const T* __restrict__ gko,
+    T* __restrict__ gq, T* __restrict__ gk, int64_t q_rows, int64_t k_rows, float scale, float temp) {
+  constexpr int E = Vec<T>::N;
+  constexpr int HD = LPR * E;
+  const int64_t gt = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  int64_t row = gt / LPR;
+  const int c = static_cast<int>(gt % LPR);
+  const bool is_k = row >= q_rows;
+  if (is_k) row -= q_rows;
+  const bool live = is_k ? row < k_rows : true;
+  float f[E], g[E];
+  float ss = 0.f, dot = 0.f;
+  if (live) {
+    load16<T>((is_k ? k : q) + row * HD + c * E, f);
+    load16<T>((is_k ? gko : gqo) + row * HD + c * E, g);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      ss = fmaf(f[e], f[e], ss);
+      dot = fmaf(f[e], g[e], dot);
+    }
+  }
+  ss = wave_sum<LPR>(ss);
+  dot = wave_sum<LPR>(dot);
+  if (!live) return;
+  const float ninv = 1.f / fmaxf(__builtin_sqrtf(ss), 1e-6f);
+  const float d = dot * ninv;  // <xn, g>
+  const float fac = (is_k ? scale * temp : scale) * ninv;
+  float o[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) o[e] = fminf(fmaxf(fac * (g[e] - f[e] * ninv * d), -100.f), 100.f);
+  store16<T>((is_k ? gk : gq) + row * HD + c * E, o);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void qk_norm_bwd_scalar_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ gqo, const T* __restrict__ gko,
+    T* __restrict__ gq, T* __restrict__ gk, int64_t q_rows, int64_t k_rows, int hd, float scale, float temp) {
+  int64_t row = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const bool is_k = row >= q_rows;
+  if (is_k) row -= q_rows;
+  if (is_k && row >= k_rows) return;
+  const T* xr = (is_k ? k : q) + row * hd;
+  const T* gr = (is_k ? gko : gqo) + row * hd;
+  T* dst = (is_k ? gk : gq) + row * hd;
+  float ss = 0.f, dot = 0.f;
+  for (int i = 0; i < hd; ++i) {
+    const float f = to_f32(xr[i]);
+    ss = fmaf(f, f, ss);
+    dot = fmaf(f, to_f32(gr[i]), dot);
+  }
+  const float ninv = 1.f / fmaxf(__builtin_sqrtf(ss), 1e-6f);
+  const float d = dot * ninv;
+  const float fac = (is_k ? scale * temp : scale) * ninv;
+  for (int i = 0; i < hd; ++i)
+    dst[i] = from_f32<T>(fminf(fmaxf(fac * (to_f32(gr[i]) - to_f32(xr[i]) * ninv * d), -100.f), 100.f));
+}
+
+template <typename T>
+static int launch_qk_norm_bwd(const void* q, const void* k, const void* gqo, const void* gko, void* gq,
+                              void* gk, int64_t q_rows, int64_t k_rows, int64_t hd, float scale, float temp,
+                              hipStream_t st) {
+  constexpr int E = Vec<T>::N;
+  auto Q = static_cast<const T*>(q);
+  auto K = static_cast<const T*>(k);
+  auto GQO = static_cast<const T*>(gqo);
+  auto GKO = static_cast<const T*>(gko);
+  auto GQ = static_cast<T*>(gq);
+  auto GK = static_cast<T*>(gk);
+  const int64_t lpr = hd / E;
+  const bool vec_ok = hd % E == 0 && lpr >= 1 && lpr <= 64 && (lpr & (lpr - 1)) == 0 && aligned16(q) &&
+                      aligned16(k) && aligned16(gqo) && aligned16(gko) && aligned16(gq) && aligned16(gk);
+  if (vec_ok) {
+    const int64_t threads = (q_rows + k_rows) * lpr;
+    const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock));
+#define HYDRA_QKNB_CASE(L)                                                                              \
+  case L:                                                                                               \
+    qk_norm_bwd_vec_kernel<T, L><<<grid, kBlock, 0, st>>>(Q, K, GQO, GKO, GQ, GK, q_rows, k_rows, scale, \
+                                                          temp);                                        \
+    return check_launch("qk_norm_bwd_vec_kernel");
+    switch (lpr) {
+      HYDRA_QKNB_CASE(1) HYDRA_QKNB_CASE(2) HYDRA_QKNB_CASE(4) HYDRA_QKNB_CASE(8)
+      HYDRA_QKNB_CASE(16) HYDRA_QKNB_CASE(32) HYDRA_QKNB_CASE(64)
+      default: break;
+    }
+#undef HYDRA_QKNB_CASE
+  }
+  const dim3 grid(static_cast<unsigned>((q_rows + k_rows + kBlock - 1) / kBlock));
+  qk_norm_bwd_scalar_kernel<T><<<grid, kBlock, 0, st>>>(Q, K, GQO, GKO, GQ, GK, q_rows, k_rows, (int)hd, scale,
+                                                        temp);
+  return check_launch("qk_norm_bwd_scalar_kernel");
+}
+
 }  // namespace hydra
 
 using namespace hydra;
@@ -436,9 +834,9 @@ extern "C" int hydra_rope_fwd(const void* x, const void* cos, const void* sin,
   auto st = static_cast<hipStream_t>(stream);
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     switch (cs_dtype) {
-      case HYDRA_F32: return launch_rope<T, float>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
-      case HYDRA_BF16: return launch_rope<T, bf16>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
-      case HYDRA_F16: return launch_rope<T, f16>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
+      case HYDRA_F32: return launch_rope<T, float, false>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
+      case HYDRA_BF16: return launch_rope<T, bf16, false>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
+      case HYDRA_F16: return launch_rope<T, f16, false>(x, cos, sin, out, B, H, S, D, xs, cs_rs, st);
       default: return fail(HYDRA_ERR_ARG, "rope: unknown cos/sin dtype code");
     }
   });
@@ -473,5 +871,82 @@ extern "C" int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out,
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     return launch_qk_norm<T>(q, k, q_out, k_out, q_rows, k_rows, hd, scale,
                              temperature, st);
+  });
+}
+
+extern "C" int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
+                                  void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
+                                  int64_t gx_rs, float eps, int dtype, void* stream) {
+  HYDRA_REQUIRE(rows >= 0 && dim >= 1, "rms_norm_bwd: rows must be >= 0 and dim >= 1");
+  HYDRA_REQUIRE(dim <= (int64_t(1) << 24), "rms_norm_bwd: dim too large");
+  HYDRA_REQUIRE(x_rs >= dim && gy_rs >= dim && gx_rs >= dim, "rms_norm_bwd: row stride smaller than dim");
+  HYDRA_REQUIRE(x && w && grad_y && grad_x && grad_w, "rms_norm_bwd: null pointer");
+  auto st = static_cast<hipStream_t>(stream);
+  if (rows == 0) {
+    const int64_t bytes = dim * dtype_size(dtype);
+    HYDRA_REQUIRE(bytes > 0, "rms_norm_bwd: unknown dtype code");
+    // no rows: the weight gradient is zero (a fill kernel, not a memset, so
+    // the call can sit in a captured graph)
+    return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+      rms_norm_bwd_w_kernel<T><<<dim3((dim + kBlock - 1) / kBlock), kBlock, 0, st>>>(
+          nullptr, static_cast<T*>(grad_w), 0, static_cast<int>(dim));
+      return check_launch("rms_norm_bwd_w_kernel");
+    });
+  }
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_rms_norm_bwd<T>(x, w, grad_y, grad_x, grad_w, rows, dim, x_rs, gy_rs, gx_rs, eps, st);
+  });
+}
+
+extern "C" int hydra_rope_bwd(const void* grad_y, const void* cos, const void* sin, void* grad_x,
+                              int64_t B, int64_t H, int64_t S, int64_t D, const int64_t* gys, int64_t cs_rs,
+                              int dtype, int cs_dtype, void* stream) {
+  HYDRA_REQUIRE(B >= 0 && H >= 0 && S >= 0 && D >= 0, "rope_bwd: negative size");
+  HYDRA_REQUIRE(D % 2 == 0, "rope_bwd: head_dim must be even");
+  HYDRA_REQUIRE(gys != nullptr, "rope_bwd: null stride array");
+  if (B * H * S * D == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(grad_y && cos && sin && grad_x, "rope_bwd: null pointer");
+  HYDRA_REQUIRE(cs_rs >= D / 2, "rope_bwd: cos/sin row stride smaller than head_dim/2");
+  HYDRA_REQUIRE(B * H <= 65535, "rope_bwd: B*H must be <= 65535");
+  HYDRA_REQUIRE(S * D < (int64_t(1) << 31), "rope_bwd: S*D too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    switch (cs_dtype) {
+      case HYDRA_F32: return launch_rope<T, float, true>(grad_y, cos, sin, grad_x, B, H, S, D, gys, cs_rs, st);
+      case HYDRA_BF16: return launch_rope<T, bf16, true>(grad_y, cos, sin, grad_x, B, H, S, D, gys, cs_rs, st);
+      case HYDRA_F16: return launch_rope<T, f16, true>(grad_y, cos, sin, grad_x, B, H, S, D, gys, cs_rs, st);
+      default: return fail(HYDRA_ERR_ARG, "rope_bwd: unknown cos/sin dtype code");
+    }
+  });
+}
+
+extern "C" int hydra_swiglu_bwd(const void* gate, const void* up, const void* grad_y, void* grad_gate,
+                                void* grad_up, int64_t rows, int64_t hidden, int64_t g_rs, int64_t u_rs,
+                                int64_t gy_rs, int64_t gg_rs, int64_t gu_rs, int dtype, void* stream) {
+  HYDRA_REQUIRE(rows >= 0 && hidden >= 0, "swiglu_bwd: negative size");
+  if (rows * hidden == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(gate && up && grad_y && grad_gate && grad_up, "swiglu_bwd: null pointer");
+  HYDRA_REQUIRE(g_rs >= hidden && u_rs >= hidden && gy_rs >= hidden && gg_rs >= hidden && gu_rs >= hidden,
+                "swiglu_bwd: row stride smaller than hidden");
+  HYDRA_REQUIRE((rows * hidden + kBlock - 1) / kBlock < (int64_t(1) << 31), "swiglu_bwd: tensor too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_swiglu_bwd<T>(gate, up, grad_y, grad_gate, grad_up, rows, hidden, g_rs, u_rs, gy_rs, gg_rs,
+                                gu_rs, st);
+  });
+}
+
+extern "C" int hydra_qk_norm_bwd(const void* q, const void* k, const void* grad_qo, const void* grad_ko,
+                                 void* grad_q, void* grad_k, int64_t q_rows, int64_t k_rows, int64_t hd,
+                                 float scale, float temperature, int dtype, void* stream) {
+  HYDRA_REQUIRE(q_rows >= 0 && k_rows >= 0 && hd >= 1, "qk_norm_bwd: bad size");
+  if (q_rows + k_rows == 0) return HYDRA_OK;
+  HYDRA_REQUIRE((q_rows == 0 || (q && grad_qo && grad_q)) && (k_rows == 0 || (k && grad_ko && grad_k)),
+                "qk_norm_bwd: null pointer");
+  HYDRA_REQUIRE((q_rows + k_rows) * hd < (int64_t(1) << 40), "qk_norm_bwd: tensor too large");
+  auto st = static_cast<hipStream_t>(stream);
+  return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_qk_norm_bwd<T>(q, k, grad_qo, grad_ko, grad_q, grad_k, q_rows, k_rows, hd, scale, temperature,
+                                 st);
   });
 }

@@ -6,8 +6,11 @@ kernels of libhydra_amd.so.  The flag names keep the reference's
 "TRITON" spelling so callers need no change; here they mean "the HIP
 library is loaded".
 
-Forward only.  The ops are wrapped in autograd Functions whose backward
-raises, so a training graph fails loudly instead of getting no gradient.
+Autograd: RMSNorm, SwiGLU and QK-norm are autograd Functions whose backward
+runs the HIP backward kernels (the reference's fused backward, same
+formulas, clamps and flags); RoPE, which the reference's Triton path leaves
+untracked, gets the gradient autograd gives through its CPU path, also on
+the GPU.
 """
 from __future__ import annotations
 
@@ -17,7 +20,6 @@ from typing import Tuple
 import torch
 
 from .. import _lib
-from .._autograd import track
 
 try:
     from torch.compiler import disable as compiler_disable
@@ -42,10 +44,14 @@ USE_FUSED_ROPE = USE_TRITON_KERNELS and _env_on("HYDRA_ENABLE_FUSED_ROPE", "1") 
 USE_FUSED_QK_NORM = USE_TRITON_KERNELS
 USE_FUSED_SWIGLU = USE_TRITON_KERNELS
 USE_FUSED_RMS_NORM = USE_TRITON_KERNELS and _env_on("HYDRA_ENABLE_FUSED_RMS_NORM", "1") and not _env_on("HYDRA_DISABLE_FUSED_RMS_NORM", "0")
-# Backward kernels are not part of this build.
-USE_FUSED_SWIGLU_BACKWARD = False
-USE_FUSED_RMS_NORM_BACKWARD = False
-USE_FUSED_QK_NORM_BACKWARD = False
+# Fused backward switches (fused_ops.py:80-94): default on, env overrides.
+def _bwd_flags(enabled: bool):
+    return (enabled and _env_on("HYDRA_ENABLE_FUSED_SWIGLU_BWD", "1") and not _env_on("HYDRA_DISABLE_FUSED_SWIGLU_BWD", "0"),
+            enabled and _env_on("HYDRA_ENABLE_FUSED_RMS_NORM_BWD", "1") and not _env_on("HYDRA_DISABLE_FUSED_RMS_NORM_BWD", "0"),
+            enabled and _env_on("HYDRA_ENABLE_FUSED_QK_NORM_BWD", "1") and not _env_on("HYDRA_DISABLE_FUSED_QK_NORM_BWD", "0"))
+
+
+USE_FUSED_SWIGLU_BACKWARD, USE_FUSED_RMS_NORM_BACKWARD, USE_FUSED_QK_NORM_BACKWARD = _bwd_flags(USE_TRITON_KERNELS)
 LIGER_CE_AVAILABLE = False
 USE_LIGER_CE = False
 
@@ -57,6 +63,7 @@ def set_use_triton_kernels(enabled: bool) -> None:
     reference does without Triton.  While disabled, the fused_* functions
     raise instead of running: this build has no non-HIP path."""
     global USE_TRITON_KERNELS, USE_FUSED_ROPE, USE_FUSED_QK_NORM, USE_FUSED_SWIGLU, USE_FUSED_RMS_NORM
+    global USE_FUSED_SWIGLU_BACKWARD, USE_FUSED_RMS_NORM_BACKWARD, USE_FUSED_QK_NORM_BACKWARD
     if enabled and not TRITON_AVAILABLE:
         raise RuntimeError("hydra_amd HIP library is not available (build it with __graft_entry__.build())")
     USE_TRITON_KERNELS = bool(enabled)
@@ -64,6 +71,7 @@ def set_use_triton_kernels(enabled: bool) -> None:
     USE_FUSED_QK_NORM = USE_TRITON_KERNELS
     USE_FUSED_SWIGLU = USE_TRITON_KERNELS
     USE_FUSED_RMS_NORM = USE_TRITON_KERNELS and _env_on("HYDRA_ENABLE_FUSED_RMS_NORM", "1") and not _env_on("HYDRA_DISABLE_FUSED_RMS_NORM", "0")
+    USE_FUSED_SWIGLU_BACKWARD, USE_FUSED_RMS_NORM_BACKWARD, USE_FUSED_QK_NORM_BACKWARD = _bwd_flags(USE_TRITON_KERNELS)
 
 
 def get_kernel_status() -> dict:
@@ -92,21 +100,13 @@ def _enabled(flag: bool, name: str) -> None:
             "HYDRA_DISABLE_* env) and this build has no other path")
 
 
-_track = track
 
 
 # ---------------------------------------------------------------------------
 # 1. RoPE (fused_ops.py:240-297)
 # ---------------------------------------------------------------------------
-@compiler_disable
-def fused_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Rotary embedding on interleaved pairs.
-
-    x: [B, n_heads, S, head_dim] (any strides); cos/sin: [1, 1, Smax, hd/2]
-    or [S, hd/2].  Returns a contiguous tensor of x's shape and dtype."""
-    _enabled(USE_FUSED_ROPE, "fused_rope")
-    _lib.require_gpu("fused_rope", x, cos, sin)
-    B, H, S, D = x.shape
+def _rope_cache_2d(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    S, D = x.shape[2], x.shape[3]
     if cos.dim() == 4:
         cos = cos[0, 0, :S, :]
         sin = sin[0, 0, :S, :]
@@ -119,17 +119,84 @@ def fused_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
         cos = cos.contiguous()
     if sin.dtype != cos.dtype:
         sin = sin.to(cos.dtype)
+    return cos, sin
+
+
+def _rope_call(entry: str, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    B, H, S, D = x.shape
+    if x.stride(-1) != 1:
+        x = x.contiguous()
     out = torch.empty((B, H, S, D), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _lib.call("hydra_rope_fwd", x.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(),
+        _lib.call(entry, x.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(),
                   B, H, S, D, _lib.strides(x), cos.stride(0), _lib.dtype_code(x),
                   _lib.dtype_code(cos), _lib.stream(x))
-    return _track(out, x)
+    return out
+
+
+class _RoPEFunction(torch.autograd.Function):
+    """Forward hydra_rope_fwd; backward hydra_rope_bwd (the rotation's
+    transpose), i.e. the gradient autograd gives through the reference's
+    CPU path (_rope_pytorch, fused_ops.py:300-306)."""
+
+    @staticmethod
+    def forward(ctx, x, cos, sin):
+        ctx.save_for_backward(cos, sin)
+        return _rope_call("hydra_rope_fwd", x, cos, sin)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        cos, sin = ctx.saved_tensors
+        return _rope_call("hydra_rope_bwd", grad_out, cos, sin), None, None
+
+
+@compiler_disable
+def fused_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotary embedding on interleaved pairs.
+
+    x: [B, n_heads, S, head_dim] (any strides); cos/sin: [1, 1, Smax, hd/2]
+    or [S, hd/2].  Returns a contiguous tensor of x's shape and dtype."""
+    _enabled(USE_FUSED_ROPE, "fused_rope")
+    _lib.require_gpu("fused_rope", x, cos, sin)
+    cos, sin = _rope_cache_2d(x, cos, sin)
+    return _RoPEFunction.apply(x, cos, sin)
 
 
 # ---------------------------------------------------------------------------
-# 2. QK-norm (fused_ops.py:474-526)
+# 2. QK-norm (fused_ops.py:474-545)
 # ---------------------------------------------------------------------------
+class _QKNormFunction(torch.autograd.Function):
+    """FusedQKNormFunction (fused_ops.py:496-545): forward hydra_qk_norm_fwd,
+    backward hydra_qk_norm_bwd."""
+
+    @staticmethod
+    def forward(ctx, q, k, scale, temperature):
+        qc, kc = q.contiguous(), k.contiguous()
+        qo, ko = torch.empty_like(qc), torch.empty_like(kc)
+        hd = q.shape[-1]
+        with torch.cuda.device(q.device):
+            _lib.call("hydra_qk_norm_fwd", qc.data_ptr(), kc.data_ptr(), qo.data_ptr(), ko.data_ptr(),
+                      qc.numel() // hd, kc.numel() // hd, hd, float(scale), float(temperature),
+                      _lib.dtype_code(q), _lib.stream(q))
+        ctx.save_for_backward(qc, kc)
+        ctx.scale, ctx.temperature = float(scale), float(temperature)
+        return qo, ko
+
+    @staticmethod
+    def backward(ctx, grad_q_out, grad_k_out):
+        _enabled(USE_FUSED_QK_NORM_BACKWARD, "fused_qk_norm backward")
+        q, k = ctx.saved_tensors
+        gqo = torch.zeros_like(q) if grad_q_out is None else grad_q_out.to(q.dtype).contiguous()
+        gko = torch.zeros_like(k) if grad_k_out is None else grad_k_out.to(k.dtype).contiguous()
+        gq, gk = torch.empty_like(q), torch.empty_like(k)
+        hd = q.shape[-1]
+        with torch.cuda.device(q.device):
+            _lib.call("hydra_qk_norm_bwd", q.data_ptr(), k.data_ptr(), gqo.data_ptr(), gko.data_ptr(),
+                      gq.data_ptr(), gk.data_ptr(), q.numel() // hd, k.numel() // hd, hd, ctx.scale,
+                      ctx.temperature, _lib.dtype_code(q), _lib.stream(q))
+        return gq, gk, None, None
+
+
 @compiler_disable
 def fused_qk_norm(q: torch.Tensor, k: torch.Tensor, scale: float,
                   temperature: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -139,18 +206,11 @@ def fused_qk_norm(q: torch.Tensor, k: torch.Tensor, scale: float,
     _lib.require_gpu("fused_qk_norm", q, k)
     if q.dtype != k.dtype or q.shape[-1] != k.shape[-1]:
         raise ValueError("fused_qk_norm: q and k must share dtype and head_dim")
-    qc, kc = q.contiguous(), k.contiguous()
-    qo, ko = torch.empty_like(qc), torch.empty_like(kc)
-    hd = q.shape[-1]
-    with torch.cuda.device(q.device):
-        _lib.call("hydra_qk_norm_fwd", qc.data_ptr(), kc.data_ptr(), qo.data_ptr(), ko.data_ptr(),
-                  qc.numel() // hd, kc.numel() // hd, hd, float(scale), float(temperature),
-                  _lib.dtype_code(q), _lib.stream(q))
-    return _track(qo, q, k), _track(ko, q, k)
+    return _QKNormFunction.apply(q, k, scale, temperature)
 
 
 # ---------------------------------------------------------------------------
-# 3. SwiGLU (fused_ops.py:808-843)
+# 3. SwiGLU (fused_ops.py:808-862)
 # ---------------------------------------------------------------------------
 def _rows_view(t: torch.Tensor):
     """(rows, row_stride) when t is a 2-D-collapsible view with unit stride on
@@ -170,6 +230,49 @@ def _rows_view(t: torch.Tensor):
     return rows, rs
 
 
+def _as_rows(t: torch.Tensor):
+    """t (or a contiguous copy when its layout does not collapse to rows)
+    with its (rows, row_stride)."""
+    v = _rows_view(t)
+    if v is None:
+        t = t.contiguous()
+        v = _rows_view(t)
+    return t, v
+
+
+class _SwiGLUFunction(torch.autograd.Function):
+    """FusedSwiGLUFunction (fused_ops.py:823-862): forward hydra_swiglu_fwd,
+    backward hydra_swiglu_bwd; gate/up may be the halves of one gate_up."""
+
+    @staticmethod
+    def forward(ctx, gate, up):
+        gate, gv = _as_rows(gate)
+        up, uv = _as_rows(up)
+        hidden = gate.shape[-1] if gate.dim() else 1
+        out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+        with torch.cuda.device(gate.device):
+            _lib.call("hydra_swiglu_fwd", gate.data_ptr(), up.data_ptr(), out.data_ptr(),
+                      gv[0], hidden, gv[1], uv[1], hidden, _lib.dtype_code(gate), _lib.stream(gate))
+        ctx.save_for_backward(gate, up)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        _enabled(USE_FUSED_SWIGLU_BACKWARD, "fused_swiglu backward")
+        gate, up = ctx.saved_tensors
+        _, gv = _as_rows(gate)
+        _, uv = _as_rows(up)
+        go, ov = _as_rows(grad_out.to(gate.dtype))
+        hidden = gate.shape[-1] if gate.dim() else 1
+        gg = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+        gu = torch.empty(up.shape, dtype=up.dtype, device=up.device)
+        with torch.cuda.device(gate.device):
+            _lib.call("hydra_swiglu_bwd", gate.data_ptr(), up.data_ptr(), go.data_ptr(), gg.data_ptr(),
+                      gu.data_ptr(), gv[0], hidden, gv[1], uv[1], ov[1], hidden, hidden,
+                      _lib.dtype_code(gate), _lib.stream(gate))
+        return gg, gu
+
+
 @compiler_disable
 def fused_swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up.  gate/up may be the strided halves of one gate_up
@@ -178,24 +281,48 @@ def fused_swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     _lib.require_gpu("fused_swiglu", gate, up)
     if gate.shape != up.shape or gate.dtype != up.dtype:
         raise ValueError("fused_swiglu: gate and up must have the same shape and dtype")
-    gv, uv = _rows_view(gate), _rows_view(up)
-    if gv is None:
-        gate = gate.contiguous()
-        gv = _rows_view(gate)
-    if uv is None:
-        up = up.contiguous()
-        uv = _rows_view(up)
-    hidden = gate.shape[-1] if gate.dim() else 1
-    out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
-    with torch.cuda.device(gate.device):
-        _lib.call("hydra_swiglu_fwd", gate.data_ptr(), up.data_ptr(), out.data_ptr(),
-                  gv[0], hidden, gv[1], uv[1], hidden, _lib.dtype_code(gate), _lib.stream(gate))
-    return _track(out, gate, up)
+    return _SwiGLUFunction.apply(gate, up)
 
 
 # ---------------------------------------------------------------------------
-# 4. RMSNorm (fused_ops.py:1114-1159)
+# 4. RMSNorm (fused_ops.py:1114-1172)
 # ---------------------------------------------------------------------------
+class _RMSNormFunction(torch.autograd.Function):
+    """FusedRMSNormFunction (fused_ops.py:1135-1172): forward
+    hydra_rms_norm_fwd, backward hydra_rms_norm_bwd.  A weight of another
+    dtype than x is used (and its gradient first rounded) in x's dtype."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        dim = x.shape[-1]
+        w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
+        w = w.contiguous()
+        x, xv = _as_rows(x)
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        with torch.cuda.device(x.device):
+            _lib.call("hydra_rms_norm_fwd", x.data_ptr(), w.data_ptr(), out.data_ptr(),
+                      xv[0], dim, xv[1], dim, float(eps), _lib.dtype_code(x), _lib.stream(x))
+        ctx.save_for_backward(x, w)
+        ctx.eps = float(eps)
+        ctx.w_dtype = weight.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        _enabled(USE_FUSED_RMS_NORM_BACKWARD, "fused_rms_norm backward")
+        x, w = ctx.saved_tensors
+        dim = x.shape[-1]
+        _, xv = _as_rows(x)
+        go, ov = _as_rows(grad_out.to(x.dtype))
+        gx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        gw = torch.empty((dim,), dtype=x.dtype, device=x.device)
+        with torch.cuda.device(x.device):
+            _lib.call("hydra_rms_norm_bwd", x.data_ptr(), w.data_ptr(), go.data_ptr(), gx.data_ptr(),
+                      gw.data_ptr(), xv[0], dim, xv[1], ov[1], dim, ctx.eps, _lib.dtype_code(x),
+                      _lib.stream(x))
+        return gx, gw.to(ctx.w_dtype), None
+
+
 @compiler_disable
 def fused_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """x * rsqrt(mean(x^2, -1) + eps) * weight, fp32 inside, x.dtype out."""
@@ -204,14 +331,4 @@ def fused_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> 
     dim = x.shape[-1]
     if weight.shape != (dim,):
         raise ValueError(f"fused_rms_norm: weight shape {tuple(weight.shape)} != ({dim},)")
-    w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
-    w = w.contiguous()
-    xv = _rows_view(x)
-    if xv is None:
-        x = x.contiguous()
-        xv = _rows_view(x)
-    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    with torch.cuda.device(x.device):
-        _lib.call("hydra_rms_norm_fwd", x.data_ptr(), w.data_ptr(), out.data_ptr(),
-                  xv[0], dim, xv[1], dim, float(eps), _lib.dtype_code(x), _lib.stream(x))
-    return _track(out, x, weight)
+    return _RMSNormFunction.apply(x, weight, eps)

@@ -81,6 +81,57 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
                       int64_t q_rows, int64_t k_rows, int64_t hd,
                       float scale, float temperature, int dtype, void* stream);
 
+/* ---- backward of the fused ops ---------------------------------------- */
+/* Each follows the reference's PyTorch backward (fp32 math, every gradient
+ * clamped to [-100, 100], one rounding into `dtype`), which its Triton
+ * backward kernel reproduces. */
+
+/* RMSNorm backward.  Per row r = rsqrt(mean(x^2) + eps), xn = x * r:
+ *   grad_x = clamp(g * w * r - xn * mean(g * w * xn))
+ *   grad_w = clamp(sum over rows of xn * g)          (fp32 sum, then rounded)
+ * The grad_x correction term is the reference's as written (the exact
+ * derivative carries one more factor r).  Replaces FusedRMSNormFunction.
+ * backward (hydra/kernels/fused_ops.py:1161-1172) with
+ * _rms_norm_backward_pytorch (:1251-1281) / _fused_rms_norm_backward_kernel
+ * (:1027-1111) + the grad_w reduction (:1244-1246).  x, grad_y, grad_x:
+ * [rows, dim] with row strides x_rs, gy_rs, gx_rs; w, grad_w: [dim].  The
+ * weight gradient is summed in a fixed order (deterministic); uses a
+ * library-owned scratch buffer (grown on first use of a shape, so run a
+ * shape once before capturing it in a graph). */
+int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
+                       void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
+                       int64_t gx_rs, float eps, int dtype, void* stream);
+
+/* RoPE backward: grad_x = the rotation of hydra_rope_fwd transposed,
+ *   gx[..,2i] = g[..,2i]*cos + g[..,2i+1]*sin, gx[..,2i+1] = -g[..,2i]*sin + g[..,2i+1]*cos.
+ * The reference's Triton RoPE records no gradient (fused_ops.py:256-297);
+ * this is what autograd gives through its CPU path _rope_pytorch (:300-306).
+ * grad_y: [B,H,S,D] with element strides gys[4] (gys[3] must be 1);
+ * grad_x: contiguous [B,H,S,D]. */
+int hydra_rope_bwd(const void* grad_y, const void* cos, const void* sin, void* grad_x,
+                   int64_t B, int64_t H, int64_t S, int64_t D, const int64_t* gys, int64_t cs_rs,
+                   int dtype, int cs_dtype, void* stream);
+
+/* SwiGLU backward, s = sigmoid(gate):
+ *   grad_gate = clamp(g * up * s * (1 + gate * (1 - s))), grad_up = clamp(g * gate * s).
+ * Replaces FusedSwiGLUFunction.backward (hydra/kernels/fused_ops.py:845-862)
+ * with _swiglu_backward_pytorch (:926-948) / _fused_swiglu_backward_kernel
+ * (:748-805).  All [rows, hidden] with their own row strides (gate/up may be
+ * the halves of one gate_up tensor, grad_gate/grad_up of one grad tensor). */
+int hydra_swiglu_bwd(const void* gate, const void* up, const void* grad_y, void* grad_gate,
+                     void* grad_up, int64_t rows, int64_t hidden, int64_t g_rs, int64_t u_rs,
+                     int64_t gy_rs, int64_t gg_rs, int64_t gu_rs, int dtype, void* stream);
+
+/* QK-norm backward.  Per row n = max(||x||, 1e-6), xn = x / n:
+ *   grad = clamp(s / n * (g - xn * <xn, g>)),  s = scale for q, scale * temperature for k.
+ * Replaces FusedQKNormFunction.backward (hydra/kernels/fused_ops.py:533-545)
+ * with _qk_norm_backward_pytorch (:638-672) / _fused_qk_norm_backward_kernel
+ * (:389-471).  q, grad_qo, grad_q: [q_rows, hd]; k, grad_ko, grad_k:
+ * [k_rows, hd]; all contiguous, same dtype. */
+int hydra_qk_norm_bwd(const void* q, const void* k, const void* grad_qo, const void* grad_ko,
+                      void* grad_q, void* grad_k, int64_t q_rows, int64_t k_rows, int64_t hd,
+                      float scale, float temperature, int dtype, void* stream);
+
 /* ---- CCGQA attention (hydra/attention/backends/ccgqa) ------------------ */
 
 /* Feature bits of hydra_ccgqa_prep_fwd, mirroring the CCGQAAttention ctor

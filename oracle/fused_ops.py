@@ -71,3 +71,68 @@ def rope_cache(head_dim: int, max_seq_len: int, theta: float = 10000.0):
     t = torch.arange(max_seq_len, dtype=torch.float32)
     ang = torch.outer(t, freqs)
     return ang.cos()[None, None], ang.sin()[None, None]
+
+
+# ---------------------------------------------------------------------------
+# Backward of the fused ops (the reference's PyTorch backward paths)
+# ---------------------------------------------------------------------------
+def rms_norm_backward(x: torch.Tensor, weight: torch.Tensor, grad_out: torch.Tensor,
+                      eps: float = 1e-6):
+    """_rms_norm_backward_pytorch (hydra/kernels/fused_ops.py:1251-1281), fp32
+    inside: r = rsqrt(mean(x^2) + eps), x_norm = x * r;
+    grad_w = clamp(sum over rows of x_norm * g, +-100) in weight.dtype;
+    grad_x = clamp(g * w * r - x_norm * mean(g * w * x_norm), +-100) in x.dtype.
+    The correction term is the reference's as written: the exact derivative
+    has one more factor r in it (the two agree when mean(x^2) + eps = 1)."""
+    dim = x.shape[-1]
+    xf = x.reshape(-1, dim).float()
+    wf = weight.float()
+    gf = grad_out.reshape(-1, dim).float()
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    xn = xf * r
+    grad_w = (xn * gf).sum(0).clamp(-100.0, 100.0).to(weight.dtype)
+    corr = (gf * wf * xn).mean(-1, keepdim=True)
+    grad_x = (gf * wf * r - xn * corr).clamp(-100.0, 100.0).to(x.dtype)
+    return grad_x.view(x.shape), grad_w
+
+
+def swiglu_backward(gate: torch.Tensor, up: torch.Tensor, grad_out: torch.Tensor):
+    """_swiglu_backward_pytorch (fused_ops.py:926-948), fp32 inside:
+    s = sigmoid(g); grad_gate = clamp(go * u * s * (1 + g * (1 - s)), +-100);
+    grad_up = clamp(go * g * s, +-100); each in its input's dtype."""
+    g, u, go = gate.float(), up.float(), grad_out.float()
+    s = torch.sigmoid(g)
+    grad_gate = (go * u * (s * (1.0 + g * (1.0 - s)))).clamp(-100.0, 100.0).to(gate.dtype)
+    grad_up = (go * (g * s)).clamp(-100.0, 100.0).to(up.dtype)
+    return grad_gate, grad_up
+
+
+def qk_norm_backward(q: torch.Tensor, k: torch.Tensor, grad_q: torch.Tensor,
+                     grad_k: torch.Tensor, scale: float, temperature: float = 1.0):
+    """_qk_norm_backward_pytorch (fused_ops.py:638-672), fp32 inside, per
+    row: n = max(||x||, 1e-6), xn = x / n,
+    grad = clamp(s / n * (g - xn * <xn, g>), +-100) with s = scale for q and
+    scale * temperature for k; in the inputs' dtype."""
+    def one(x, gx, s):
+        xf, gf = x.float(), gx.float()
+        n = torch.norm(xf, p=2, dim=-1, keepdim=True).clamp(min=1e-6)
+        xn = xf / n
+        dot = (xn * gf).sum(-1, keepdim=True)
+        return (s / n * (gf - xn * dot)).clamp(-100.0, 100.0).to(x.dtype)
+    return one(q, grad_q, scale), one(k, grad_k, scale * temperature)
+
+
+def rope_backward(grad_out: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Gradient of `rope` with respect to x, as autograd gives it through the
+    reference's CPU path (_rope_pytorch, fused_ops.py:300-306; the Triton
+    path records no gradient): each pair rotated back,
+    (g1 c + g2 s, -g1 s + g2 c), fp32 inside, in grad_out.dtype."""
+    S = grad_out.shape[2]
+    if cos.dim() == 2:
+        cos, sin = cos[None, None], sin[None, None]
+    cos = cos[:, :, :S, :].float()
+    sin = sin[:, :, :S, :].float()
+    g = grad_out.float()
+    g1, g2 = g[..., ::2], g[..., 1::2]
+    out = torch.stack([g1 * cos + g2 * sin, -g1 * sin + g2 * cos], dim=-1).flatten(-2)
+    return out.to(grad_out.dtype)

@@ -15,7 +15,8 @@ What it pins (functions whose composition no closed form fixes):
     top-k indices and the mask, on scores with forced ties, plus whether
     torch.topk itself resolves those ties to the lowest index;
   * the CPU fallbacks of the fused ops (hydra/kernels/fused_ops.py:300-306,
-    587-596, 881-883, 1196-1205).
+    587-596, 881-883, 1196-1205) and the RMSNorm backward
+    (fused_ops.py:1251-1281), whose grad_x no closed form pins.
 
 All weights and inputs are rounded to bf16-representable values and stored as
 raw bf16 bit patterns (uint16), so the fp32 and bf16 device paths see the
@@ -152,6 +153,32 @@ def make_fused_ops() -> None:
     print("wrote fused ops")
 
 
+def make_fused_ops_backward() -> None:
+    """_rms_norm_backward_pytorch (hydra/kernels/fused_ops.py:1251-1281): its
+    grad_x correction term is not the exact derivative, so no autograd check
+    pins it; these vectors do.  Rows of x are scaled so mean(x^2) spans ~0.04
+    to ~25 (the term's missing factor is visible), plus rows large enough
+    for the +-100 clamp."""
+    import hydra.kernels.fused_ops as fo
+
+    g = torch.Generator().manual_seed(12)
+    rows, dim = 24, 80
+    scales = torch.cat([torch.full((8,), 0.2), torch.full((8,), 1.0), torch.full((6,), 5.0),
+                        torch.full((2,), 40.0)])
+    x = bf16_round(torch.randn(rows, dim, generator=g) * scales[:, None])
+    w = bf16_round(torch.randn(dim, generator=g))
+    go = bf16_round(torch.randn(rows, dim, generator=g) * 3.0)
+    go[-1] = bf16_round(torch.full((dim,), 900.0))  # a clamped row
+    with torch.no_grad():
+        gx, gw, _ = fo._rms_norm_backward_pytorch(x, w, go, 1e-6, x.shape)
+        np.savez_compressed(
+            HERE / "fused_ops_bwd_cpu.npz",
+            x=bf16_bits(x), w=bf16_bits(w), grad_out=bf16_bits(go), eps=np.array(1e-6),
+            rms_grad_x=gx.numpy(), rms_grad_w=gw.numpy(),
+        )
+    print("wrote fused ops backward")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
@@ -162,6 +189,7 @@ def main() -> None:
     make_ccgqa(ref)
     make_mod()
     make_fused_ops()
+    make_fused_ops_backward()
     (HERE / "VERSIONS.txt").write_text(
         f"torch {torch.__version__}\nnumpy {np.__version__}\nreference {ref} (hydra 0.2.0)\n"
     )

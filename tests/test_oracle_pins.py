@@ -380,3 +380,86 @@ def test_residual_scatter_invariants():
     assert torch.equal(rep[0, 7], y[0, 0]) and torch.equal(rep[0, 2], h[0, 2])
     gth = omod.gather(h, idx)
     assert torch.equal(gth[1, 1], h[1, 9])
+
+
+# ---------------------------------------------------------------------------
+# Backward of the fused ops
+# ---------------------------------------------------------------------------
+def _rms_bwd_golden():
+    d = np.load(GOLDEN / "fused_ops_bwd_cpu.npz")
+    return (bf16_from_bits(d["x"]), bf16_from_bits(d["w"]), bf16_from_bits(d["grad_out"]),
+            float(d["eps"]), torch.from_numpy(d["rms_grad_x"]), torch.from_numpy(d["rms_grad_w"]))
+
+
+def test_rms_norm_backward_golden():
+    """The oracle equals the reference's _rms_norm_backward_pytorch on rows
+    with mean(x^2) from ~0.04 to ~1600 and a clamped row."""
+    x, w, go, eps, gx_ref, gw_ref = _rms_bwd_golden()
+    gx, gw = ofo.rms_norm_backward(x, w, go, eps)
+    assert torch.allclose(gx, gx_ref, rtol=1e-6, atol=1e-6)
+    assert torch.allclose(gw, gw_ref, rtol=1e-6, atol=1e-5)
+    assert gx.abs().max() <= 100.0 and (gx.abs() == 100.0).any()
+
+
+def test_rms_norm_backward_autograd_where_exact():
+    """grad_w is the exact derivative (autograd of F.rms_norm, fp64); grad_x
+    is too on rows with mean(x^2) + eps = 1, where the reference's
+    correction term loses nothing."""
+    g = torch.Generator().manual_seed(21)
+    rows, dim, eps = 6, 48, 1e-6
+    x = torch.randn(rows, dim, generator=g, dtype=torch.float64)
+    x = x / torch.sqrt(x.pow(2).mean(-1, keepdim=True)) * math.sqrt(1.0 - eps)
+    w = torch.randn(dim, generator=g, dtype=torch.float64)
+    go = torch.randn(rows, dim, generator=g, dtype=torch.float64)
+    xa, wa = x.clone().requires_grad_(), w.clone().requires_grad_()
+    F.rms_norm(xa, [dim], weight=wa, eps=eps).backward(go)
+    gx, gw = ofo.rms_norm_backward(x.float(), w.float(), go.float(), eps)
+    assert torch.allclose(gw.double(), wa.grad, rtol=1e-4, atol=1e-4)
+    assert torch.allclose(gx.double(), xa.grad, rtol=1e-4, atol=1e-4)
+    # and off unit RMS the written formula differs from the derivative
+    x2 = x * 3.0
+    xa2 = x2.clone().requires_grad_()
+    F.rms_norm(xa2, [dim], weight=w, eps=eps).backward(go)
+    gx2, _ = ofo.rms_norm_backward(x2.float(), w.float(), go.float(), eps)
+    assert not torch.allclose(gx2.double(), xa2.grad, rtol=1e-2, atol=1e-2)
+
+
+def test_swiglu_backward_autograd_and_clamp():
+    g = torch.Generator().manual_seed(22)
+    gate = torch.randn(5, 33, generator=g, dtype=torch.float64) * 3
+    up = torch.randn(5, 33, generator=g, dtype=torch.float64)
+    go = torch.randn(5, 33, generator=g, dtype=torch.float64)
+    ga, ua = gate.clone().requires_grad_(), up.clone().requires_grad_()
+    (F.silu(ga) * ua).backward(go)
+    gg, gu = ofo.swiglu_backward(gate, up, go)
+    # (the backward computes in fp32, as the reference's does)
+    assert torch.allclose(gg, ga.grad, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(gu, ua.grad, rtol=1e-5, atol=1e-6)
+    gg, gu = ofo.swiglu_backward(gate, up, go * 1e4)
+    assert torch.allclose(gg, (ga.grad * 1e4).clamp(-100, 100), rtol=1e-5, atol=1e-4)
+    assert gu.abs().max() == 100.0
+
+
+def test_qk_norm_backward_autograd():
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(2, 3, 7, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(2, 1, 7, 16, generator=g, dtype=torch.float64) * 4
+    gq = torch.randn_like(q)
+    gk = torch.randn_like(k)
+    qa, ka = q.clone().requires_grad_(), k.clone().requires_grad_()
+    qo, ko = ofo.qk_norm(qa, ka, 2.5, 0.6)
+    torch.autograd.backward([qo, ko], [gq, gk])
+    dq, dk = ofo.qk_norm_backward(q, k, gq, gk, 2.5, 0.6)
+    assert torch.allclose(dq, qa.grad, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(dk, ka.grad, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_backward_autograd():
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(2, 3, 11, 16, generator=g, dtype=torch.float64)
+    go = torch.randn_like(x)
+    cos, sin = ofo.rope_cache(16, 20)
+    xa = x.clone().requires_grad_()
+    ofo.rope(xa, cos.double(), sin.double()).backward(go)
+    gx = ofo.rope_backward(go, cos, sin)
+    assert torch.allclose(gx, xa.grad, rtol=1e-6, atol=1e-6)
