@@ -275,8 +275,60 @@ def bench_fused_ops(dev, iters=60):
     nbytes = 3 * N * H * 2
     res["swiglu"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
     del sets
+    res.update(_bench_fused_backward(dev, g, iters))
     for v in res.values():
         v["pct_peak"] = 100.0 * v["GBs"] / HBM_PEAK_GBS
+    return res
+
+
+def _bench_fused_backward(dev, g, iters):
+    """The backward kernels at the config-2 shapes, called through the C ABI
+    on preallocated buffers (algorithmic bytes: every input read once, every
+    output written once)."""
+    from hydra_amd import _lib
+    from oracle.fused_ops import rope_cache
+
+    res = {}
+    bf = torch.bfloat16
+    N, D, H = 8 * 2048, 768, 2048
+    st = lambda t: _lib.stream(t)
+    # RMSNorm backward [16384, 768]: x, grad_y -> grad_x, grad_w
+    w = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(bf)
+    gw = torch.empty(D, device=dev, dtype=bf)
+    sets = [(torch.randn(N, D, device=dev, generator=g).to(bf), torch.randn(N, D, device=dev, generator=g).to(bf),
+             torch.empty(N, D, device=dev, dtype=bf)) for _ in range(6)]
+    ms = _time_rotating(lambda x, gy, gx: _lib.call(
+        "hydra_rms_norm_bwd", x.data_ptr(), w.data_ptr(), gy.data_ptr(), gx.data_ptr(), gw.data_ptr(),
+        N, D, D, D, D, 1e-6, _lib.dtype_code(x), st(x)), sets, iters)
+    nbytes = 3 * N * D * 2 + 2 * D * 2
+    res["rms_norm_bwd"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
+    del sets
+    # RoPE backward [8,12,2048,64]
+    cos, sin = rope_cache(64, 2048)
+    cos, sin = cos[0, 0].to(dev), sin[0, 0].to(dev)
+    shape = (8, 12, 2048, 64)
+    strides = lambda t: _lib.strides(t)
+    sets = [(torch.randn(*shape, device=dev, generator=g).to(bf), torch.empty(shape, device=dev, dtype=bf))
+            for _ in range(6)]
+    ms = _time_rotating(lambda gy, gx: _lib.call(
+        "hydra_rope_bwd", gy.data_ptr(), cos.data_ptr(), sin.data_ptr(), gx.data_ptr(), 8, 12, 2048, 64,
+        strides(gy), cos.stride(0), _lib.dtype_code(gy), _lib.dtype_code(cos), st(gy)), sets, iters)
+    nbytes = 2 * 8 * 12 * 2048 * 64 * 2 + 2 * 2048 * 32 * 4
+    res["rope_bwd"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
+    del sets
+    # SwiGLU backward: halves of gate_up [16384, 4096], grad_y [16384, 2048]
+    # -> grad_gate_up [16384, 4096]
+    sets = []
+    for _ in range(2):
+        gu = torch.randn(N, 2 * H, device=dev, generator=g).to(bf)
+        gy = torch.randn(N, H, device=dev, generator=g).to(bf)
+        sets.append((gu, gy, torch.empty(N, 2 * H, device=dev, dtype=bf)))
+    ms = _time_rotating(lambda gu, gy, gg: _lib.call(
+        "hydra_swiglu_bwd", gu.data_ptr(), gu[:, H:].data_ptr(), gy.data_ptr(), gg.data_ptr(),
+        gg[:, H:].data_ptr(), N, H, 2 * H, 2 * H, H, 2 * H, 2 * H, _lib.dtype_code(gu), st(gu)), sets, iters)
+    nbytes = 5 * N * H * 2
+    res["swiglu_bwd"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
+    del sets
     return res
 
 

@@ -419,16 +419,18 @@ static int launch_qk_norm(const void* q, const void* k, void* qo, void* ko,
 // as written.  The weight gradient sum over rows of xn * g is folded into
 // the same pass: each lane keeps the sums of its columns over the block's
 // rows, the block reduces them through LDS and writes one fp32 partial row;
-// rms_norm_bwd_w_kernel adds the partial rows in block order (deterministic)
-// and clamps.  The block walks rows [blockIdx.x * RPB + i * gridDim.x * RPB, ..).
-template <typename T, int LPR, int CPL>
+// rms_norm_bwd_w_kernel adds the partial rows in a fixed order
+// (deterministic) and clamps.  The block walks rows
+// [blockIdx.x * RPB + i * gridDim.x * RPB, ..), RI row groups per wave per
+// step with all their loads issued first.
+template <typename T, int LPR, int CPL, int RI>
 __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ gy,
     T* __restrict__ gx, float* __restrict__ part, int64_t rows, int nvec, int dim,
     int64_t x_rs, int64_t gy_rs, int64_t gx_rs, float eps) {
   constexpr int E = Vec<T>::N;
-  constexpr int RPW = 64 / LPR;                 // rows per wave
-  constexpr int RPB = (kBlock / 64) * RPW;      // rows per block step
+  constexpr int RPW = 64 / LPR;                   // rows per wave per group
+  constexpr int RPB = (kBlock / 64) * RPW * RI;   // rows per block step
   __shared__ float red[kBlock / 64][RPW][CPL * E * LPR];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, l = lane % LPR;
@@ -448,47 +450,56 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
   }
   for (int64_t rb = static_cast<int64_t>(blockIdx.x) * RPB; rb < rows;
        rb += static_cast<int64_t>(gridDim.x) * RPB) {
-    const int64_t row = rb + wave * RPW + sub;
-    const bool live = row < rows;
-    float xf[CPL][E], gf[CPL][E];
-    float ss = 0.f;
+    // the RI row groups' loads are all issued before any reduction
+    float xf[RI][CPL][E], gf[RI][CPL][E];
 #pragma unroll
-    for (int v = 0; v < CPL; ++v) {
-      const int vi = l + LPR * v;
-      if (live && vi < nvec) {
-        load16<T, true>(x + row * x_rs + vi * E, xf[v]);
-        load16<T, true>(gy + row * gy_rs + vi * E, gf[v]);
-      } else {
+    for (int g = 0; g < RI; ++g) {
+      const int64_t row = rb + (wave * RI + g) * RPW + sub;
 #pragma unroll
-        for (int e = 0; e < E; ++e) xf[v][e] = gf[v][e] = 0.f;
+      for (int v = 0; v < CPL; ++v) {
+        const int vi = l + LPR * v;
+        if (row < rows && vi < nvec) {
+          load16<T, true>(x + row * x_rs + vi * E, xf[g][v]);
+          load16<T, true>(gy + row * gy_rs + vi * E, gf[g][v]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) xf[g][v][e] = gf[g][v][e] = 0.f;
+        }
       }
-#pragma unroll
-      for (int e = 0; e < E; ++e) ss = fmaf(xf[v][e], xf[v][e], ss);
     }
-    ss = wave_sum<LPR>(ss);
-    const float r = rsqrtf(ss / static_cast<float>(dim) + eps);
-    float cs = 0.f;
 #pragma unroll
-    for (int v = 0; v < CPL; ++v)
+    for (int g = 0; g < RI; ++g) {
+      const int64_t row = rb + (wave * RI + g) * RPW + sub;
+      float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float xn = xf[v][e] * r;
-        cs = fmaf(gf[v][e] * wf[v][e], xn, cs);
-        accw[v][e] = fmaf(xn, gf[v][e], accw[v][e]);
+      for (int v = 0; v < CPL; ++v)
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss = fmaf(xf[g][v][e], xf[g][v][e], ss);
+      ss = wave_sum<LPR>(ss);
+      const float r = rsqrtf(ss / static_cast<float>(dim) + eps);
+      float cs = 0.f;
+#pragma unroll
+      for (int v = 0; v < CPL; ++v)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float xn = xf[g][v][e] * r;
+          cs = fmaf(gf[g][v][e] * wf[v][e], xn, cs);
+          accw[v][e] = fmaf(xn, gf[g][v][e], accw[v][e]);
+        }
+      const float corr = wave_sum<LPR>(cs) / static_cast<float>(dim);
+      if (row >= rows) continue;
+#pragma unroll
+      for (int v = 0; v < CPL; ++v) {
+        const int vi = l + LPR * v;
+        if (vi >= nvec) continue;
+        float o[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float xn = xf[g][v][e] * r;
+          o[e] = fminf(fmaxf(gf[g][v][e] * wf[v][e] * r - xn * corr, -100.f), 100.f);
+        }
+        store16<T, true>(gx + row * gx_rs + vi * E, o);
       }
-    const float corr = wave_sum<LPR>(cs) / static_cast<float>(dim);
-    if (!live) continue;
-#pragma unroll
-    for (int v = 0; v < CPL; ++v) {
-      const int vi = l + LPR * v;
-      if (vi >= nvec) continue;
-      float o[E];
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float xn = xf[v][e] * r;
-        o[e] = fminf(fmaxf(gf[v][e] * wf[v][e] * r - xn * corr, -100.f), 100.f);
-      }
-      store16<T, true>(gx + row * gx_rs + vi * E, o);
     }
   }
   // Weight-gradient partial of this block: sum over (wave, sub) in order.
@@ -509,14 +520,40 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
   }
 }
 
+// Weight gradient from the n partial rows, in one launch: a block of 16
+// waves per 64-column strip, wave w adding partial rows w, w+16, .. (loads
+// unrolled so several are in flight), then the 16 waves' sums in order;
+// clamped.  Deterministic.
+constexpr int kRmsBwdWaves = 16;
 template <typename T>
-__global__ __launch_bounds__(kBlock) void rms_norm_bwd_w_kernel(const float* __restrict__ part,
-                                                                 T* __restrict__ gw, int nblk, int dim) {
-  const int col = blockIdx.x * kBlock + threadIdx.x;
-  if (col >= dim) return;
+__global__ __launch_bounds__(64 * kRmsBwdWaves) void rms_norm_bwd_w_kernel(const float* __restrict__ part,
+                                                                          T* __restrict__ gw, int n, int dim) {
+  __shared__ float red[kRmsBwdWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (int b = 0; b < nblk; ++b) s += part[static_cast<int64_t>(b) * dim + col];
-  gw[col] = from_f32<T>(fminf(fmaxf(s, -100.f), 100.f));
+  if (col < dim) {
+    int r = wave;
+    for (; r + 3 * kRmsBwdWaves < n; r += 4 * kRmsBwdWaves) {
+      const float a = part[static_cast<int64_t>(r) * dim + col];
+      const float b = part[static_cast<int64_t>(r + kRmsBwdWaves) * dim + col];
+      const float c = part[static_cast<int64_t>(r + 2 * kRmsBwdWaves) * dim + col];
+      const float d = part[static_cast<int64_t>(r + 3 * kRmsBwdWaves) * dim + col];
+      s += a;
+      s += b;
+      s += c;
+      s += d;
+    }
+    for (; r < n; r += kRmsBwdWaves) s += part[static_cast<int64_t>(r) * dim + col];
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && col < dim) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRmsBwdWaves; ++w) t += red[w][lane];
+    gw[col] = from_f32<T>(fminf(fmaxf(t, -100.f), 100.f));
+  }
 }
 
 // Rows of any width / alignment: one wave per row, scalar columns.
@@ -553,11 +590,21 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_scalar_kernel(
   }
 }
 
+// The weight gradient from the n partial rows.
+template <typename T>
+static int rms_bwd_reduce_w(const float* part, T* gw, int n, int dim, hipStream_t st) {
+  const int rc0 = check_launch("rms_norm_bwd_kernel");
+  if (rc0 != HYDRA_OK) return rc0;
+  rms_norm_bwd_w_kernel<T><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(part, gw, n, dim);
+  return check_launch("rms_norm_bwd_w_kernel");
+}
+
 template <typename T, int LPR, int CPL>
 static int launch_rms_bwd_vec(const T* X, const T* W, const T* GY, T* GX, T* GW, int64_t rows, int nvec,
                               int dim, int64_t x_rs, int64_t gy_rs, int64_t gx_rs, float eps,
                               hipStream_t st) {
-  constexpr int RPB = (kBlock / 64) * (64 / LPR);
+  constexpr int RI = CPL >= 4 ? 1 : (CPL >= 2 ? 2 : 4);  // row groups per wave per step
+  constexpr int RPB = (kBlock / 64) * (64 / LPR) * RI;
   // A fixed number of blocks (from the shape only), so the summation order
   // of the weight gradient does not depend on the device.
   const int nblk = static_cast<int>(std::min<int64_t>((rows + RPB - 1) / RPB, 512));
@@ -565,12 +612,9 @@ static int launch_rms_bwd_vec(const T* X, const T* W, const T* GY, T* GX, T* GW,
   const int rc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(nblk) * dim * sizeof(float), st, &ws);
   if (rc != HYDRA_OK) return rc;
   auto part = static_cast<float*>(ws);
-  rms_norm_bwd_kernel<T, LPR, CPL><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, nvec, dim, x_rs,
+  rms_norm_bwd_kernel<T, LPR, CPL, RI><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, nvec, dim, x_rs,
                                                                  gy_rs, gx_rs, eps);
-  const int rc1 = check_launch("rms_norm_bwd_kernel");
-  if (rc1 != HYDRA_OK) return rc1;
-  rms_norm_bwd_w_kernel<T><<<dim3((dim + kBlock - 1) / kBlock), kBlock, 0, st>>>(part, GW, nblk, dim);
-  return check_launch("rms_norm_bwd_w_kernel");
+  return rms_bwd_reduce_w(part, GW, nblk, dim, st);
 }
 
 template <typename T>
@@ -612,10 +656,7 @@ static int launch_rms_norm_bwd(const void* x, const void* w, const void* gy, voi
   auto part = static_cast<float*>(ws);
   rms_norm_bwd_scalar_kernel<T><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, (int)dim, x_rs, gy_rs,
                                                               gx_rs, eps);
-  const int rc1 = check_launch("rms_norm_bwd_scalar_kernel");
-  if (rc1 != HYDRA_OK) return rc1;
-  rms_norm_bwd_w_kernel<T><<<dim3((dim + kBlock - 1) / kBlock), kBlock, 0, st>>>(part, GW, nblk * 4, (int)dim);
-  return check_launch("rms_norm_bwd_w_kernel");
+  return rms_bwd_reduce_w(part, GW, nblk * 4, (int)dim, st);
 }
 
 // SwiGLU backward (reference: _swiglu_backward_pytorch, fused_ops.py:926-948;
@@ -888,7 +929,7 @@ extern "C" int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad
     // no rows: the weight gradient is zero (a fill kernel, not a memset, so
     // the call can sit in a captured graph)
     return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
-      rms_norm_bwd_w_kernel<T><<<dim3((dim + kBlock - 1) / kBlock), kBlock, 0, st>>>(
+      rms_norm_bwd_w_kernel<T><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(
           nullptr, static_cast<T*>(grad_w), 0, static_cast<int>(dim));
       return check_launch("rms_norm_bwd_w_kernel");
     });
