@@ -1,25 +1,39 @@
 """ccgqa_attention_fused (hydra/attention/backends/ccgqa/kernels/fused_attention.py:826-840)
-on the gfx950 attention kernel: q [B,H,N,D], k/v [B,Hkv,N,D] -> out [B,H,N,D],
-scale 1/sqrt(D), optional causal mask.  Forward only."""
+on the gfx950 attention kernels: q [B,H,N,D], k/v [B,Hkv,N,D] -> out [B,H,N,D],
+scale 1/sqrt(D), optional causal mask.  CCGQAAttentionFused is an autograd
+Function like the reference's (:638-823): the forward keeps q, k, v, out and
+the fp32 log-sum-exp, the backward runs the HIP split-K backward (dK/dV and
+dQ launches, no atomics)."""
 from __future__ import annotations
 
 import torch
 
-from ....._autograd import track
-from ..ops import attention_forward
+from ..ops import attention_backward, attention_forward
+
+
+class CCGQAAttentionFused(torch.autograd.Function):
+    """fused_attention.py:638-823.  `use_fused_backward` is accepted for the
+    reference's signature; both of its settings run the HIP backward here
+    (the reference's False branch recomputes the same gradients with torch
+    matmuls, :791-821)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal=False, use_fused_backward=True):
+        want = any(ctx.needs_input_grad[:3])
+        out, lse = attention_forward(q, k, v, causal=bool(is_causal), want_lse=want)
+        if want:
+            ctx.save_for_backward(q, k, v, out, lse)
+        ctx.is_causal = bool(is_causal)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = attention_backward(q, k, v, out, lse, grad_out, causal=ctx.is_causal)
+        return dq, dk, dv, None, None
 
 
 def ccgqa_attention_fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           is_causal: bool = False, use_fused_backward: bool = True) -> torch.Tensor:
     """Public API of the fused CCGQA attention (fused_attention.py:826-840)."""
-    with torch.no_grad():
-        out, _ = attention_forward(q.detach(), k.detach(), v.detach(), causal=bool(is_causal))
-    return track(out, q, k, v)
-
-
-class CCGQAAttentionFused:
-    """Name kept for callers of fused_attention.py:638; forward only."""
-
-    @staticmethod
-    def apply(q, k, v, is_causal=False, use_fused_backward=True):
-        return ccgqa_attention_fused(q, k, v, is_causal, use_fused_backward)
+    return CCGQAAttentionFused.apply(q, k, v, is_causal, use_fused_backward)

@@ -138,6 +138,44 @@ def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
     return out, lse
 
 
+def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                       lse: torch.Tensor, grad_out: torch.Tensor, *, causal: bool,
+                       scale: Optional[float] = None):
+    """Gradients (dq, dk, dv) of attention_forward's output, from the forward's
+    inputs, its output and its fp32 log-sum-exp (want_lse=True): the split-K
+    backward of CCGQAAttentionFused (fused_attention.py:706-823, kernels
+    :113-338 and :432-635).  dk and dv sum the Hq/Hkv query heads that share
+    a K/V head.  No key mask (the reference's fused backward has none)."""
+    _lib.require_gpu("attention_backward", q, k, v, out, lse, grad_out)
+    B, Hq, S, hd = q.shape
+    Hkv = k.shape[1]
+    if k.shape != (B, Hkv, S, hd) or v.shape != (B, Hkv, S, hd) or out.shape != q.shape \
+            or grad_out.shape != q.shape:
+        raise ValueError(f"attention_backward: shapes q {tuple(q.shape)}, k {tuple(k.shape)}, "
+                         f"v {tuple(v.shape)}, out {tuple(out.shape)}, grad {tuple(grad_out.shape)}")
+    if Hq % Hkv != 0:
+        raise ValueError("attention_backward: n_heads must be a multiple of n_kv_heads")
+    if not (q.dtype == k.dtype == v.dtype == out.dtype):
+        raise ValueError("attention_backward: q, k, v and out must share a dtype")
+    if lse.shape != (B, Hq, S) or lse.dtype != torch.float32:
+        raise ValueError("attention_backward: lse must be fp32 [B, Hq, S]")
+    q, k, v, out = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v, out))
+    grad_out = grad_out.to(q.dtype)
+    grad_out = grad_out if grad_out.stride(-1) == 1 else grad_out.contiguous()
+    lse = lse.contiguous()
+    dq, dk, dv = torch.empty_like(q, memory_format=torch.contiguous_format), \
+        torch.empty_like(k, memory_format=torch.contiguous_format), \
+        torch.empty_like(v, memory_format=torch.contiguous_format)
+    sc = float(hd ** -0.5) if scale is None else float(scale)
+    with torch.cuda.device(q.device):
+        _lib.call("hydra_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                  grad_out.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                  B, Hq, Hkv, S, hd, _lib.strides(q), _lib.strides(k), _lib.strides(v),
+                  _lib.strides(out), _lib.strides(grad_out), _lib.strides(dq), _lib.strides(dk),
+                  _lib.strides(dv), 1 if causal else 0, sc, _lib.dtype_code(q), _lib.stream(q))
+    return dq, dk, dv
+
+
 def qk_norm_score_bound(temperature: float) -> float:
     """Bound on |q.k| after CCGQAAttention's QK L2-norm (attention.py:260-262):
     q has unit norm and k the norm |temperature|, RoPE is a rotation, and the

@@ -1,0 +1,798 @@
+// CCGQA attention backward on gfx950: the gradients of
+// o = softmax(scale * q k^T [+ causal mask]) v with respect to q, k and v,
+// K/V heads shared by G = Hq/Hkv query heads in repeat_interleave order.
+// Reference semantics: CCGQAAttentionFused.backward
+// (hydra/attention/backends/ccgqa/kernels/fused_attention.py:706-823) and its
+// split-K kernels _bwd_gqa_kv_kernel / _bwd_gqa_dq_kernel (:113-338) and
+// _bwd_kernel / _bwd_dq_kernel (:432-635): P is recomputed from the
+// forward's log-sum-exp, D = rowsum(dO * O), dS = P (dP - D) scale with
+// dP = dO V^T, dV = sum_g P_g^T dO_g, dK = sum_g dS_g^T Q_g, dQ = dS K.
+// fp32 accumulation, one rounding per output, no atomics: every launch is
+// deterministic.
+//
+// Three launches on the bf16 path (v_mfma_f32_32x32x16_bf16):
+//  * attn_bwd_rowdot_kernel: D and lse * log2(e) per query row (fp32).
+//  * attn_bwd_dkdv_kernel: lanes own keys.  A workgroup is 4 waves, KB key
+//    blocks of 32 keys x HG = 4/KB head groups; a step stages 32 query rows
+//    of Q and dO for HG heads in LDS, row-major (A operand of S = Q K^T and
+//    dP = dO V^T) and transposed (A operand of dV^T += dO^T P and
+//    dK^T += Q^T dS), so the KB waves of a head group share each staged
+//    tile.  K and V fragments stay in registers for the whole walk; at the
+//    end the head groups' partial dK/dV are summed through LDS in a fixed
+//    order.  Workgroups start with the lowest keys (the longest causal walks).
+//  * attn_bwd_dq_kernel: lanes own queries, as in the forward: S^T = K Q^T,
+//    dP^T = V dO^T, dQ^T += K^T dS^T; a step stages 64 keys of K and V
+//    (row-major) and K^T in LDS, shared by the 4 query tasks of an item.
+// The MFMA B operand of the PV-type products is taken straight from the
+// score accumulator registers; the A operand is read from the transposed
+// LDS tile in the same (register-order) permutation of the summed index.
+// Generic path (attn_bwd_generic_*): one thread per query / key row, fp32
+// math, any element type, head_dim <= 256.
+#include "common.h"
+
+#include <algorithm>
+
+namespace hydra {
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16_t zero16() {
+  f32x16_t z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) z[r] = 0.f;
+  return z;
+}
+
+// Registers base..base+7 of a C tile as a bf16 B fragment.  Register r of a
+// 32x32 C tile holds row 8(r/4) + 4hf + r%4, so this fragment's 8 k-values
+// are rows 16c + 4hf + 0..3 and 16c + 8 + 4hf + 0..3 (c = base / 8).
+__device__ __forceinline__ uint4 pack_c8(const f32x16_t& x, int base) {
+  return make_uint4(pack2<bf16>(x[base + 0], x[base + 1]), pack2<bf16>(x[base + 2], x[base + 3]),
+                    pack2<bf16>(x[base + 4], x[base + 5]), pack2<bf16>(x[base + 6], x[base + 7]));
+}
+
+// A fragment from a transposed LDS tile t[row][col] (pitch in elements),
+// with the columns in the permutation pack_c8 gives the k index: lane
+// (n, hf) takes row `row`, columns 16c + 4hf + 0..3 and 16c + 8 + 4hf + 0..3.
+__device__ __forceinline__ uint4 lds_a_perm(const uint16_t* t, int row, int pitch, int c, int hf) {
+  const uint16_t* p = t + row * pitch + 16 * c + 4 * hf;
+  const uint2 lo = *reinterpret_cast<const uint2*>(p);
+  const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// Element i of two 16-byte rows a and b as one 32-bit word (a_i | b_i << 16).
+__device__ __forceinline__ uint32_t pair_word(const uint4& a, const uint4& b, int i) {
+  const uint32_t wa = i < 2 ? a.x : i < 4 ? a.y : i < 6 ? a.z : a.w;
+  const uint32_t wb = i < 2 ? b.x : i < 4 ? b.y : i < 6 ? b.z : b.w;
+  return (i & 1) ? (wa >> 16) | (wb & 0xffff0000u) : (wa & 0xffffu) | (wb << 16);
+}
+
+// Writes the 8 d-values of rows 2p and 2p+1 (chunk c) into a transposed tile
+// t[d][row] as 8 words.
+__device__ __forceinline__ void st_pair_t(uint16_t* t, int pitch, int c, int p, const uint4& a,
+                                          const uint4& b) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    *reinterpret_cast<uint32_t*>(&t[(8 * c + i) * pitch + 2 * p]) = pair_word(a, b, i);
+}
+
+__device__ __forceinline__ uint4 ld16_or0(const bf16* p, bool ok) {
+  return ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// D[r] = sum_d dO[r,d] O[r,d] and lse2[r] = lse[r] * log2(e), r = (b*Hq+h)*S+s.
+// TPR threads per row, each a strided set of E-element chunks.
+template <typename T, int TPR, bool VEC>
+__global__ __launch_bounds__(256) void attn_bwd_rowdot_kernel(
+    const T* __restrict__ o, const T* __restrict__ dout, const float* __restrict__ lse,
+    float* __restrict__ dvec, float* __restrict__ lse2, int64_t rows, int Hq, int S, int hd,
+    int64_t os0, int64_t os1, int64_t os2, int64_t ds0, int64_t ds1, int64_t ds2) {
+  constexpr int E = VEC ? 16 / int(sizeof(T)) : 1;
+  const int64_t r = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / TPR;
+  const int sub = threadIdx.x % TPR;
+  float acc = 0.f;
+  if (r < rows) {
+    const int s = static_cast<int>(r % S);
+    const int64_t bh = r / S;
+    const int h = static_cast<int>(bh % Hq);
+    const int64_t b = bh / Hq;
+    const T* orow = o + b * os0 + h * os1 + s * os2;
+    const T* drow = dout + b * ds0 + h * ds1 + s * ds2;
+    for (int e = sub * E; e < hd; e += TPR * E) {
+      if constexpr (VEC) {
+        float a[E], c[E];
+        load16<T>(orow + e, a);
+        load16<T>(drow + e, c);
+#pragma unroll
+        for (int i = 0; i < E; ++i) acc = fmaf(a[i], c[i], acc);
+      } else {
+        acc = fmaf(to_f32(orow[e]), to_f32(drow[e]), acc);
+      }
+    }
+  }
+  acc = wave_sum<TPR>(acc);
+  if (r < rows && sub == 0) {
+    dvec[r] = acc;
+    lse2[r] = lse[r] * kLog2e;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV, lanes own keys (bf16, MFMA).
+template <int HD>
+struct DkdvLayout {
+  static constexpr int QP = HD + 8;          // row-major pitch (elements): 16-byte rows, 4-bank skew
+  static constexpr int TP = 32 + 4;          // transposed pitch (elements)
+  static constexpr int ROWS = 32 * QP;       // one row-major 32-row tile
+  static constexpr int TRS = HD * TP;        // one transposed tile
+  static constexpr int HGE = 2 * ROWS + 2 * TRS + 2 * 32 * 2;  // Q, dO, Q^T, dO^T, lse2, D (elements)
+};
+
+template <int HD, bool CAUSAL, int KB>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
+    bf16* __restrict__ dk, bf16* __restrict__ dv, int Hq, int Hkv, int S, int G,
+    int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
+    int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0, int64_t dvs1, int64_t dvs2,
+    float scale_log2, float scale) {
+  constexpr int HG = 4 / KB;
+  constexpr int KS = HD / 16;   // k-steps over head_dim
+  constexpr int DT = HD / 32;   // 32-row d tiles of dK^T / dV^T
+  constexpr int DC = HD / 8;    // 16-byte chunks per row
+  using L = DkdvLayout<HD>;
+  constexpr int STAGE = HG * L::HGE;
+  constexpr int UNITS = HG * 16 * DC;         // (head group, row pair, chunk) staging units
+  constexpr int UPT = (UNITS + 255) / 256;
+  constexpr int FOLD = (HG - 1) * KB * 64 * 2 * DT * 16;  // floats exchanged at the end
+  constexpr int SMEM = 2 * STAGE > FOLD * 2 ? 2 * STAGE : FOLD * 2;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, hf = lane >> 5;
+  const int kbl = wave % KB, hg = wave / KB;
+  const int BHkv = gridDim.x / ((S + 32 * KB - 1) / (32 * KB));
+  const int bk = blockIdx.x % BHkv, kg = blockIdx.x / BHkv;
+  const int b = bk / Hkv, kvh = bk - b * Hkv;
+  const int kg0 = 32 * KB * kg;           // first key of the workgroup
+  const int kw0 = kg0 + 32 * kbl;         // first key of this wave
+  const int key = kw0 + n;
+
+  // K and V fragments (B operands of S = Q K^T, dP = dO V^T).
+  uint4 kf[KS], vf[KS];
+  {
+    const bool ok = key < S;
+    const bf16* kr = k + b * ks0 + kvh * ks1 + static_cast<int64_t>(ok ? key : 0) * ks2;
+    const bf16* vr = v + b * vs0 + kvh * vs1 + static_cast<int64_t>(ok ? key : 0) * vs2;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kf[s] = ld16_or0(kr + 16 * s + 8 * hf, ok);
+      vf[s] = ld16_or0(vr + 16 * s + 8 * hf, ok);
+    }
+  }
+  f32x16_t dka[DT], dva[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) { dka[dt] = zero16(); dva[dt] = zero16(); }
+
+  const int nqt = (S + 31) / 32;
+  const int qt0 = CAUSAL ? kg0 / 32 : 0;
+  const int nq = nqt - qt0;
+  const int rounds = G / HG;
+  const int nsteps = rounds * nq;
+
+  // Staging registers: per unit the chunk c of rows 2p, 2p+1 of Q and dO.
+  uint4 sq[UPT][2], sd[UPT][2];
+  float sl = 0.f, sdv = 0.f;  // lse2 / D of one row (threads < 32 * HG)
+  auto fetch = [&](int step) {
+    const int hr = step / nq, qt = qt0 + (step - hr * nq);
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int unit = tid + 256 * u;
+      if (UNITS % 256 == 0 || unit < UNITS) {
+        const int g = unit / (16 * DC), rem = unit - g * (16 * DC);
+        const int p = rem / DC, c = rem - p * DC;
+        const int h = kvh * G + hr * HG + g;
+        const int r0 = 32 * qt + 2 * p;
+        const bf16* qb = q + b * qs0 + h * qs1 + 8 * c;
+        const bf16* db = dout + b * ds0 + h * ds1 + 8 * c;
+        sq[u][0] = ld16_or0(qb + static_cast<int64_t>(min(r0, S - 1)) * qs2, r0 < S);
+        sq[u][1] = ld16_or0(qb + static_cast<int64_t>(min(r0 + 1, S - 1)) * qs2, r0 + 1 < S);
+        sd[u][0] = ld16_or0(db + static_cast<int64_t>(min(r0, S - 1)) * ds2, r0 < S);
+        sd[u][1] = ld16_or0(db + static_cast<int64_t>(min(r0 + 1, S - 1)) * ds2, r0 + 1 < S);
+      }
+    }
+    if (tid < 32 * HG) {
+      const int g = tid >> 5, row = 32 * qt + (tid & 31);
+      const int h = kvh * G + hr * HG + g;
+      const int64_t ri = (static_cast<int64_t>(b) * Hq + h) * S + min(row, S - 1);
+      // Rows past S get lse2 = +inf: their P is exactly 0.
+      sl = row < S ? lse2[ri] : INFINITY;
+      sdv = row < S ? dvec[ri] : 0.f;
+    }
+  };
+  auto land = [&](int buf) {
+    uint16_t* st = smem + buf * STAGE;
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int unit = tid + 256 * u;
+      if (UNITS % 256 == 0 || unit < UNITS) {
+        const int g = unit / (16 * DC), rem = unit - g * (16 * DC);
+        const int p = rem / DC, c = rem - p * DC;
+        uint16_t* hb = st + g * L::HGE;
+        *reinterpret_cast<uint4*>(&hb[(2 * p) * L::QP + 8 * c]) = sq[u][0];
+        *reinterpret_cast<uint4*>(&hb[(2 * p + 1) * L::QP + 8 * c]) = sq[u][1];
+        *reinterpret_cast<uint4*>(&hb[L::ROWS + (2 * p) * L::QP + 8 * c]) = sd[u][0];
+        *reinterpret_cast<uint4*>(&hb[L::ROWS + (2 * p + 1) * L::QP + 8 * c]) = sd[u][1];
+        st_pair_t(hb + 2 * L::ROWS, L::TP, c, p, sq[u][0], sq[u][1]);
+        st_pair_t(hb + 2 * L::ROWS + L::TRS, L::TP, c, p, sd[u][0], sd[u][1]);
+      }
+    }
+    if (tid < 32 * HG) {
+      float* f = reinterpret_cast<float*>(st + (tid >> 5) * L::HGE + 2 * L::ROWS + 2 * L::TRS);
+      f[tid & 31] = sl;
+      f[32 + (tid & 31)] = sdv;
+    }
+  };
+
+  if (nsteps > 0) {
+    fetch(0);
+    land(0);
+  }
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    if (step + 1 < nsteps) fetch(step + 1);
+    const int hr = step / nq, qt = qt0 + (step - hr * nq);
+    const int q0 = 32 * qt;
+    // Causal: the tile reaches this wave's keys iff q0 + 31 >= kw0; only
+    // the diagonal tile q0 == kw0 needs the key <= query mask.
+    if (!CAUSAL || q0 >= kw0) {
+      const uint16_t* hb = smem + buf * STAGE + hg * L::HGE;
+      const uint16_t* Qs = hb;
+      const uint16_t* Ds = hb + L::ROWS;
+      const uint16_t* Qt = hb + 2 * L::ROWS;
+      const uint16_t* Dt = Qt + L::TRS;
+      const float* lsv = reinterpret_cast<const float*>(Dt + L::TRS);
+      f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 aq = *reinterpret_cast<const uint4*>(&Qs[n * L::QP + 16 * ks + 8 * hf]);
+        s = mfma(aq, kf[ks], s);
+        const uint4 ad = *reinterpret_cast<const uint4*>(&Ds[n * L::QP + 16 * ks + 8 * hf]);
+        dp = mfma(ad, vf[ks], dp);
+      }
+      const bool diag = CAUSAL && q0 == kw0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 l4 = *reinterpret_cast<const float4*>(&lsv[8 * j + 4 * hf]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&lsv[32 + 8 * j + 4 * hf]);
+        const float lj[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dj[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * j + i;
+          float p = __builtin_amdgcn_exp2f(fmaf(s[r], scale_log2, -lj[i]));
+          if (diag) p = (key <= q0 + 8 * j + 4 * hf + i) ? p : 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - dj[i]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint4 pb = pack_c8(s, 8 * c);
+        const uint4 sb = pack_c8(dp, 8 * c);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          dva[dt] = mfma(lds_a_perm(Dt, 32 * dt + n, L::TP, c, hf), pb, dva[dt]);
+          dka[dt] = mfma(lds_a_perm(Qt, 32 * dt + n, L::TP, c, hf), sb, dka[dt]);
+        }
+      }
+    }
+    if (step + 1 < nsteps) land(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Fold the head groups (fixed order: group 0 + group 1 + ...), then store.
+  float* xf = reinterpret_cast<float*>(smem);
+  if constexpr (HG > 1) {
+    if (hg > 0) {
+      float* dst = xf + (((hg - 1) * KB + kbl) * 2 * DT * 16) * 64;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          dst[((2 * dt) * 16 + r) * 64 + lane] = dka[dt][r];
+          dst[((2 * dt + 1) * 16 + r) * 64 + lane] = dva[dt][r];
+        }
+    }
+    __syncthreads();
+    if (hg == 0) {
+#pragma unroll
+      for (int g = 1; g < HG; ++g) {
+        const float* src = xf + (((g - 1) * KB + kbl) * 2 * DT * 16) * 64;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            dka[dt][r] += src[((2 * dt) * 16 + r) * 64 + lane];
+            dva[dt][r] += src[((2 * dt + 1) * 16 + r) * 64 + lane];
+          }
+      }
+    }
+  }
+  if (hg == 0 && key < S) {
+    bf16* kr = dk + b * dks0 + kvh * dks1 + static_cast<int64_t>(key) * dks2;
+    bf16* vr = dv + b * dvs0 + kvh * dvs1 + static_cast<int64_t>(key) * dvs2;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * dt + 8 * j + 4 * hf;
+        const f32x16_t& a = dka[dt];
+        const f32x16_t& c = dva[dt];
+        *reinterpret_cast<uint2*>(kr + d) =
+            make_uint2(pack2<bf16>(a[4 * j] * scale, a[4 * j + 1] * scale),
+                       pack2<bf16>(a[4 * j + 2] * scale, a[4 * j + 3] * scale));
+        *reinterpret_cast<uint2*>(vr + d) =
+            make_uint2(pack2<bf16>(c[4 * j], c[4 * j + 1]), pack2<bf16>(c[4 * j + 2], c[4 * j + 3]));
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ, lanes own queries (bf16, MFMA).
+template <int HD>
+struct DqLayout {
+  static constexpr int BN = 64;              // keys per step
+  static constexpr int KP = HD + 8;          // row-major pitch (elements)
+  static constexpr int TP = BN + 4;          // transposed pitch (elements)
+  static constexpr int ROWS = BN * KP;
+  static constexpr int TRS = HD * TP;
+  static constexpr int STAGE = 2 * ROWS + TRS;  // K, V, K^T
+};
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
+    bf16* __restrict__ dq, int Hq, int Hkv, int S, int G, int ntasks, int items,
+    int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
+    int64_t dqs0, int64_t dqs1, int64_t dqs2, float scale_log2, float scale) {
+  using L = DqLayout<HD>;
+  constexpr int BN = L::BN;
+  constexpr int MT = BN / 32;
+  constexpr int KS = HD / 16;
+  constexpr int DT = HD / 32;
+  constexpr int DC = HD / 8;
+  constexpr int UNITS = (BN / 2) * DC;        // (key pair, chunk) staging units
+  constexpr int UPT = (UNITS + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * L::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, hf = lane >> 5;
+  const int BHkv = gridDim.x / items;
+  const int bk = blockIdx.x % BHkv;
+  const int item = items - 1 - static_cast<int>(blockIdx.x / BHkv);  // longest first
+  const int b = bk / Hkv, kvh = bk - b * Hkv;
+  const int task = 4 * item + wave;
+  const bool active = task < ntasks;
+  const int qb = (active ? task : ntasks - 1) / G;
+  const int h = kvh * G + (active ? task : ntasks - 1) % G;
+  const int q0 = 32 * qb, qi = q0 + n;
+  const bool qok = active && qi < S;
+
+  // Q (B operand of S^T = K Q^T) and dO (B operand of dP^T = V dO^T) rows.
+  uint4 qf[KS], of[KS];
+  float l2 = 0.f, dd = 0.f;
+  {
+    const bf16* qr = q + b * qs0 + h * qs1 + static_cast<int64_t>(qok ? qi : 0) * qs2;
+    const bf16* orow = dout + b * ds0 + h * ds1 + static_cast<int64_t>(qok ? qi : 0) * ds2;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qf[s] = ld16_or0(qr + 16 * s + 8 * hf, qok);
+      of[s] = ld16_or0(orow + 16 * s + 8 * hf, qok);
+    }
+    if (qok) {
+      const int64_t ri = (static_cast<int64_t>(b) * Hq + h) * S + qi;
+      l2 = lse2[ri];
+      dd = dvec[ri];
+    }
+  }
+  f32x16_t acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
+
+  // Keys the item needs: up to its last query (causal) or all of them.
+  const int last_task = min(4 * item + 3, ntasks - 1);
+  const int qmax = min(32 * (last_task / G) + 31, S - 1);
+  const int nkt = CAUSAL ? qmax / BN + 1 : (S + BN - 1) / BN;
+  const int my_last = CAUSAL ? min(q0 + 31, S - 1) : S - 1;  // this wave's last visible key
+
+  const bf16* kbase = k + b * ks0 + kvh * ks1;
+  const bf16* vbase = v + b * vs0 + kvh * vs1;
+  uint4 sk[UPT][2], sv[UPT][2];
+  auto fetch = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int unit = tid + 256 * u;
+      if (UNITS % 256 == 0 || unit < UNITS) {
+        const int p = unit / DC, c = unit - p * DC;
+        const int k0 = BN * kt + 2 * p;
+        sk[u][0] = ld16_or0(kbase + static_cast<int64_t>(min(k0, S - 1)) * ks2 + 8 * c, k0 < S);
+        sk[u][1] = ld16_or0(kbase + static_cast<int64_t>(min(k0 + 1, S - 1)) * ks2 + 8 * c, k0 + 1 < S);
+        sv[u][0] = ld16_or0(vbase + static_cast<int64_t>(min(k0, S - 1)) * vs2 + 8 * c, k0 < S);
+        sv[u][1] = ld16_or0(vbase + static_cast<int64_t>(min(k0 + 1, S - 1)) * vs2 + 8 * c, k0 + 1 < S);
+      }
+    }
+  };
+  auto land = [&](int buf) {
+    uint16_t* st = smem + buf * L::STAGE;
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int unit = tid + 256 * u;
+      if (UNITS % 256 == 0 || unit < UNITS) {
+        const int p = unit / DC, c = unit - p * DC;
+        *reinterpret_cast<uint4*>(&st[(2 * p) * L::KP + 8 * c]) = sk[u][0];
+        *reinterpret_cast<uint4*>(&st[(2 * p + 1) * L::KP + 8 * c]) = sk[u][1];
+        *reinterpret_cast<uint4*>(&st[L::ROWS + (2 * p) * L::KP + 8 * c]) = sv[u][0];
+        *reinterpret_cast<uint4*>(&st[L::ROWS + (2 * p + 1) * L::KP + 8 * c]) = sv[u][1];
+        st_pair_t(st + 2 * L::ROWS, L::TP, c, p, sk[u][0], sk[u][1]);
+      }
+    }
+  };
+
+  fetch(0);
+  land(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nkt) fetch(kt + 1);
+    const int key0 = BN * kt;
+    if (active && key0 <= my_last) {
+      const uint16_t* Ks = smem + buf * L::STAGE;
+      const uint16_t* Vs = Ks + L::ROWS;
+      const uint16_t* Kt = Ks + 2 * L::ROWS;
+      f32x16_t st[MT], dp[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) { st[mt] = zero16(); dp[mt] = zero16(); }
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int row = (32 * mt + n) * L::KP + 16 * s + 8 * hf;
+          st[mt] = mfma(*reinterpret_cast<const uint4*>(&Ks[row]), qf[s], st[mt]);
+          dp[mt] = mfma(*reinterpret_cast<const uint4*>(&Vs[row]), of[s], dp[mt]);
+        }
+      // Keys past S, and keys after the query when causal, get P = 0.
+      const bool masked = key0 + BN > S || (CAUSAL && key0 + BN - 1 > q0);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = __builtin_amdgcn_exp2f(fmaf(st[mt][r], scale_log2, -l2));
+          if (masked) {
+            const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
+            const bool ok = key < S && (!CAUSAL || key <= qi);
+            p = ok ? p : 0.f;
+          }
+          dp[mt][r] = p * (dp[mt][r] - dd);
+        }
+#pragma unroll
+      for (int c = 0; c < 2 * MT; ++c) {
+        const uint4 sb = pack_c8(dp[c >> 1], 8 * (c & 1));
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          acc[dt] = mfma(lds_a_perm(Kt, 32 * dt + n, L::TP, c, hf), sb, acc[dt]);
+      }
+    }
+    if (kt + 1 < nkt) land(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (qok) {
+    bf16* orow = dq + b * dqs0 + h * dqs1 + static_cast<int64_t>(qi) * dqs2;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * dt + 8 * j + 4 * hf;
+        const f32x16_t& a = acc[dt];
+        *reinterpret_cast<uint2*>(orow + d) =
+            make_uint2(pack2<bf16>(a[4 * j] * scale, a[4 * j + 1] * scale),
+                       pack2<bf16>(a[4 * j + 2] * scale, a[4 * j + 3] * scale));
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic path: fp32 math, one thread per query row (dQ) or key row (dK, dV).
+// Rows of up to MAXD elements are accumulated in registers.
+template <typename T, int MAXD, bool CAUSAL>
+__global__ __launch_bounds__(128) void attn_bwd_generic_dq_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
+    T* __restrict__ dq, int64_t rows, int Hq, int Hkv, int S, int hd,
+    int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
+    int64_t dqs0, int64_t dqs1, int64_t dqs2, float scale_log2, float scale) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 128 + threadIdx.x;
+  if (r >= rows) return;
+  const int s = static_cast<int>(r % S);
+  const int64_t bh = r / S;
+  const int h = static_cast<int>(bh % Hq);
+  const int64_t b = bh / Hq;
+  const int kvh = h / (Hq / Hkv);
+  const T* qr = q + b * qs0 + h * qs1 + s * qs2;
+  const T* dr = dout + b * ds0 + h * ds1 + s * ds2;
+  constexpr int UNR = MAXD <= 64 ? MAXD : 1;  // longer rows live in scratch anyway
+  float qv[MAXD], ov[MAXD], acc[MAXD];
+#pragma unroll UNR
+  for (int e = 0; e < MAXD; ++e) {
+    qv[e] = e < hd ? to_f32(qr[e]) : 0.f;
+    ov[e] = e < hd ? to_f32(dr[e]) : 0.f;
+    acc[e] = 0.f;
+  }
+  const float l2 = lse2[r], dd = dvec[r];
+  const int tend = CAUSAL ? s + 1 : S;
+  for (int t = 0; t < tend; ++t) {
+    const T* kr = k + b * ks0 + kvh * ks1 + t * ks2;
+    const T* vr = v + b * vs0 + kvh * vs1 + t * vs2;
+    float sc = 0.f, dpv = 0.f;
+#pragma unroll UNR
+    for (int e = 0; e < MAXD; ++e)
+      if (e < hd) {
+        sc = fmaf(qv[e], to_f32(kr[e]), sc);
+        dpv = fmaf(ov[e], to_f32(vr[e]), dpv);
+      }
+    const float p = exp2f(fmaf(sc, scale_log2, -l2));
+    const float ds = p * (dpv - dd);
+#pragma unroll UNR
+    for (int e = 0; e < MAXD; ++e)
+      if (e < hd) acc[e] = fmaf(ds, to_f32(kr[e]), acc[e]);
+  }
+  T* orow = dq + b * dqs0 + h * dqs1 + s * dqs2;
+#pragma unroll UNR
+  for (int e = 0; e < MAXD; ++e)
+    if (e < hd) orow[e] = from_f32<T>(acc[e] * scale);
+}
+
+template <typename T, int MAXD, bool CAUSAL>
+__global__ __launch_bounds__(128) void attn_bwd_generic_dkdv_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
+    T* __restrict__ dk, T* __restrict__ dv, int64_t rows, int Hq, int Hkv, int S, int hd,
+    int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
+    int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0, int64_t dvs1, int64_t dvs2,
+    float scale_log2, float scale) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 128 + threadIdx.x;
+  if (r >= rows) return;
+  const int t = static_cast<int>(r % S);
+  const int64_t bk = r / S;
+  const int kvh = static_cast<int>(bk % Hkv);
+  const int64_t b = bk / Hkv;
+  const int G = Hq / Hkv;
+  const T* kr = k + b * ks0 + kvh * ks1 + t * ks2;
+  const T* vr = v + b * vs0 + kvh * vs1 + t * vs2;
+  constexpr int UNR = MAXD <= 64 ? MAXD : 1;  // longer rows live in scratch anyway
+  float kv[MAXD], vv[MAXD], ak[MAXD], av[MAXD];
+#pragma unroll UNR
+  for (int e = 0; e < MAXD; ++e) {
+    kv[e] = e < hd ? to_f32(kr[e]) : 0.f;
+    vv[e] = e < hd ? to_f32(vr[e]) : 0.f;
+    ak[e] = 0.f;
+    av[e] = 0.f;
+  }
+  for (int g = 0; g < G; ++g) {
+    const int h = kvh * G + g;
+    const int64_t rb = (b * Hq + h) * S;
+    for (int s = CAUSAL ? t : 0; s < S; ++s) {
+      const T* qr = q + b * qs0 + h * qs1 + s * qs2;
+      const T* dr = dout + b * ds0 + h * ds1 + s * ds2;
+      float sc = 0.f, dpv = 0.f;
+#pragma unroll UNR
+      for (int e = 0; e < MAXD; ++e)
+        if (e < hd) {
+          sc = fmaf(to_f32(qr[e]), kv[e], sc);
+          dpv = fmaf(to_f32(dr[e]), vv[e], dpv);
+        }
+      const float p = exp2f(fmaf(sc, scale_log2, -lse2[rb + s]));
+      const float ds = p * (dpv - dvec[rb + s]);
+#pragma unroll UNR
+      for (int e = 0; e < MAXD; ++e)
+        if (e < hd) {
+          av[e] = fmaf(p, to_f32(dr[e]), av[e]);
+          ak[e] = fmaf(ds, to_f32(qr[e]), ak[e]);
+        }
+    }
+  }
+  T* okr = dk + b * dks0 + kvh * dks1 + t * dks2;
+  T* ovr = dv + b * dvs0 + kvh * dvs1 + t * dvs2;
+#pragma unroll UNR
+  for (int e = 0; e < MAXD; ++e)
+    if (e < hd) {
+      okr[e] = from_f32<T>(ak[e] * scale);
+      ovr[e] = from_f32<T>(av[e]);
+    }
+}
+
+struct BwdArgs {
+  const void *q, *k, *v, *o, *dout;
+  const float* lse;
+  void *dq, *dk, *dv;
+  int B, Hq, Hkv, S, hd;
+  const int64_t *qs, *ks, *vs, *os, *dos, *dqs, *dks, *dvs;
+  bool causal;
+  float scale;
+  hipStream_t st;
+};
+
+template <typename T>
+int launch_rowdot(const BwdArgs& a, float* dvec, float* lse2) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.S;
+  constexpr int E = 16 / int(sizeof(T));
+  const bool vec = a.hd % E == 0 && aligned16(a.o) && aligned16(a.dout) && a.os[0] % E == 0 &&
+                   a.os[1] % E == 0 && a.os[2] % E == 0 && a.dos[0] % E == 0 &&
+                   a.dos[1] % E == 0 && a.dos[2] % E == 0;
+  constexpr int TPR = 16;
+  const dim3 grid(static_cast<unsigned>((rows * TPR + 255) / 256));
+  const T* o = static_cast<const T*>(a.o);
+  const T* d = static_cast<const T*>(a.dout);
+  if (vec)
+    attn_bwd_rowdot_kernel<T, TPR, true><<<grid, 256, 0, a.st>>>(
+        o, d, a.lse, dvec, lse2, rows, a.Hq, a.S, a.hd, a.os[0], a.os[1], a.os[2], a.dos[0],
+        a.dos[1], a.dos[2]);
+  else
+    attn_bwd_rowdot_kernel<T, TPR, false><<<grid, 256, 0, a.st>>>(
+        o, d, a.lse, dvec, lse2, rows, a.Hq, a.S, a.hd, a.os[0], a.os[1], a.os[2], a.dos[0],
+        a.dos[1], a.dos[2]);
+  return check_launch("attn_bwd: rowdot");
+}
+
+template <int HD, bool CAUSAL>
+int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2) {
+  const float sl2 = a.scale * kLog2e;
+  const int BHkv = a.B * a.Hkv, G = a.Hq / a.Hkv;
+  const bf16* q = static_cast<const bf16*>(a.q);
+  const bf16* k = static_cast<const bf16*>(a.k);
+  const bf16* v = static_cast<const bf16*>(a.v);
+  const bf16* d = static_cast<const bf16*>(a.dout);
+  {
+    // Two key blocks x two head groups when G is even, else four key blocks.
+    const int KB = G % 2 == 0 ? 2 : 4;
+    const int nkg = (a.S + 32 * KB - 1) / (32 * KB);
+    const dim3 grid(static_cast<unsigned>(nkg * BHkv));
+#define HYDRA_DKDV(KBV)                                                                         \
+  attn_bwd_dkdv_kernel<HD, CAUSAL, KBV><<<grid, 256, 0, a.st>>>(                                \
+      q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), a.Hq, a.Hkv, \
+      a.S, G, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2],  \
+      a.dos[0], a.dos[1], a.dos[2], a.dks[0], a.dks[1], a.dks[2], a.dvs[0], a.dvs[1],          \
+      a.dvs[2], sl2, a.scale)
+    if (KB == 2) HYDRA_DKDV(2);
+    else HYDRA_DKDV(4);
+#undef HYDRA_DKDV
+    if (int rc = check_launch("attn_bwd: dkdv")) return rc;
+  }
+  const int ntasks = ((a.S + 31) / 32) * G;
+  const int items = (ntasks + 3) / 4;
+  attn_bwd_dq_kernel<HD, CAUSAL><<<dim3(static_cast<unsigned>(items * BHkv)), 256, 0, a.st>>>(
+      q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dq), a.Hq, a.Hkv, a.S, G, ntasks, items,
+      a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2], a.dos[0],
+      a.dos[1], a.dos[2], a.dqs[0], a.dqs[1], a.dqs[2], sl2, a.scale);
+  return check_launch("attn_bwd: dq");
+}
+
+template <typename T, int MAXD, bool CAUSAL>
+int launch_generic(const BwdArgs& a, const float* dvec, const float* lse2) {
+  const float sl2 = a.scale * kLog2e;
+  const T* q = static_cast<const T*>(a.q);
+  const T* k = static_cast<const T*>(a.k);
+  const T* v = static_cast<const T*>(a.v);
+  const T* d = static_cast<const T*>(a.dout);
+  const int64_t qrows = static_cast<int64_t>(a.B) * a.Hq * a.S;
+  const int64_t krows = static_cast<int64_t>(a.B) * a.Hkv * a.S;
+  attn_bwd_generic_dkdv_kernel<T, MAXD, CAUSAL>
+      <<<dim3(static_cast<unsigned>((krows + 127) / 128)), 128, 0, a.st>>>(
+          q, k, v, d, dvec, lse2, static_cast<T*>(a.dk), static_cast<T*>(a.dv), krows, a.Hq,
+          a.Hkv, a.S, a.hd, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0],
+          a.vs[1], a.vs[2], a.dos[0], a.dos[1], a.dos[2], a.dks[0], a.dks[1], a.dks[2],
+          a.dvs[0], a.dvs[1], a.dvs[2], sl2, a.scale);
+  if (int rc = check_launch("attn_bwd: generic dkdv")) return rc;
+  attn_bwd_generic_dq_kernel<T, MAXD, CAUSAL>
+      <<<dim3(static_cast<unsigned>((qrows + 127) / 128)), 128, 0, a.st>>>(
+          q, k, v, d, dvec, lse2, static_cast<T*>(a.dq), qrows, a.Hq, a.Hkv, a.S, a.hd,
+          a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2],
+          a.dos[0], a.dos[1], a.dos[2], a.dqs[0], a.dqs[1], a.dqs[2], sl2, a.scale);
+  return check_launch("attn_bwd: generic dq");
+}
+
+template <typename T, bool CAUSAL>
+int launch_generic_d(const BwdArgs& a, const float* dvec, const float* lse2) {
+  if (a.hd <= 32) return launch_generic<T, 32, CAUSAL>(a, dvec, lse2);
+  if (a.hd <= 64) return launch_generic<T, 64, CAUSAL>(a, dvec, lse2);
+  if (a.hd <= 128) return launch_generic<T, 128, CAUSAL>(a, dvec, lse2);
+  return launch_generic<T, 256, CAUSAL>(a, dvec, lse2);
+}
+
+template <typename T>
+int run_generic(const BwdArgs& a, float* dvec, float* lse2) {
+  if (int rc = launch_rowdot<T>(a, dvec, lse2)) return rc;
+  return a.causal ? launch_generic_d<T, true>(a, dvec, lse2)
+                  : launch_generic_d<T, false>(a, dvec, lse2);
+}
+
+template <int HD>
+int run_mfma(const BwdArgs& a, float* dvec, float* lse2) {
+  if (int rc = launch_rowdot<bf16>(a, dvec, lse2)) return rc;
+  return a.causal ? launch_mfma<HD, true>(a, dvec, lse2) : launch_mfma<HD, false>(a, dvec, lse2);
+}
+
+}  // namespace
+}  // namespace hydra
+
+using namespace hydra;
+
+extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                              const void* grad_o, const float* lse, void* grad_q, void* grad_k,
+                              void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                              int64_t hd, const int64_t* qs, const int64_t* ks,
+                              const int64_t* vs, const int64_t* os, const int64_t* gos,
+                              const int64_t* gqs, const int64_t* gks, const int64_t* gvs,
+                              int causal, float scale, int dtype, void* stream) {
+  HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_bwd: bad size");
+  HYDRA_REQUIRE(Hq % Hkv == 0, "attn_bwd: n_heads must be a multiple of n_kv_heads");
+  HYDRA_REQUIRE(qs && ks && vs && os && gos && gqs && gks && gvs, "attn_bwd: null stride array");
+  HYDRA_REQUIRE(qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1 && gos[3] == 1 &&
+                    gqs[3] == 1 && gks[3] == 1 && gvs[3] == 1,
+                "attn_bwd: every tensor needs unit stride along head_dim");
+  HYDRA_REQUIRE(hd <= 256, "attn_bwd: head_dim must be <= 256");
+  HYDRA_REQUIRE(dtype == HYDRA_F32 || dtype == HYDRA_BF16 || dtype == HYDRA_F16,
+                "attn_bwd: unknown dtype");
+  if (B * S == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(q && k && v && o && grad_o && lse && grad_q && grad_k && grad_v,
+                "attn_bwd: null pointer");
+  HYDRA_REQUIRE(S < (int64_t(1) << 30) && B * Hq * S < (int64_t(1) << 31),
+                "attn_bwd: problem too large");
+  auto st = static_cast<hipStream_t>(stream);
+  const int64_t rows = B * Hq * S;
+  void* ws = nullptr;
+  if (int rc = device_workspace(kWsAttnBwd, static_cast<size_t>(rows) * 2 * sizeof(float), st, &ws))
+    return rc;
+  float* dvec = static_cast<float*>(ws);
+  float* lse2 = dvec + rows;
+  const BwdArgs a{q, k, v, o, grad_o, lse, grad_q, grad_k, grad_v, static_cast<int>(B),
+                  static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(S),
+                  static_cast<int>(hd), qs, ks, vs, os, gos, gqs, gks, gvs, causal != 0, scale,
+                  st};
+  bool mfma_ok = dtype == HYDRA_BF16 && (hd == 32 || hd == 64 || hd == 128);
+  for (const int64_t* s : {qs, ks, vs, gos, gqs, gks, gvs})
+    mfma_ok = mfma_ok && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0;
+  for (const void* p : {q, k, v, grad_o, static_cast<const void*>(grad_q),
+                        static_cast<const void*>(grad_k), static_cast<const void*>(grad_v)})
+    mfma_ok = mfma_ok && aligned16(p);
+  if (mfma_ok) {
+    switch (hd) {
+      case 32: return run_mfma<32>(a, dvec, lse2);
+      case 64: return run_mfma<64>(a, dvec, lse2);
+      default: return run_mfma<128>(a, dvec, lse2);
+    }
+  }
+  switch (dtype) {
+    case HYDRA_F32: return run_generic<float>(a, dvec, lse2);
+    case HYDRA_BF16: return run_generic<bf16>(a, dvec, lse2);
+    default: return run_generic<f16>(a, dvec, lse2);
+  }
+}

@@ -230,6 +230,29 @@ int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
                    const int64_t* os, int causal, float scale,
                    float score_bound, int dtype, void* stream);
 
+/* Causal / full GQA attention backward: given the forward's q, k, v, its
+ * output o and lse (hydra_attn_fwd's fp32 [B,Hq,S] natural-log sum-exp of
+ * the scaled scores, contiguous), and the upstream gradient grad_o, writes
+ *   grad_v[b,j] = sum_g P^T grad_o,  grad_k[b,j] = sum_g dS^T q * scale,
+ *   grad_q = dS k * scale,  dS = P (grad_o v^T - rowsum(grad_o * o)),
+ * with P recomputed from lse, summing the G = Hq/Hkv query heads of K/V
+ * head j.  No key mask.  fp32 accumulation, outputs rounded once; no
+ * atomics (repeat calls are bit-identical).
+ * Replaces CCGQAAttentionFused.backward (kernels/fused_attention.py:706-823)
+ * and its kernels _bwd_gqa_kv_kernel / _bwd_gqa_dq_kernel (:113-338) and
+ * _bwd_kernel / _bwd_dq_kernel (:432-635).
+ * q, o, grad_o, grad_q: [B,Hq,S,hd]; k, v, grad_k, grad_v: [B,Hkv,S,hd];
+ * element strides *s[4], unit stride along hd for all.  bf16 with hd in
+ * {32, 64, 128}, 16-byte aligned pointers and strides that are multiples of
+ * 8 run on MFMA; every other case on the VALU path (hd <= 256).  Uses a
+ * library-owned workspace of 8 * B * Hq * S bytes (grown on first use). */
+int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                   const void* grad_o, const float* lse, void* grad_q, void* grad_k,
+                   void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                   const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
+                   const int64_t* gos, const int64_t* gqs, const int64_t* gks,
+                   const int64_t* gvs, int causal, float scale, int dtype, void* stream);
+
 /* ---- Mixture-of-Depths hard routing (hydra/routing, model/framework) --- */
 
 /* Per-row top-k of router scores, ties broken by the lower index, in the

@@ -200,6 +200,39 @@ def attention_key_padding(q, k, v, *, causal=True, mask=None, scale=None):
     return p @ vd
 
 
+def attention_backward(q, k, v, grad_out, *, causal=True, scale=None):
+    """fp64 restatement of the split-K backward of CCGQAAttentionFused
+    (kernels/fused_attention.py:113-338, :432-635): with P the softmax of
+    scale * q k^T (causal: key t visible to query s iff t <= s) recomputed
+    from its log-sum-exp, O = P V and D = rowsum(dO * O),
+      dV_j = sum_g P_g^T dO_g,  dS = P (dO V^T - D) scale,
+      dK_j = sum_g dS_g^T Q_g,  dQ = dS K,
+    summing the G = Hq/Hkv query heads g of K/V head j (repeat_interleave
+    order) as _bwd_gqa_kv_kernel does.  Returns (dq, dk, dv) in fp64.
+    Pinned against autograd through `attention_key_padding`."""
+    B, Hq, S, hd = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    sc = (1.0 / math.sqrt(hd)) if scale is None else scale
+    qd, dod = q.double(), grad_out.double()
+    kd = k.double().repeat_interleave(G, 1)
+    vd = v.double().repeat_interleave(G, 1)
+    logits = (qd @ kd.transpose(-1, -2)) * sc
+    if causal:
+        logits = logits.masked_fill(~torch.ones(S, S, dtype=torch.bool).tril(), float("-inf"))
+    lse = torch.logsumexp(logits, -1, keepdim=True)
+    p = torch.exp(logits - lse)
+    o = p @ vd
+    d = (dod * o).sum(-1, keepdim=True)
+    dv = p.transpose(-1, -2) @ dod
+    ds = p * (dod @ vd.transpose(-1, -2) - d) * sc
+    dk = ds.transpose(-1, -2) @ qd
+    dq = ds @ kd
+    dk = dk.view(B, Hkv, G, S, hd).sum(2)
+    dv = dv.view(B, Hkv, G, S, hd).sum(2)
+    return dq, dk, dv
+
+
 def forward(params: dict, x: torch.Tensor, cfg: CCGQAConfig, mask=None):
     """CCGQAAttention.forward (attention.py:201-331)."""
     B, S, _ = x.shape

@@ -1,0 +1,119 @@
+"""GPU parity of the CCGQA attention backward (hydra_attn_bwd) against the
+oracle's restatement of the reference's split-K backward, on the same
+bf16-rounded inputs (the oracle is pinned by autograd in
+tests/test_oracle_pins.py).
+
+The forward's log-sum-exp feeds the backward, as in the reference.
+Tolerance: normwise max-rel-err < 2e-2 for bf16 (P and dS enter the MFMA
+products in bf16, as in the reference's tl.dot), < 1e-5 for fp32 (VALU path,
+fp32 throughout).  At the full config-3 shape the check is per batch against
+the oracle plus two size-independent identities: sum_t dK[t] = 0 (each row of
+dS sums to zero) and sum_t dV[t] = sum over the group's heads and rows of dO
+(each row of P sums to one)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import max_rel_err
+from oracle import ccgqa as occ
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+def _inputs(B, Hq, Hkv, S, hd, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, S, hd, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, S, hd, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, S, hd, generator=g).to(dtype)
+    go = torch.randn(B, Hq, S, hd, generator=g).to(dtype)
+    return q, k, v, go
+
+
+def _run(q, k, v, go, causal, cuda):
+    from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+
+    qd, kd, vd, god = (t.to(cuda) for t in (q, k, v, go))
+    out, lse = attention_forward(qd, kd, vd, causal=causal, want_lse=True)
+    return attention_backward(qd, kd, vd, out, lse, god, causal=causal)
+
+
+def _check(got, q, k, v, go, causal, tol):
+    ref = occ.attention_backward(q, k, v, go, causal=causal)
+    for name, a, r in zip(("dq", "dk", "dv"), got, ref):
+        assert a.dtype == q.dtype and a.shape == r.shape
+        err = max_rel_err(a.cpu(), r)
+        assert err < tol, f"{name}: {err:.3g}"
+
+
+# (B, Hq, Hkv, S, hd): GQA 4:1 (two key blocks x two head groups per
+# workgroup), ragged S, MHA and odd G (four key blocks), G = 2, head_dim 32/128.
+MFMA_CASES = [(2, 4, 1, 256, 64), (1, 8, 2, 300, 64), (2, 2, 2, 128, 128), (1, 3, 1, 200, 32),
+              (1, 6, 3, 97, 64), (1, 4, 1, 1000, 128), (1, 1, 1, 33, 64)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", MFMA_CASES)
+def test_attention_backward_mfma(cuda, shape, causal):
+    q, k, v, go = _inputs(*shape, torch.bfloat16, seed=sum(shape))
+    _check(_run(q, k, v, go, causal, cuda), q, k, v, go, causal, TOL[torch.bfloat16])
+
+
+# VALU path: fp32, and bf16 with head_dim outside {32, 64, 128} (config 0's
+# debug shape has head_dim 16).
+GENERIC_CASES = [(torch.float32, (1, 4, 2, 64, 16)), (torch.float32, (2, 2, 1, 37, 64)),
+                 (torch.bfloat16, (2, 8, 2, 128, 16)), (torch.bfloat16, (1, 2, 1, 50, 48))]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype,shape", GENERIC_CASES)
+def test_attention_backward_generic(cuda, dtype, shape, causal):
+    q, k, v, go = _inputs(*shape, dtype, seed=sum(shape) + 1)
+    _check(_run(q, k, v, go, causal, cuda), q, k, v, go, causal, TOL[dtype])
+
+
+@pytest.mark.parametrize("use_fused_backward", [True, False])
+def test_ccgqa_attention_fused_autograd(cuda, use_fused_backward):
+    """The reference's public API (fused_attention.py:826-840) under autograd:
+    loss.backward() fills q/k/v .grad through the HIP backward."""
+    from hydra_amd.attention.backends.ccgqa.kernels import ccgqa_attention_fused
+
+    q, k, v, go = _inputs(2, 4, 1, 192, 64, torch.bfloat16, seed=3)
+    qd, kd, vd = (t.to(cuda).requires_grad_() for t in (q, k, v))
+    out = ccgqa_attention_fused(qd, kd, vd, is_causal=True, use_fused_backward=use_fused_backward)
+    out.backward(go.to(cuda))
+    _check((qd.grad, kd.grad, vd.grad), q, k, v, go, True, TOL[torch.bfloat16])
+
+
+def test_attention_backward_strided_and_deterministic(cuda):
+    """q/k/v as [B,S,H,D] buffers seen transposed, grad_out non-contiguous;
+    two calls give bit-identical gradients (no atomics)."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+
+    q, k, v, go = _inputs(2, 4, 2, 160, 64, torch.bfloat16, seed=4)
+    qd, kd, vd = (t.transpose(1, 2).contiguous().to(cuda).transpose(1, 2) for t in (q, k, v))
+    god = go.transpose(1, 2).contiguous().to(cuda).transpose(1, 2)
+    out, lse = attention_forward(qd, kd, vd, causal=True, want_lse=True)
+    first = attention_backward(qd, kd, vd, out, lse, god, causal=True)
+    second = attention_backward(qd, kd, vd, out, lse, god, causal=True)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+    _check(first, q, k, v, go, True, TOL[torch.bfloat16])
+
+
+def test_attention_backward_config3_shape(cuda):
+    """Config 3's attention (B 4, 4 query heads, 1 KV head, hd 64, S 4096,
+    causal): batches 0 and 3 against the oracle, all four through the
+    row-sum identities."""
+    B, Hq, Hkv, S, hd = 4, 4, 1, 4096, 64
+    q, k, v, go = _inputs(B, Hq, Hkv, S, hd, torch.bfloat16, seed=7)
+    dq, dk, dv = _run(q, k, v, go, True, cuda)
+    for b in (0, 3):
+        _check((dq[b:b + 1], dk[b:b + 1], dv[b:b + 1]), q[b:b + 1], k[b:b + 1], v[b:b + 1],
+               go[b:b + 1], True, TOL[torch.bfloat16])
+    dk64, dv64 = dk.double().cpu(), dv.double().cpu()
+    assert (dk64.sum(2).abs() / dk64.abs().sum(2)).max() < 1e-2
+    want_v = go.double().view(B, Hkv, Hq // Hkv, S, hd).sum((2, 3))
+    assert max_rel_err(dv64.sum(2), want_v) < 1e-2

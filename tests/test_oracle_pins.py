@@ -463,3 +463,28 @@ def test_rope_backward_autograd():
     ofo.rope(xa, cos.double(), sin.double()).backward(go)
     gx = ofo.rope_backward(go, cos, sin)
     assert torch.allclose(gx, xa.grad, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(2, 4, 1, 9, 8), (1, 4, 2, 13, 6), (1, 2, 2, 5, 4)])
+def test_attention_backward_autograd(causal, shape):
+    """The split-K restatement (explicit P, D = rowsum(dO * O), head sums
+    over the GQA group) against autograd through the forward oracle, which
+    expands K/V by repeat_interleave: a wrong head mapping, a missing scale
+    or D taken from the wrong side fails here."""
+    B, Hq, Hkv, S, hd = shape
+    g = torch.Generator().manual_seed(S * hd + causal)
+    q, k, v = (torch.randn(B, h, S, hd, generator=g, dtype=torch.float64).requires_grad_()
+               for h in (Hq, Hkv, Hkv))
+    go = torch.randn(B, Hq, S, hd, generator=g, dtype=torch.float64)
+    occ.attention_key_padding(q, k, v, causal=causal).backward(go)
+    dq, dk, dv = occ.attention_backward(q.detach(), k.detach(), v.detach(), go, causal=causal)
+    for got, ref in ((dq, q.grad), (dk, k.grad), (dv, v.grad)):
+        assert torch.allclose(got, ref, rtol=1e-10, atol=1e-12)
+    # a non-default scale, and causal row 0 whose only key is itself: dq = 0 there
+    q2 = q.detach().clone().requires_grad_()
+    occ.attention_key_padding(q2, k.detach(), v.detach(), causal=causal, scale=0.3).backward(go)
+    dq2, _, _ = occ.attention_backward(q2.detach(), k.detach(), v.detach(), go, causal=causal, scale=0.3)
+    assert torch.allclose(dq2, q2.grad, rtol=1e-10, atol=1e-12)
+    if causal:
+        assert dq[:, :, 0].abs().max() < 1e-12
