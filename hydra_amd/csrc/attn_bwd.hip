@@ -39,6 +39,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kVmcnt0 = 0x3f70;  // s_waitcnt vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
 
 __device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -84,6 +85,22 @@ __device__ __forceinline__ void st_pair_t(uint16_t* t, int pitch, int c, int p, 
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     *reinterpret_cast<uint32_t*>(&t[(8 * c + i) * pitch + 2 * p]) = pair_word(a, b, i);
+}
+
+// Buffer resource over `bytes` bytes from `base`: loads past the end return
+// zero (hardware range check), so tiles that overhang S need no branches --
+// which also keeps the compiler's vmcnt bookkeeping exact across the
+// prefetch.
+constexpr int kRsrcFlags = 0x00020000;  // raw (untyped) access, gfx9 family
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           kRsrcFlags);
+}
+__device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float ld4_buf(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
 __device__ __forceinline__ uint4 ld16_or0(const bf16* p, bool ok) {
@@ -139,8 +156,8 @@ struct DkdvLayout {
   static constexpr int HGE = 2 * ROWS + 2 * TRS + 2 * 32 * 2;  // Q, dO, Q^T, dO^T, lse2, D (elements)
 };
 
-template <int HD, bool CAUSAL, int KB>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
+template <int HD, bool CAUSAL, int KB, int HG>
+__global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
     bf16* __restrict__ dk, bf16* __restrict__ dv, int Hq, int Hkv, int S, int G,
@@ -148,14 +165,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
     int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
     int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0, int64_t dvs1, int64_t dvs2,
     float scale_log2, float scale) {
-  constexpr int HG = 4 / KB;
+  constexpr int NT = 64 * KB * HG;
   constexpr int KS = HD / 16;   // k-steps over head_dim
   constexpr int DT = HD / 32;   // 32-row d tiles of dK^T / dV^T
   constexpr int DC = HD / 8;    // 16-byte chunks per row
   using L = DkdvLayout<HD>;
   constexpr int STAGE = HG * L::HGE;
   constexpr int UNITS = HG * 16 * DC;         // (head group, row pair, chunk) staging units
-  constexpr int UPT = (UNITS + 255) / 256;
+  constexpr int UPT = (UNITS + NT - 1) / NT;
   constexpr int FOLD = (HG - 1) * KB * 64 * 2 * DT * 16;  // floats exchanged at the end
   constexpr int SMEM = 2 * STAGE > FOLD * 2 ? 2 * STAGE : FOLD * 2;
   __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
@@ -182,6 +199,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
       vf[s] = ld16_or0(vr + 16 * s + 8 * hf, ok);
     }
   }
+  // Retire these loads before the loop: the in-order vmcnt would otherwise
+  // make the loop's first use of kf/vf wait for the tile prefetches too.
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
   f32x16_t dka[DT], dva[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) { dka[dt] = zero16(); dva[dt] = zero16(); }
@@ -193,67 +213,72 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
   const int nsteps = rounds * nq;
 
   // Staging registers: per unit the chunk c of rows 2p, 2p+1 of Q and dO.
-  uint4 sq[UPT][2], sd[UPT][2];
-  float sl = 0.f, sdv = 0.f;  // lse2 / D of one row (threads < 32 * HG)
-  auto fetch = [&](int step) {
+  struct Regs {
+    uint4 q[UPT][2], d[UPT][2];
+    float l, dv;  // lse2 / D of one row (threads < 32 * HG)
+  };
+  Regs ra, rb;
+  auto fetch = [&](int step, Regs& R) {
     const int hr = step / nq, qt = qt0 + (step - hr * nq);
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
-      const int unit = tid + 256 * u;
-      if (UNITS % 256 == 0 || unit < UNITS) {
-        const int g = unit / (16 * DC), rem = unit - g * (16 * DC);
-        const int p = rem / DC, c = rem - p * DC;
+      const int unit = tid + NT * u;
+      if (UNITS % NT == 0 || unit < UNITS) {
+        // 16 * DC >= 64 units share a head group, so g is wave-uniform (and
+        // the buffer resources below scalar).
+        const int g = __builtin_amdgcn_readfirstlane(unit / (16 * DC));
+        const int rem = unit - g * (16 * DC);
+        const int c = rem >> 4, p = rem & 15;  // p fastest: conflict-free transposed writes
         const int h = kvh * G + hr * HG + g;
-        const int r0 = 32 * qt + 2 * p;
-        const bf16* qb = q + b * qs0 + h * qs1 + 8 * c;
-        const bf16* db = dout + b * ds0 + h * ds1 + 8 * c;
-        sq[u][0] = ld16_or0(qb + static_cast<int64_t>(min(r0, S - 1)) * qs2, r0 < S);
-        sq[u][1] = ld16_or0(qb + static_cast<int64_t>(min(r0 + 1, S - 1)) * qs2, r0 + 1 < S);
-        sd[u][0] = ld16_or0(db + static_cast<int64_t>(min(r0, S - 1)) * ds2, r0 < S);
-        sd[u][1] = ld16_or0(db + static_cast<int64_t>(min(r0 + 1, S - 1)) * ds2, r0 + 1 < S);
+        const int r0 = 32 * qt + 2 * p;  // rows >= S read as zero
+        const auto qr = rows_rsrc(q + b * qs0 + h * qs1, (S - 1) * qs2 * 2 + HD * 2);
+        const auto dr = rows_rsrc(dout + b * ds0 + h * ds1, (S - 1) * ds2 * 2 + HD * 2);
+        const int qo = r0 * static_cast<int>(qs2) * 2 + 16 * c;
+        const int dof = r0 * static_cast<int>(ds2) * 2 + 16 * c;
+        R.q[u][0] = ld16_buf(qr, qo);
+        R.q[u][1] = ld16_buf(qr, qo + static_cast<int>(qs2) * 2);
+        R.d[u][0] = ld16_buf(dr, dof);
+        R.d[u][1] = ld16_buf(dr, dof + static_cast<int>(ds2) * 2);
       }
     }
-    if (tid < 32 * HG) {
+    {
+      // Rows of this round's HG heads (threads < 32 HG); rows past S, and
+      // the other threads, read lse2 = D = 0 through an out-of-range offset
+      // (with zero Q and dO rows such rows add nothing: dS = P (0 - 0) = 0
+      // and dO^T P = 0).  Every thread issues the same loads, so the
+      // compiler's vmcnt bookkeeping stays exact.
       const int g = tid >> 5, row = 32 * qt + (tid & 31);
-      const int h = kvh * G + hr * HG + g;
-      const int64_t ri = (static_cast<int64_t>(b) * Hq + h) * S + min(row, S - 1);
-      // Rows past S get lse2 = +inf: their P is exactly 0.
-      sl = row < S ? lse2[ri] : INFINITY;
-      sdv = row < S ? dvec[ri] : 0.f;
+      const int64_t h0 = static_cast<int64_t>(b) * Hq + kvh * G + hr * HG;
+      const int off = (tid < 32 * HG && row < S) ? (g * S + row) * 4 : 0x7ffffff0;
+      R.l = ld4_buf(rows_rsrc(lse2 + h0 * S, int64_t(HG) * S * 4), off);
+      R.dv = ld4_buf(rows_rsrc(dvec + h0 * S, int64_t(HG) * S * 4), off);
     }
   };
-  auto land = [&](int buf) {
+  auto land = [&](int buf, const Regs& R) {
     uint16_t* st = smem + buf * STAGE;
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
-      const int unit = tid + 256 * u;
-      if (UNITS % 256 == 0 || unit < UNITS) {
+      const int unit = tid + NT * u;
+      if (UNITS % NT == 0 || unit < UNITS) {
         const int g = unit / (16 * DC), rem = unit - g * (16 * DC);
-        const int p = rem / DC, c = rem - p * DC;
+        const int c = rem >> 4, p = rem & 15;  // p fastest: conflict-free transposed writes
         uint16_t* hb = st + g * L::HGE;
-        *reinterpret_cast<uint4*>(&hb[(2 * p) * L::QP + 8 * c]) = sq[u][0];
-        *reinterpret_cast<uint4*>(&hb[(2 * p + 1) * L::QP + 8 * c]) = sq[u][1];
-        *reinterpret_cast<uint4*>(&hb[L::ROWS + (2 * p) * L::QP + 8 * c]) = sd[u][0];
-        *reinterpret_cast<uint4*>(&hb[L::ROWS + (2 * p + 1) * L::QP + 8 * c]) = sd[u][1];
-        st_pair_t(hb + 2 * L::ROWS, L::TP, c, p, sq[u][0], sq[u][1]);
-        st_pair_t(hb + 2 * L::ROWS + L::TRS, L::TP, c, p, sd[u][0], sd[u][1]);
+        *reinterpret_cast<uint4*>(&hb[(2 * p) * L::QP + 8 * c]) = R.q[u][0];
+        *reinterpret_cast<uint4*>(&hb[(2 * p + 1) * L::QP + 8 * c]) = R.q[u][1];
+        *reinterpret_cast<uint4*>(&hb[L::ROWS + (2 * p) * L::QP + 8 * c]) = R.d[u][0];
+        *reinterpret_cast<uint4*>(&hb[L::ROWS + (2 * p + 1) * L::QP + 8 * c]) = R.d[u][1];
+        st_pair_t(hb + 2 * L::ROWS, L::TP, c, p, R.q[u][0], R.q[u][1]);
+        st_pair_t(hb + 2 * L::ROWS + L::TRS, L::TP, c, p, R.d[u][0], R.d[u][1]);
       }
     }
     if (tid < 32 * HG) {
       float* f = reinterpret_cast<float*>(st + (tid >> 5) * L::HGE + 2 * L::ROWS + 2 * L::TRS);
-      f[tid & 31] = sl;
-      f[32 + (tid & 31)] = sdv;
+      f[tid & 31] = R.l;
+      f[32 + (tid & 31)] = R.dv;
     }
   };
 
-  if (nsteps > 0) {
-    fetch(0);
-    land(0);
-  }
-  __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    if (step + 1 < nsteps) fetch(step + 1);
+  auto compute = [&](int step, int buf) {
     const int hr = step / nq, qt = qt0 + (step - hr * nq);
     const int q0 = 32 * qt;
     // Causal: the tile reaches this wave's keys iff q0 + 31 >= kw0; only
@@ -300,9 +325,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
         }
       }
     }
-    if (step + 1 < nsteps) land(buf ^ 1);
+  };
+
+  // Two register sets alternate, so a tile's loads have two steps to land.
+  // Fetches are unconditional (past the end they repeat the last tile) so
+  // that every path issues the same loads and each land() waits only for
+  // its own set.
+  const int last = nsteps - 1;  // >= 0
+  fetch(0, ra);
+  land(0, ra);
+  fetch(min(1, last), rb);
+  __syncthreads();
+  int step = 0;
+  for (; step < last; step += 2) {
+    fetch(min(step + 2, last), ra);
+    compute(step, 0);
+    land(1, rb);
+    __syncthreads();
+    fetch(min(step + 3, last), rb);
+    compute(step + 1, 1);
+    land(0, ra);
     __syncthreads();
   }
+  if (step == last) compute(step, 0);  // odd count: the last tile is in buffer 0
+  __syncthreads();  // the fold below reuses the staging buffers
 
   // Fold the head groups (fixed order: group 0 + group 1 + ...), then store.
   float* xf = reinterpret_cast<float*>(smem);
@@ -411,6 +457,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
       dd = dvec[ri];
     }
   }
+  // Retire these loads before the loop (see attn_bwd_dkdv_kernel).
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
   f32x16_t acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
@@ -421,45 +469,45 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   const int nkt = CAUSAL ? qmax / BN + 1 : (S + BN - 1) / BN;
   const int my_last = CAUSAL ? min(q0 + 31, S - 1) : S - 1;  // this wave's last visible key
 
-  const bf16* kbase = k + b * ks0 + kvh * ks1;
-  const bf16* vbase = v + b * vs0 + kvh * vs1;
-  uint4 sk[UPT][2], sv[UPT][2];
-  auto fetch = [&](int kt) {
+  const auto krs = rows_rsrc(k + b * ks0 + kvh * ks1, (S - 1) * ks2 * 2 + HD * 2);
+  const auto vrs = rows_rsrc(v + b * vs0 + kvh * vs1, (S - 1) * vs2 * 2 + HD * 2);
+  struct Regs {
+    uint4 k[UPT][2], v[UPT][2];
+  };
+  Regs ra, rb;
+  auto fetch = [&](int kt, Regs& R) {
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int unit = tid + 256 * u;
       if (UNITS % 256 == 0 || unit < UNITS) {
-        const int p = unit / DC, c = unit - p * DC;
-        const int k0 = BN * kt + 2 * p;
-        sk[u][0] = ld16_or0(kbase + static_cast<int64_t>(min(k0, S - 1)) * ks2 + 8 * c, k0 < S);
-        sk[u][1] = ld16_or0(kbase + static_cast<int64_t>(min(k0 + 1, S - 1)) * ks2 + 8 * c, k0 + 1 < S);
-        sv[u][0] = ld16_or0(vbase + static_cast<int64_t>(min(k0, S - 1)) * vs2 + 8 * c, k0 < S);
-        sv[u][1] = ld16_or0(vbase + static_cast<int64_t>(min(k0 + 1, S - 1)) * vs2 + 8 * c, k0 + 1 < S);
+        const int c = unit >> 5, p = unit & 31;  // p fastest: conflict-free transposed writes
+        const int k0 = BN * kt + 2 * p;  // keys >= S read as zero
+        const int ko = k0 * static_cast<int>(ks2) * 2 + 16 * c;
+        const int vo = k0 * static_cast<int>(vs2) * 2 + 16 * c;
+        R.k[u][0] = ld16_buf(krs, ko);
+        R.k[u][1] = ld16_buf(krs, ko + static_cast<int>(ks2) * 2);
+        R.v[u][0] = ld16_buf(vrs, vo);
+        R.v[u][1] = ld16_buf(vrs, vo + static_cast<int>(vs2) * 2);
       }
     }
   };
-  auto land = [&](int buf) {
+  auto land = [&](int buf, const Regs& R) {
     uint16_t* st = smem + buf * L::STAGE;
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int unit = tid + 256 * u;
       if (UNITS % 256 == 0 || unit < UNITS) {
-        const int p = unit / DC, c = unit - p * DC;
-        *reinterpret_cast<uint4*>(&st[(2 * p) * L::KP + 8 * c]) = sk[u][0];
-        *reinterpret_cast<uint4*>(&st[(2 * p + 1) * L::KP + 8 * c]) = sk[u][1];
-        *reinterpret_cast<uint4*>(&st[L::ROWS + (2 * p) * L::KP + 8 * c]) = sv[u][0];
-        *reinterpret_cast<uint4*>(&st[L::ROWS + (2 * p + 1) * L::KP + 8 * c]) = sv[u][1];
-        st_pair_t(st + 2 * L::ROWS, L::TP, c, p, sk[u][0], sk[u][1]);
+        const int c = unit >> 5, p = unit & 31;  // p fastest: conflict-free transposed writes
+        *reinterpret_cast<uint4*>(&st[(2 * p) * L::KP + 8 * c]) = R.k[u][0];
+        *reinterpret_cast<uint4*>(&st[(2 * p + 1) * L::KP + 8 * c]) = R.k[u][1];
+        *reinterpret_cast<uint4*>(&st[L::ROWS + (2 * p) * L::KP + 8 * c]) = R.v[u][0];
+        *reinterpret_cast<uint4*>(&st[L::ROWS + (2 * p + 1) * L::KP + 8 * c]) = R.v[u][1];
+        st_pair_t(st + 2 * L::ROWS, L::TP, c, p, R.k[u][0], R.k[u][1]);
       }
     }
   };
 
-  fetch(0);
-  land(0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nkt) fetch(kt + 1);
+  auto compute = [&](int kt, int buf) {
     const int key0 = BN * kt;
     if (active && key0 <= my_last) {
       const uint16_t* Ks = smem + buf * L::STAGE;
@@ -498,9 +546,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
           acc[dt] = mfma(lds_a_perm(Kt, 32 * dt + n, L::TP, c, hf), sb, acc[dt]);
       }
     }
-    if (kt + 1 < nkt) land(buf ^ 1);
+  };
+
+  // Two register sets alternate (see attn_bwd_dkdv_kernel).
+  const int last = nkt - 1;  // >= 0
+  fetch(0, ra);
+  land(0, ra);
+  fetch(min(1, last), rb);
+  __syncthreads();
+  int kt = 0;
+  for (; kt < last; kt += 2) {
+    fetch(min(kt + 2, last), ra);
+    compute(kt, 0);
+    land(1, rb);
+    __syncthreads();
+    fetch(min(kt + 3, last), rb);
+    compute(kt + 1, 1);
+    land(0, ra);
     __syncthreads();
   }
+  if (kt == last) compute(kt, 0);  // odd count: the last tile is in buffer 0
 
   if (qok) {
     bf16* orow = dq + b * dqs0 + h * dqs1 + static_cast<int64_t>(qi) * dqs2;
@@ -671,18 +736,26 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2) {
   const bf16* v = static_cast<const bf16*>(a.v);
   const bf16* d = static_cast<const bf16*>(a.dout);
   {
-    // Two key blocks x two head groups when G is even, else four key blocks.
-    const int KB = G % 2 == 0 ? 2 : 4;
+    // Workgroup shape: KB blocks of 32 keys x HG head groups (G % HG == 0).
+    // Four head groups (8 waves) when the LDS ring fits (hd <= 64), two when
+    // G is even, else one (four key blocks).
+    const int HGv = (G % 4 == 0 && HD <= 64) ? 4 : (G % 2 == 0 ? 2 : 1);
+    const int KB = HGv == 1 ? 4 : 2;
     const int nkg = (a.S + 32 * KB - 1) / (32 * KB);
     const dim3 grid(static_cast<unsigned>(nkg * BHkv));
-#define HYDRA_DKDV(KBV)                                                                         \
-  attn_bwd_dkdv_kernel<HD, CAUSAL, KBV><<<grid, 256, 0, a.st>>>(                                \
+#define HYDRA_DKDV(KBV, HGV)                                                                    \
+  attn_bwd_dkdv_kernel<HD, CAUSAL, KBV, HGV><<<grid, 64 * KBV * HGV, 0, a.st>>>(                \
       q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), a.Hq, a.Hkv, \
       a.S, G, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2],  \
       a.dos[0], a.dos[1], a.dos[2], a.dks[0], a.dks[1], a.dks[2], a.dvs[0], a.dvs[1],          \
       a.dvs[2], sl2, a.scale)
-    if (KB == 2) HYDRA_DKDV(2);
-    else HYDRA_DKDV(4);
+    if (HGv == 4) {
+      if constexpr (HD <= 64) HYDRA_DKDV(2, 4);
+    } else if (HGv == 2) {
+      HYDRA_DKDV(2, 2);
+    } else {
+      HYDRA_DKDV(4, 1);
+    }
 #undef HYDRA_DKDV
     if (int rc = check_launch("attn_bwd: dkdv")) return rc;
   }
@@ -778,8 +851,11 @@ extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const
                   static_cast<int>(hd), qs, ks, vs, os, gos, gqs, gks, gvs, causal != 0, scale,
                   st};
   bool mfma_ok = dtype == HYDRA_BF16 && (hd == 32 || hd == 64 || hd == 128);
+  // Tiles are addressed with 32-bit byte offsets within one head's rows
+  // (up to 64 rows past S).
   for (const int64_t* s : {qs, ks, vs, gos, gqs, gks, gvs})
-    mfma_ok = mfma_ok && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0;
+    mfma_ok = mfma_ok && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= hd &&
+              (S + 64) * s[2] * 2 < (int64_t(1) << 31);
   for (const void* p : {q, k, v, grad_o, static_cast<const void*>(grad_q),
                         static_cast<const void*>(grad_k), static_cast<const void*>(grad_v)})
     mfma_ok = mfma_ok && aligned16(p);
