@@ -31,6 +31,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace hydra {
 namespace {
@@ -177,7 +178,8 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
   constexpr int SMEM = 2 * STAGE > FOLD * 2 ? 2 * STAGE : FOLD * 2;
   __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: per-wave branches stay uniform
   const int n = lane & 31, hf = lane >> 5;
   const int kbl = wave % KB, hg = wave / KB;
   const int BHkv = gridDim.x / ((S + 32 * KB - 1) / (32 * KB));
@@ -278,12 +280,10 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
     }
   };
 
-  auto compute = [&](int step, int buf) {
-    const int hr = step / nq, qt = qt0 + (step - hr * nq);
-    const int q0 = 32 * qt;
-    // Causal: the tile reaches this wave's keys iff q0 + 31 >= kw0; only
-    // the diagonal tile q0 == kw0 needs the key <= query mask.
-    if (!CAUSAL || q0 >= kw0) {
+  // One 32-query tile; DIAG: the tile on this wave's diagonal (key <= query mask).
+  auto tile = [&](auto diag_tag, int q0, int buf) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    {
       const uint16_t* hb = smem + buf * STAGE + hg * L::HGE;
       const uint16_t* Qs = hb;
       const uint16_t* Ds = hb + L::ROWS;
@@ -298,7 +298,6 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
         const uint4 ad = *reinterpret_cast<const uint4*>(&Ds[n * L::QP + 16 * ks + 8 * hf]);
         dp = mfma(ad, vf[ks], dp);
       }
-      const bool diag = CAUSAL && q0 == kw0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float4 l4 = *reinterpret_cast<const float4*>(&lsv[8 * j + 4 * hf]);
@@ -309,7 +308,7 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
         for (int i = 0; i < 4; ++i) {
           const int r = 4 * j + i;
           float p = __builtin_amdgcn_exp2f(fmaf(s[r], scale_log2, -lj[i]));
-          if (diag) p = (key <= q0 + 8 * j + 4 * hf + i) ? p : 0.f;
+          if constexpr (DIAG) p = (key <= q0 + 8 * j + 4 * hf + i) ? p : 0.f;
           s[r] = p;
           dp[r] = p * (dp[r] - dj[i]);
         }
@@ -325,6 +324,14 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
         }
       }
     }
+  };
+  auto compute = [&](int step, int buf) {
+    const int hr = step / nq, qt = qt0 + (step - hr * nq);
+    const int q0 = 32 * qt;
+    // Causal: the tile reaches this wave's keys iff q0 + 31 >= kw0; only
+    // the diagonal tile q0 == kw0 needs the key <= query mask.
+    if (CAUSAL && q0 == kw0) tile(std::true_type{}, q0, buf);
+    else if (!CAUSAL || q0 > kw0) tile(std::false_type{}, q0, buf);
   };
 
   // Two register sets alternate, so a tile's loads have two steps to land.
@@ -427,7 +434,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   constexpr int UPT = (UNITS + 255) / 256;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * L::STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: per-wave branches stay uniform
   const int n = lane & 31, hf = lane >> 5;
   const int BHkv = gridDim.x / items;
   const int bk = blockIdx.x % BHkv;
@@ -507,9 +515,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
     }
   };
 
-  auto compute = [&](int kt, int buf) {
-    const int key0 = BN * kt;
-    if (active && key0 <= my_last) {
+  // One 64-key tile; MASKED: keys past S or after a query of this wave.
+  auto tile = [&](auto mask_tag, int key0, int buf) {
+    constexpr bool MASKED = decltype(mask_tag)::value;
+    {
       const uint16_t* Ks = smem + buf * L::STAGE;
       const uint16_t* Vs = Ks + L::ROWS;
       const uint16_t* Kt = Ks + 2 * L::ROWS;
@@ -524,14 +533,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
           st[mt] = mfma(*reinterpret_cast<const uint4*>(&Ks[row]), qf[s], st[mt]);
           dp[mt] = mfma(*reinterpret_cast<const uint4*>(&Vs[row]), of[s], dp[mt]);
         }
-      // Keys past S, and keys after the query when causal, get P = 0.
-      const bool masked = key0 + BN > S || (CAUSAL && key0 + BN - 1 > q0);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float p = __builtin_amdgcn_exp2f(fmaf(st[mt][r], scale_log2, -l2));
-          if (masked) {
+          if constexpr (MASKED) {  // keys past S, and after the query when causal: P = 0
             const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
             const bool ok = key < S && (!CAUSAL || key <= qi);
             p = ok ? p : 0.f;
@@ -546,6 +553,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
           acc[dt] = mfma(lds_a_perm(Kt, 32 * dt + n, L::TP, c, hf), sb, acc[dt]);
       }
     }
+  };
+  auto compute = [&](int kt, int buf) {
+    const int key0 = BN * kt;
+    if (!active || key0 > my_last) return;
+    if (key0 + BN > S || (CAUSAL && key0 + BN - 1 > q0)) tile(std::true_type{}, key0, buf);
+    else tile(std::false_type{}, key0, buf);
   };
 
   // Two register sets alternate (see attn_bwd_dkdv_kernel).
