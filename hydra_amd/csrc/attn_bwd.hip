@@ -31,6 +31,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace hydra {
@@ -161,7 +162,8 @@ template <int HD, bool CAUSAL, int KB, int HG>
 __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
-    bf16* __restrict__ dk, bf16* __restrict__ dv, int Hq, int Hkv, int S, int G,
+    bf16* __restrict__ dk, bf16* __restrict__ dv, float* __restrict__ part, int Hq, int Hkv,
+    int S, int G, int nwg, int ch, int maxch,
     int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
     int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0, int64_t dvs1, int64_t dvs2,
@@ -182,9 +184,20 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: per-wave branches stay uniform
   const int n = lane & 31, hf = lane >> 5;
   const int kbl = wave % KB, hg = wave / KB;
-  const int BHkv = gridDim.x / ((S + 32 * KB - 1) / (32 * KB));
-  const int bk = blockIdx.x % BHkv, kg = blockIdx.x / BHkv;
+  const int BHkv = gridDim.x / nwg;
+  const int bk = blockIdx.x % BHkv;
   const int b = bk / Hkv, kvh = bk - b * Hkv;
+  const int nkg = (S + 32 * KB - 1) / (32 * KB);
+  const int nqt = (S + 31) / 32;
+  // Workgroup -> (key group kg, chunk): key groups in order (the longest
+  // causal walks first), each split into ceil(nq / ch) chunks of ch query
+  // tiles.  Scalar loop over at most nkg groups.
+  int kg = 0, nch = 1, chunk = static_cast<int>(blockIdx.x) / BHkv;
+  for (;; ++kg) {
+    nch = ((CAUSAL ? nqt - KB * kg : nqt) + ch - 1) / ch;
+    if (chunk < nch || kg + 1 >= nkg) break;
+    chunk -= nch;
+  }
   const int kg0 = 32 * KB * kg;           // first key of the workgroup
   const int kw0 = kg0 + 32 * kbl;         // first key of this wave
   const int key = kw0 + n;
@@ -208,9 +221,8 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) { dka[dt] = zero16(); dva[dt] = zero16(); }
 
-  const int nqt = (S + 31) / 32;
-  const int qt0 = CAUSAL ? kg0 / 32 : 0;
-  const int nq = nqt - qt0;
+  const int qt0 = (CAUSAL ? KB * kg : 0) + chunk * ch;  // this chunk's query tiles
+  const int nq = min(ch, nqt - qt0);
   const int rounds = G / HG;
   const int nsteps = rounds * nq;
 
@@ -385,7 +397,25 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
       }
     }
   }
-  if (hg == 0 && key < S) {
+  if (nch > 1) {
+    // One of several chunks: fp32 partials, summed in chunk order by
+    // attn_bwd_dkdv_reduce_kernel.
+    if (hg == 0 && key < S) {
+      float* pk = part + ((static_cast<int64_t>(bk) * nkg + kg) * maxch + chunk) * (KB * 32 * HD * 2) +
+                  (32 * kbl + n) * HD;
+      float* pv = pk + KB * 32 * HD;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * dt + 8 * j + 4 * hf;
+          *reinterpret_cast<float4*>(pk + d) =
+              make_float4(dka[dt][4 * j], dka[dt][4 * j + 1], dka[dt][4 * j + 2], dka[dt][4 * j + 3]);
+          *reinterpret_cast<float4*>(pv + d) =
+              make_float4(dva[dt][4 * j], dva[dt][4 * j + 1], dva[dt][4 * j + 2], dva[dt][4 * j + 3]);
+        }
+    }
+  } else if (hg == 0 && key < S) {
     bf16* kr = dk + b * dks0 + kvh * dks1 + static_cast<int64_t>(key) * dks2;
     bf16* vr = dv + b * dvs0 + kvh * dvs1 + static_cast<int64_t>(key) * dvs2;
 #pragma unroll
@@ -402,6 +432,39 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
             make_uint2(pack2<bf16>(c[4 * j], c[4 * j + 1]), pack2<bf16>(c[4 * j + 2], c[4 * j + 3]));
       }
   }
+}
+
+// Sums the chunk partials of key groups that were split (in chunk order),
+// scales dK and writes both gradients; one thread per 4 values of a row.
+template <int HD, bool CAUSAL, int KB>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_reduce_kernel(
+    const float* __restrict__ part, bf16* __restrict__ dk, bf16* __restrict__ dv, int Hkv, int S,
+    int ch, int maxch, int64_t total, int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0,
+    int64_t dvs1, int64_t dvs2, float scale) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int d = 4 * static_cast<int>(i % (HD / 4));
+  const int64_t row = i / (HD / 4);
+  const int key = static_cast<int>(row % S);
+  const int bk = static_cast<int>(row / S);
+  const int nkg = (S + 32 * KB - 1) / (32 * KB), nqt = (S + 31) / 32;
+  const int kg = key / (32 * KB);
+  const int nch = ((CAUSAL ? nqt - KB * kg : nqt) + ch - 1) / ch;
+  if (nch <= 1) return;
+  const float* pk = part + (static_cast<int64_t>(bk) * nkg + kg) * maxch * (KB * 32 * HD * 2) +
+                    (key - 32 * KB * kg) * HD + d;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f), c = a;
+  for (int j = 0; j < nch; ++j) {
+    const float4 x = *reinterpret_cast<const float4*>(pk + static_cast<int64_t>(j) * (KB * 32 * HD * 2));
+    const float4 y = *reinterpret_cast<const float4*>(pk + static_cast<int64_t>(j) * (KB * 32 * HD * 2) + KB * 32 * HD);
+    a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+    c.x += y.x; c.y += y.y; c.z += y.z; c.w += y.w;
+  }
+  const int b = bk / Hkv, kvh = bk - b * Hkv;
+  *reinterpret_cast<uint2*>(dk + b * dks0 + kvh * dks1 + key * dks2 + d) =
+      make_uint2(pack2<bf16>(a.x * scale, a.y * scale), pack2<bf16>(a.z * scale, a.w * scale));
+  *reinterpret_cast<uint2*>(dv + b * dvs0 + kvh * dvs1 + key * dvs2 + d) =
+      make_uint2(pack2<bf16>(c.x, c.y), pack2<bf16>(c.z, c.w));
 }
 
 // ---------------------------------------------------------------------------
@@ -740,8 +803,36 @@ int launch_rowdot(const BwdArgs& a, float* dvec, float* lse2) {
   return check_launch("attn_bwd: rowdot");
 }
 
+// Shape of the dK/dV launch.  Workgroup: KB blocks of 32 keys x HG head
+// groups (G % HG == 0): four head groups (8 waves) when the LDS ring fits
+// (hd <= 64), two when G is even, else one (four key blocks).  With fewer
+// than two key groups per CU the query range of each key group is cut into
+// chunks of ch tiles (fp32 partials + a reduce launch), so the long causal
+// walks of the first key groups spread over more CUs.
+struct DkdvPlan {
+  int KB, HG, ch, nwg, maxch;
+  size_t part_bytes;
+};
+
+DkdvPlan plan_dkdv(int hd, int S, int G, int BHkv, bool causal) {
+  DkdvPlan p{};
+  p.HG = (G % 4 == 0 && hd <= 64) ? 4 : (G % 2 == 0 ? 2 : 1);
+  p.KB = p.HG == 1 ? 4 : 2;
+  const int nkg = (S + 32 * p.KB - 1) / (32 * p.KB), nqt = (S + 31) / 32;
+  p.ch = nqt;
+  if (static_cast<int64_t>(nkg) * BHkv < 2 * static_cast<int64_t>(device_cus())) {
+    const char* e = std::getenv("HYDRA_ATTN_BWD_CHUNK");
+    p.ch = std::max(1, std::min(nqt, e ? std::atoi(e) : 16));
+  }
+  p.nwg = 0;
+  for (int kg = 0; kg < nkg; ++kg) p.nwg += ((causal ? nqt - p.KB * kg : nqt) + p.ch - 1) / p.ch;
+  p.maxch = (nqt + p.ch - 1) / p.ch;
+  p.part_bytes = p.maxch > 1 ? static_cast<size_t>(BHkv) * nkg * p.maxch * p.KB * 32 * hd * 2 * 4 : 0;
+  return p;
+}
+
 template <int HD, bool CAUSAL>
-int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2) {
+int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* part) {
   const float sl2 = a.scale * kLog2e;
   const int BHkv = a.B * a.Hkv, G = a.Hq / a.Hkv;
   const bf16* q = static_cast<const bf16*>(a.q);
@@ -749,28 +840,32 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2) {
   const bf16* v = static_cast<const bf16*>(a.v);
   const bf16* d = static_cast<const bf16*>(a.dout);
   {
-    // Workgroup shape: KB blocks of 32 keys x HG head groups (G % HG == 0).
-    // Four head groups (8 waves) when the LDS ring fits (hd <= 64), two when
-    // G is even, else one (four key blocks).
-    const int HGv = (G % 4 == 0 && HD <= 64) ? 4 : (G % 2 == 0 ? 2 : 1);
-    const int KB = HGv == 1 ? 4 : 2;
-    const int nkg = (a.S + 32 * KB - 1) / (32 * KB);
-    const dim3 grid(static_cast<unsigned>(nkg * BHkv));
-#define HYDRA_DKDV(KBV, HGV)                                                                    \
-  attn_bwd_dkdv_kernel<HD, CAUSAL, KBV, HGV><<<grid, 64 * KBV * HGV, 0, a.st>>>(                \
-      q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), a.Hq, a.Hkv, \
-      a.S, G, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2],  \
-      a.dos[0], a.dos[1], a.dos[2], a.dks[0], a.dks[1], a.dks[2], a.dvs[0], a.dvs[1],          \
-      a.dvs[2], sl2, a.scale)
-    if (HGv == 4) {
-      if constexpr (HD <= 64) HYDRA_DKDV(2, 4);
-    } else if (HGv == 2) {
-      HYDRA_DKDV(2, 2);
+    const DkdvPlan pl = plan_dkdv(HD, a.S, G, BHkv, CAUSAL);
+    const dim3 grid(static_cast<unsigned>(pl.nwg * BHkv));
+#define HYDRA_DKDV(KBV, HGV)                                                                     \
+  attn_bwd_dkdv_kernel<HD, CAUSAL, KBV, HGV><<<grid, 64 * KBV * HGV, 0, a.st>>>(                 \
+      q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), part, a.Hq,   \
+      a.Hkv, a.S, G, pl.nwg, pl.ch, pl.maxch, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1],      \
+      a.ks[2], a.vs[0], a.vs[1], a.vs[2], a.dos[0], a.dos[1], a.dos[2], a.dks[0], a.dks[1],     \
+      a.dks[2], a.dvs[0], a.dvs[1], a.dvs[2], sl2, a.scale);                                     \
+  if (int rc = check_launch("attn_bwd: dkdv")) return rc;                                       \
+  if (pl.maxch > 1) {                                                                            \
+    const int64_t total = static_cast<int64_t>(BHkv) * a.S * (HD / 4);                          \
+    attn_bwd_dkdv_reduce_kernel<HD, CAUSAL, KBV>                                                 \
+        <<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, a.st>>>(                    \
+            part, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), a.Hkv, a.S, pl.ch,         \
+            pl.maxch, total, a.dks[0], a.dks[1], a.dks[2], a.dvs[0], a.dvs[1], a.dvs[2],         \
+            a.scale);                                                                            \
+    if (int rc = check_launch("attn_bwd: dkdv reduce")) return rc;                              \
+  }
+    if (pl.HG == 4) {
+      if constexpr (HD <= 64) { HYDRA_DKDV(2, 4) }
+    } else if (pl.HG == 2) {
+      HYDRA_DKDV(2, 2)
     } else {
-      HYDRA_DKDV(4, 1);
+      HYDRA_DKDV(4, 1)
     }
 #undef HYDRA_DKDV
-    if (int rc = check_launch("attn_bwd: dkdv")) return rc;
   }
   const int ntasks = ((a.S + 31) / 32) * G;
   const int items = (ntasks + 3) / 4;
@@ -821,9 +916,10 @@ int run_generic(const BwdArgs& a, float* dvec, float* lse2) {
 }
 
 template <int HD>
-int run_mfma(const BwdArgs& a, float* dvec, float* lse2) {
+int run_mfma(const BwdArgs& a, float* dvec, float* lse2, float* part) {
   if (int rc = launch_rowdot<bf16>(a, dvec, lse2)) return rc;
-  return a.causal ? launch_mfma<HD, true>(a, dvec, lse2) : launch_mfma<HD, false>(a, dvec, lse2);
+  return a.causal ? launch_mfma<HD, true>(a, dvec, lse2, part)
+                  : launch_mfma<HD, false>(a, dvec, lse2, part);
 }
 
 }  // namespace
@@ -854,11 +950,6 @@ extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const
                 "attn_bwd: problem too large");
   auto st = static_cast<hipStream_t>(stream);
   const int64_t rows = B * Hq * S;
-  void* ws = nullptr;
-  if (int rc = device_workspace(kWsAttnBwd, static_cast<size_t>(rows) * 2 * sizeof(float), st, &ws))
-    return rc;
-  float* dvec = static_cast<float*>(ws);
-  float* lse2 = dvec + rows;
   const BwdArgs a{q, k, v, o, grad_o, lse, grad_q, grad_k, grad_v, static_cast<int>(B),
                   static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(S),
                   static_cast<int>(hd), qs, ks, vs, os, gos, gqs, gks, gvs, causal != 0, scale,
@@ -872,11 +963,22 @@ extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const
   for (const void* p : {q, k, v, grad_o, static_cast<const void*>(grad_q),
                         static_cast<const void*>(grad_k), static_cast<const void*>(grad_v)})
     mfma_ok = mfma_ok && aligned16(p);
+  // Workspace: D and lse2 per query row, then the dK/dV chunk partials.
+  const size_t rows_bytes = (static_cast<size_t>(rows) * 2 * sizeof(float) + 255) & ~size_t(255);
+  const size_t part_bytes =
+      mfma_ok ? plan_dkdv(static_cast<int>(hd), static_cast<int>(S), static_cast<int>(Hq / Hkv),
+                          static_cast<int>(B * Hkv), causal != 0).part_bytes
+              : 0;
+  void* ws = nullptr;
+  if (int rc = device_workspace(kWsAttnBwd, rows_bytes + part_bytes, st, &ws)) return rc;
+  float* dvec = static_cast<float*>(ws);
+  float* lse2 = dvec + rows;
+  float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + rows_bytes);
   if (mfma_ok) {
     switch (hd) {
-      case 32: return run_mfma<32>(a, dvec, lse2);
-      case 64: return run_mfma<64>(a, dvec, lse2);
-      default: return run_mfma<128>(a, dvec, lse2);
+      case 32: return run_mfma<32>(a, dvec, lse2, part);
+      case 64: return run_mfma<64>(a, dvec, lse2, part);
+      default: return run_mfma<128>(a, dvec, lse2, part);
     }
   }
   switch (dtype) {

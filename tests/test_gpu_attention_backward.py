@@ -117,3 +117,22 @@ def test_attention_backward_config3_shape(cuda):
     assert (dk64.sum(2).abs() / dk64.abs().sum(2)).max() < 1e-2
     want_v = go.double().view(B, Hkv, Hq // Hkv, S, hd).sum((2, 3))
     assert max_rel_err(dv64.sum(2), want_v) < 1e-2
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(1, 8, 2, 300, 64), (1, 3, 1, 200, 32), (2, 2, 2, 130, 128)])
+def test_attention_backward_query_chunks(cuda, monkeypatch, shape, causal):
+    """dK/dV with each key group's query range cut into chunks of 3 tiles
+    (fp32 partials summed in chunk order by the reduce launch), against the
+    oracle; deterministic across calls."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+
+    monkeypatch.setenv("HYDRA_ATTN_BWD_CHUNK", "3")
+    q, k, v, go = _inputs(*shape, torch.bfloat16, seed=sum(shape) + 5)
+    qd, kd, vd, god = (t.to(cuda) for t in (q, k, v, go))
+    out, lse = attention_forward(qd, kd, vd, causal=causal, want_lse=True)
+    first = attention_backward(qd, kd, vd, out, lse, god, causal=causal)
+    second = attention_backward(qd, kd, vd, out, lse, god, causal=causal)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+    _check(first, q, k, v, go, causal, TOL[torch.bfloat16])
