@@ -281,6 +281,35 @@ def bench_fused_ops(dev, iters=60):
     return res
 
 
+def bench_attention_backward(dev, iters=20):
+    """CCGQA attention backward (hydra_attn_bwd) at config 3's attention
+    shape: B 4, 4 query heads, 1 KV head, hd 64, S 4096, causal, bf16.
+    Algorithmic flops: the five causal products (S, dP, dV, dK, dQ),
+    5 * 2 * B * Hq * S^2 / 2 * hd.  Timed with events around `iters` calls
+    (each call: row-dot, dK/dV, chunk reduce and dQ launches)."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+
+    B, Hq, Hkv, S, hd = 4, 4, 1, 4096, 64
+    g = torch.Generator(device=dev).manual_seed(3)
+    q, do = (torch.randn(B, Hq, S, hd, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(B, Hkv, S, hd, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
+    out, lse = attention_forward(q, k, v, causal=True, want_lse=True)
+    for _ in range(3):
+        attention_backward(q, k, v, out, lse, do, causal=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        attention_backward(q, k, v, out, lse, do, causal=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    flops = 5 * 2 * B * Hq * S * S / 2 * hd
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"shape": "B4 Hq4 Hkv1 S4096 hd64 causal bf16", "ms": ms, "flops": flops,
+            "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS}
+
+
 def _bench_fused_backward(dev, g, iters):
     """The backward kernels at the config-2 shapes, called through the C ABI
     on preallocated buffers (algorithmic bytes: every input read once, every
@@ -475,6 +504,7 @@ def main():
     if not args.only_c3:
         line["fused_ops"] = bench_fused_ops(dev)
         line["mod"] = bench_mod(dev)
+        line["attention_backward"] = bench_attention_backward(dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))
