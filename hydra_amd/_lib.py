@@ -50,6 +50,7 @@ SIGNATURES = {
                        _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _I, _P],
     "hydra_attn_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                        _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
+    "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],
     "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
     "hydra_mod_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P],
     "hydra_mod_gather": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],

@@ -2,6 +2,11 @@
 (:13-37, :140-192) backed by the gfx950 HIP library."""
 
 from .fused_ops import (
+    CROSS_ENTROPY_CHUNK_SIZE,
+    USE_CHUNKED_CROSS_ENTROPY,
+    ChunkedCrossEntropyFunction,
+    chunked_cross_entropy,
+    fused_chunked_cross_entropy,
     HIP_AVAILABLE,
     TRITON_AVAILABLE,
     USE_FUSED_QK_NORM,
@@ -18,6 +23,11 @@ from .fused_ops import (
 )
 
 __all__ = [
+    "chunked_cross_entropy",
+    "fused_chunked_cross_entropy",
+    "ChunkedCrossEntropyFunction",
+    "CROSS_ENTROPY_CHUNK_SIZE",
+    "USE_CHUNKED_CROSS_ENTROPY",
     "fused_rope",
     "fused_qk_norm",
     "fused_swiglu",

@@ -18,6 +18,7 @@ import os
 from typing import Tuple
 
 import torch
+import torch.nn.functional as F
 
 from .. import _lib
 
@@ -332,3 +333,86 @@ def fused_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> 
     if weight.shape != (dim,):
         raise ValueError(f"fused_rms_norm: weight shape {tuple(weight.shape)} != ({dim},)")
     return _RMSNormFunction.apply(x, weight, eps)
+
+
+# ------------------------------------------------------- chunked cross-entropy
+# fused_ops.py:1299-1577.  The token rows' softmax cross-entropy (and its
+# gradient) run in hydra_ce_rows; the projections around it are plain GEMMs
+# (hipBLASLt through F.linear / matmul).  Unlike the reference, the count of
+# valid tokens stays on the device (no host synchronisation per chunk).
+USE_CHUNKED_CROSS_ENTROPY = True
+CROSS_ENTROPY_CHUNK_SIZE = 4096
+
+
+def _ce_rows(logits: torch.Tensor, targets: torch.Tensor, ignore_index: int,
+             grad: torch.Tensor = None, grad_scale: torch.Tensor = None) -> torch.Tensor:
+    """Per-row loss logsumexp(x) - x[t] (fp32, 0 for ignored rows) of a
+    [rows, V] logits block with unit column stride; with `grad` (may be
+    `logits` itself) also writes (softmax(x) - onehot(t)) * grad_scale[0]."""
+    rows, V = logits.shape
+    loss = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    _lib.call("hydra_ce_rows", logits.data_ptr(), rows, V, logits.stride(0), targets.data_ptr(),
+              int(ignore_index), loss.data_ptr(), None, _lib.ptr(grad),
+              grad.stride(0) if grad is not None else V, _lib.ptr(grad_scale),
+              _lib.dtype_code(logits), _lib.stream(logits))
+    return loss
+
+
+class ChunkedCrossEntropyFunction(torch.autograd.Function):
+    """fused_ops.py:1382-1531: mean token cross-entropy of hidden @ weight^T
+    over tokens whose target is not ignore_index, computed chunk by chunk
+    (logits of at most chunk_size tokens exist at a time); the backward
+    recomputes each chunk's logits in fp32.  Out-of-range targets are
+    clamped into [0, vocab) as the reference does (:1407-1422, without its
+    warning, which needs a host synchronisation).  No valid token: loss 0
+    and zero gradients."""
+
+    @staticmethod
+    def forward(ctx, hidden_states, weight, targets, ignore_index, chunk_size):
+        _lib.require_gpu("chunked_cross_entropy", hidden_states, weight, targets)
+        dim = hidden_states.shape[-1]
+        h = hidden_states.reshape(-1, dim)
+        t = targets.reshape(-1).to(torch.int64).contiguous()
+        total = torch.zeros((), dtype=torch.float32, device=h.device)
+        for s in range(0, h.shape[0], chunk_size):
+            logits = F.linear(h[s:s + chunk_size], weight).contiguous()
+            total = total + _ce_rows(logits, t[s:s + chunk_size], ignore_index).sum()
+        n_valid = (t != ignore_index).sum()
+        ctx.save_for_backward(hidden_states, weight, t, n_valid)
+        ctx.ignore_index, ctx.chunk_size = int(ignore_index), int(chunk_size)
+        loss = torch.where(n_valid > 0, total / n_valid.clamp(min=1), torch.zeros_like(total))
+        return loss.to(hidden_states.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        hidden_states, weight, t, n_valid = ctx.saved_tensors
+        dim = hidden_states.shape[-1]
+        h = hidden_states.reshape(-1, dim)
+        wf = weight.float()
+        scale = (grad_output.float() / n_valid.clamp(min=1)).reshape(1).contiguous()
+        grad_h = torch.empty(h.shape, dtype=torch.float32, device=h.device)
+        grad_w = torch.zeros(weight.shape, dtype=torch.float32, device=h.device)
+        cs = ctx.chunk_size
+        for s in range(0, h.shape[0], cs):
+            hc = h[s:s + cs].float()
+            g = F.linear(hc, wf).contiguous()  # logits, overwritten by their gradient
+            _ce_rows(g, t[s:s + cs], ctx.ignore_index, grad=g, grad_scale=scale)
+            grad_h[s:s + cs] = g @ wf
+            grad_w += g.t() @ hc
+        return (grad_h.view_as(hidden_states).to(hidden_states.dtype), grad_w.to(weight.dtype),
+                None, None, None)
+
+
+def chunked_cross_entropy(hidden_states: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                          ignore_index: int = -100, chunk_size: int = None) -> torch.Tensor:
+    """fused_ops.py:1303-1379 (same value; the gradient runs through the HIP
+    backward of ChunkedCrossEntropyFunction)."""
+    return ChunkedCrossEntropyFunction.apply(hidden_states, weight, targets, ignore_index,
+                                             chunk_size or CROSS_ENTROPY_CHUNK_SIZE)
+
+
+def fused_chunked_cross_entropy(hidden_states: torch.Tensor, weight: torch.Tensor,
+                                targets: torch.Tensor, ignore_index: int = -100,
+                                chunk_size: int = None) -> torch.Tensor:
+    """fused_ops.py:1534-1577 (its Liger branch does not apply: no Liger here)."""
+    return chunked_cross_entropy(hidden_states, weight, targets, ignore_index, chunk_size)

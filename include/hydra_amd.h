@@ -253,6 +253,23 @@ int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                    const int64_t* gos, const int64_t* gqs, const int64_t* gks,
                    const int64_t* gvs, int causal, float scale, int dtype, void* stream);
 
+/* ---- LM-head loss (hydra/kernels/fused_ops.py) ------------------------- */
+
+/* Token-row softmax cross-entropy of a logits block x [rows, vocab] (unit
+ * column stride, row stride logits_rs): loss[r] = logsumexp(x[r]) - x[r, t]
+ * in fp32 (0 when targets[r] == ignore_index; other targets are clamped
+ * into [0, vocab)); lse[r] (optional) = logsumexp(x[r]).  With grad
+ * non-null, also writes grad[r] = (softmax(x[r]) - onehot(t)) * grad_scale[0]
+ * (zero rows for ignored tokens; grad may alias logits; grad_scale is a
+ * device pointer, so the caller's loss scale needs no host round trip).
+ * targets: int64.  Replaces the per-chunk F.cross_entropy and the gradient
+ * of ChunkedCrossEntropyFunction (fused_ops.py:1303-1379, 1382-1531); the
+ * projections around it stay plain GEMMs. */
+int hydra_ce_rows(const void* logits, int64_t rows, int64_t vocab, int64_t logits_rs,
+                  const int64_t* targets, int64_t ignore_index, float* loss, float* lse,
+                  void* grad, int64_t grad_rs, const float* grad_scale, int dtype,
+                  void* stream);
+
 /* ---- Mixture-of-Depths hard routing (hydra/routing, model/framework) --- */
 
 /* Per-row top-k of router scores, ties broken by the lower index, in the

@@ -136,3 +136,29 @@ def rope_backward(grad_out: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) 
     g1, g2 = g[..., ::2], g[..., 1::2]
     out = torch.stack([g1 * cos + g2 * sin, -g1 * sin + g2 * cos], dim=-1).flatten(-2)
     return out.to(grad_out.dtype)
+
+
+def chunked_cross_entropy(hidden, weight, targets, ignore_index=-100, grad_output=1.0):
+    """fp64 restatement of ChunkedCrossEntropyFunction (fused_ops.py:1382-1531):
+    logits = h W^T; targets other than ignore_index clamped into [0, V)
+    (:1407-1422); loss = mean over valid tokens of logsumexp(x) - x[t]
+    (0 with none); grad_x = (softmax(x) - onehot(t)) * grad_output / n_valid
+    on valid rows, 0 on ignored rows; grad_h = grad_x W, grad_W = grad_x^T h.
+    Returns (loss, grad_h, grad_W) in fp64.  Pinned against autograd of
+    F.cross_entropy in tests/test_oracle_pins.py."""
+    dim = hidden.shape[-1]
+    h = hidden.reshape(-1, dim).double()
+    w = weight.double()
+    t = targets.reshape(-1).long()
+    V = w.shape[0]
+    valid = t != ignore_index
+    tc = torch.where(valid, t.clamp(0, V - 1), torch.zeros_like(t))
+    x = h @ w.t()
+    lse = torch.logsumexp(x, -1)
+    rows = lse - x.gather(1, tc[:, None])[:, 0]
+    n = int(valid.sum())
+    loss = (rows * valid).sum() / n if n else torch.zeros((), dtype=torch.float64)
+    g = torch.softmax(x, -1)
+    g[torch.arange(len(t)), tc] -= 1.0
+    g = g * valid[:, None] * (grad_output / max(n, 1))
+    return loss, (g @ w).view(hidden.shape), g.t() @ h

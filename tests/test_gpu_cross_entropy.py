@@ -1,0 +1,63 @@
+"""GPU parity of the chunked LM-head cross-entropy (hydra_ce_rows plus the
+GEMMs around it) against the oracle's fp64 restatement of
+ChunkedCrossEntropyFunction (pinned by autograd of F.cross_entropy in
+tests/test_oracle_pins.py): the loss and both gradients.  Tolerance: fp32
+1e-5, bf16 2e-2 (max-rel-err; the forward's logits are bf16 GEMM outputs, as
+in the reference)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import max_rel_err
+from oracle import fused_ops as ofo
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(B, S, D, V, dtype, seed, ignore_frac=0.1):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(B, S, D, generator=g).to(dtype)
+    w = (torch.randn(V, D, generator=g) * 0.05).to(dtype)
+    t = torch.randint(0, V, (B, S), generator=g)
+    t[torch.rand(B, S, generator=g) < ignore_frac] = -100
+    return h, w, t
+
+
+@pytest.mark.parametrize("dtype,shape,chunk", [
+    (torch.float32, (2, 300, 64, 1000), 128),    # ragged last chunk
+    (torch.float32, (1, 50, 32, 1001), 4096),    # one chunk, V not a multiple of 8
+    (torch.bfloat16, (2, 256, 128, 32000), 192),  # LM-head vocab
+])
+def test_chunked_cross_entropy(cuda, dtype, shape, chunk):
+    from hydra_amd.kernels import fused_chunked_cross_entropy
+
+    h, w, t = _case(*shape, dtype, seed=sum(shape))
+    hd, wd = h.to(cuda).requires_grad_(), w.to(cuda).requires_grad_()
+    loss = fused_chunked_cross_entropy(hd, wd, t.to(cuda), chunk_size=chunk)
+    loss.backward(torch.tensor(0.5, device=cuda, dtype=dtype))
+    ref, gh, gw = ofo.chunked_cross_entropy(h, w, t, grad_output=0.5)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert loss.dtype == dtype
+    assert abs(loss.item() - ref.item()) / abs(ref.item()) < tol
+    assert max_rel_err(hd.grad.cpu(), gh) < tol
+    assert max_rel_err(wd.grad.cpu(), gw) < tol
+
+
+def test_chunked_cross_entropy_edge_targets(cuda):
+    """All targets ignored: loss 0, zero gradients.  Out-of-range targets are
+    clamped into [0, V) (fused_ops.py:1407-1422)."""
+    from hydra_amd.kernels import chunked_cross_entropy
+
+    h, w, t = _case(1, 40, 32, 100, torch.float32, seed=2)
+    hd, wd = h.to(cuda).requires_grad_(), w.to(cuda).requires_grad_()
+    loss = chunked_cross_entropy(hd, wd, torch.full_like(t, -100).to(cuda), chunk_size=16)
+    loss.backward()
+    assert loss.item() == 0 and hd.grad.abs().max() == 0 and wd.grad.abs().max() == 0
+    t[0, 3], t[0, 9] = 150, -5
+    hd.grad = wd.grad = None
+    loss = chunked_cross_entropy(hd, wd, t.to(cuda), chunk_size=16)
+    loss.backward()
+    ref, gh, gw = ofo.chunked_cross_entropy(h, w, t)
+    assert abs(loss.item() - ref.item()) / abs(ref.item()) < 1e-5
+    assert max_rel_err(hd.grad.cpu(), gh) < 1e-5 and max_rel_err(wd.grad.cpu(), gw) < 1e-5
