@@ -310,6 +310,33 @@ def bench_attention_backward(dev, iters=20):
             "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS}
 
 
+def bench_cross_entropy(dev, iters=20):
+    """hydra_ce_rows on one chunk of the LM-head loss: 4096 tokens x vocab
+    32000.  Forward: bf16 logits -> per-row loss (algorithmic bytes: the
+    logits read once).  Backward: fp32 logits rewritten in place with their
+    gradient (read once + written once; the kernel's second read of a row
+    mostly hits L2/MALL)."""
+    from hydra_amd import _lib
+
+    rows, V = 4096, 32000
+    g = torch.Generator(device=dev).manual_seed(5)
+    t = torch.randint(0, V, (rows,), device=dev, generator=g)
+    loss = torch.empty(rows, device=dev)
+    scale = torch.full((1,), 1.0 / rows, device=dev)
+    res = {"shape": "4096 tokens x vocab 32000"}
+    for name, dt, grad in (("forward_bf16", torch.bfloat16, False), ("backward_fp32", torch.float32, True)):
+        sets = [torch.randn(rows, V, device=dev, generator=g).to(dt) for _ in range(2)]
+        call = lambda x: _lib.call("hydra_ce_rows", x.data_ptr(), rows, V, V, t.data_ptr(), -100,
+                                   loss.data_ptr(), None, x.data_ptr() if grad else None, V,
+                                   scale.data_ptr() if grad else None, _lib.dtype_code(x), _lib.stream(x))
+        ms = _time_rotating(call, [(x,) for x in sets], iters)
+        nbytes = rows * V * sets[0].element_size() * (2 if grad else 1)
+        res[name] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6,
+                     "pct_peak": nbytes / ms / 1e6 / 8000 * 100}
+        del sets
+    return res
+
+
 def _bench_fused_backward(dev, g, iters):
     """The backward kernels at the config-2 shapes, called through the C ABI
     on preallocated buffers (algorithmic bytes: every input read once, every
@@ -505,6 +532,7 @@ def main():
         line["fused_ops"] = bench_fused_ops(dev)
         line["mod"] = bench_mod(dev)
         line["attention_backward"] = bench_attention_backward(dev)
+        line["cross_entropy"] = bench_cross_entropy(dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

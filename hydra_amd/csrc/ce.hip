@@ -10,9 +10,10 @@
 // grad_W = grad_x^T h) are plain GEMMs and stay on hipBLASLt.
 //
 // One 256-thread workgroup per row: an online (max, sum-exp) pass with
-// 16-byte loads, a workgroup reduction, then (backward) a second pass that
-// rewrites the row in place.  HBM-bound: a row is read once (twice with the
-// gradient, the second read mostly from L2/MALL) and written once.
+// 16-byte loads, a workgroup reduction, then (backward) the row rewritten
+// in place.  HBM-bound: a row is read once and written once -- rows of up to
+// 32 16-byte chunks per thread (vocab <= 32768 fp32 / 65536 bf16) are held
+// in registers between the two phases, longer rows are read a second time.
 #include "common.h"
 
 namespace hydra {
@@ -58,6 +59,12 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(
     const float m2 = __shfl_xor(m, off), s2 = __shfl_xor(s, off);
     lse_merge(m, s, m2, s2);
   }
+  // x[t] is read before the barrier: with grad == logits, other threads
+  // overwrite the row after it.
+  const int64_t t_raw = targets[row];
+  const bool valid = t_raw != ignore_index;
+  const int t = static_cast<int>(t_raw < 0 ? 0 : (t_raw >= V ? V - 1 : t_raw));
+  const float xt = tid == 0 ? to_f32(x[t]) : 0.f;
   if (lane == 0) { red_m[wave] = m; red_s[wave] = s; }
   __syncthreads();
   m = red_m[0];
@@ -65,11 +72,8 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(
 #pragma unroll
   for (int w = 1; w < 4; ++w) lse_merge(m, s, red_m[w], red_s[w]);
   const float lse2 = m + __log2f(s);  // log2-domain logsumexp
-  const int64_t t_raw = targets[row];
-  const bool valid = t_raw != ignore_index;
-  const int t = static_cast<int>(t_raw < 0 ? 0 : (t_raw >= V ? V - 1 : t_raw));
   if (tid == 0) {
-    loss[row] = valid ? (lse2 - to_f32(x[t]) * kLog2e) * kLn2 : 0.f;
+    loss[row] = valid ? (lse2 - xt * kLog2e) * kLn2 : 0.f;
     if (lse_out) lse_out[row] = lse2 * kLn2;
   }
   if constexpr (GRAD) {
@@ -93,6 +97,81 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(
   }
 }
 
+// Gradient variant for rows that fit in registers (V <= 256 * NCH * E):
+// the row is read from HBM once, kept in VGPRs across the reduction, and
+// rewritten from there.
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void ce_rows_reg_kernel(
+    const T* __restrict__ logits, int64_t rs, const int64_t* __restrict__ targets,
+    float* __restrict__ loss, float* __restrict__ lse_out, T* grad, int64_t grs,
+    const float* __restrict__ grad_scale, int V, int64_t ignore_index) {
+  constexpr int E = 16 / int(sizeof(T));
+  __shared__ float red_m[4], red_s[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const T* x = logits + row * rs;
+  float v[NCH][E];
+  float m = -INFINITY, s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = (c * 256 + tid) * E;
+    if (e < V) {
+      load16<T>(x + e, v[c]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) v[c][i] = -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    float cm = v[c][0] * kLog2e;
+#pragma unroll
+    for (int i = 1; i < E; ++i) cm = fmaxf(cm, v[c][i] * kLog2e);
+    if (cm == -INFINITY) continue;
+    float cs = 0.f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) cs += __builtin_amdgcn_exp2f(fmaf(v[c][i], kLog2e, -cm));
+    lse_merge(m, s, cm, cs);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(m, off), s2 = __shfl_xor(s, off);
+    lse_merge(m, s, m2, s2);
+  }
+  // x[t] is read before the barrier: with grad == logits, other threads
+  // overwrite the row after it.
+  const int64_t t_raw = targets[row];
+  const bool valid = t_raw != ignore_index;
+  const int t = static_cast<int>(t_raw < 0 ? 0 : (t_raw >= V ? V - 1 : t_raw));
+  const float xt = tid == 0 ? to_f32(x[t]) : 0.f;
+  if (lane == 0) { red_m[wave] = m; red_s[wave] = s; }
+  __syncthreads();
+  m = red_m[0];
+  s = red_s[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) lse_merge(m, s, red_m[w], red_s[w]);
+  const float lse2 = m + __log2f(s);
+  if (tid == 0) {
+    loss[row] = valid ? (lse2 - xt * kLog2e) * kLn2 : 0.f;
+    if (lse_out) lse_out[row] = lse2 * kLn2;
+  }
+  const float sc = valid ? *grad_scale : 0.f;
+  T* g = grad + row * grs;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = (c * 256 + tid) * E;
+    if (e < V) {
+      float o[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(v[c][i], kLog2e, -lse2));
+        o[i] = (p - (e + i == t ? 1.f : 0.f)) * sc;
+      }
+      store16<T>(g + e, o);
+    }
+  }
+}
+
 template <typename T, bool GRAD>
 int launch(const void* logits, int64_t rs, const int64_t* targets, float* loss, float* lse,
            void* grad, int64_t grs, const float* scale, int64_t rows, int V, int64_t ignore,
@@ -103,6 +182,19 @@ int launch(const void* logits, int64_t rs, const int64_t* targets, float* loss, 
   const dim3 grid(static_cast<unsigned>(rows));
   const T* x = static_cast<const T*>(logits);
   T* g = static_cast<T*>(grad);
+  if constexpr (GRAD) {
+    // Register-resident rows: up to 32 chunks of 16 bytes per thread.
+    const int nch = (V / E + 255) / 256;
+    if (vec && nch <= 32) {
+#define HYDRA_CE_REG(N) \
+  ce_rows_reg_kernel<T, N><<<grid, 256, 0, st>>>(x, rs, targets, loss, lse, g, grs, scale, V, ignore)
+      if (nch <= 8) HYDRA_CE_REG(8);
+      else if (nch <= 16) HYDRA_CE_REG(16);
+      else HYDRA_CE_REG(32);
+#undef HYDRA_CE_REG
+      return check_launch("ce_rows");
+    }
+  }
   if (vec)
     ce_rows_kernel<T, true, GRAD><<<grid, 256, 0, st>>>(x, rs, targets, loss, lse, g, grs, scale, V, ignore);
   else
