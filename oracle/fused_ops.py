@@ -162,3 +162,25 @@ def chunked_cross_entropy(hidden, weight, targets, ignore_index=-100, grad_outpu
     g[torch.arange(len(t)), tc] -= 1.0
     g = g * valid[:, None] * (grad_output / max(n, 1))
     return loss, (g @ w).view(hidden.shape), g.t() @ h
+
+
+def token_losses_from_hidden(hidden, weight, targets, ignore_index=-100):
+    """fp64 restatement of compute_token_losses_from_hidden
+    (hydra/training/loop.py:28-89): per-token logsumexp(x) - x[t], 0 where
+    the target is ignore_index; when some non-ignored target is out of
+    [0, V), the whole target vector (ignore entries included) is clamped
+    into [0, V) and validity recomputed (:54-70)."""
+    B, L, D = hidden.shape
+    w = weight.double()
+    V = w.shape[0]
+    h = hidden.reshape(-1, D).double()
+    t = targets.reshape(-1).long().clone()
+    valid = t != ignore_index
+    vt = t[valid]
+    if vt.numel() and ((vt < 0) | (vt >= V)).any():
+        t = t.clamp(0, V - 1)
+        valid = t != ignore_index
+    x = h @ w.t()
+    tc = torch.where(valid, t, torch.zeros_like(t))
+    loss = torch.logsumexp(x, -1) - x.gather(1, tc[:, None])[:, 0]
+    return (loss * valid).view(B, L)

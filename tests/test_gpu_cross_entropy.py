@@ -61,3 +61,19 @@ def test_chunked_cross_entropy_edge_targets(cuda):
     ref, gh, gw = ofo.chunked_cross_entropy(h, w, t)
     assert abs(loss.item() - ref.item()) / abs(ref.item()) < 1e-5
     assert max_rel_err(hd.grad.cpu(), gh) < 1e-5 and max_rel_err(wd.grad.cpu(), gw) < 1e-5
+
+
+@pytest.mark.parametrize("oob", [False, True])
+def test_token_losses_from_hidden(cuda, oob):
+    """compute_token_losses_from_hidden (loop.py:28-89) against the oracle,
+    fp32 throughout (1e-5), token chunks with a ragged tail."""
+    from hydra_amd.training import compute_token_losses_from_hidden
+
+    h, w, t = _case(2, 150, 64, 3000, torch.bfloat16, seed=21)
+    if oob:
+        t[1, 7] = 3005
+    got = compute_token_losses_from_hidden(h.to(cuda), w.to(cuda), t.to(cuda), token_chunk_size=128)
+    ref = ofo.token_losses_from_hidden(h.float(), w.float(), t)
+    assert got.dtype == torch.float32 and got.shape == (2, 150)
+    assert max_rel_err(got.cpu(), ref) < 1e-5
+    assert (got.cpu()[ref == 0] == 0).all()

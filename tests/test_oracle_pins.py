@@ -511,3 +511,21 @@ def test_chunked_cross_entropy_autograd():
     assert torch.allclose(gw, w.grad, rtol=1e-10, atol=1e-13)
     loss0, gh0, gw0 = ofo.chunked_cross_entropy(h.detach(), w.detach(), torch.full((3, 7), -100))
     assert loss0 == 0 and gh0.abs().max() == 0 and gw0.abs().max() == 0
+
+
+def test_token_losses_match_cross_entropy_none():
+    """token_losses_from_hidden = F.cross_entropy(reduction='none') (fp64)
+    with ignore_index; with an out-of-range target the reference clamps the
+    ignore entries too, so they turn into target-0 losses."""
+    g = torch.Generator().manual_seed(12)
+    h = torch.randn(2, 5, 8, generator=g, dtype=torch.float64)
+    w = torch.randn(30, 8, generator=g, dtype=torch.float64)
+    t = torch.randint(0, 30, (2, 5), generator=g)
+    t[0, 0] = -100
+    ref = F.cross_entropy(h.reshape(-1, 8) @ w.t(), t.reshape(-1), ignore_index=-100, reduction="none")
+    assert torch.allclose(ofo.token_losses_from_hidden(h, w, t).reshape(-1), ref, rtol=1e-12)
+    t[1, 1] = 31
+    got = ofo.token_losses_from_hidden(h, w, t).reshape(-1)
+    tc = t.clamp(0, 29).reshape(-1)
+    ref = F.cross_entropy(h.reshape(-1, 8) @ w.t(), tc, reduction="none")
+    assert torch.allclose(got, ref, rtol=1e-12) and got[0] > 0
