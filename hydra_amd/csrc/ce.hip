@@ -32,7 +32,7 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2
 
 template <typename T, bool VEC, bool GRAD>
 __global__ __launch_bounds__(256) void ce_rows_kernel(
-    const T* logits, int64_t rs,  // may alias grad const int64_t* __restrict__ targets,
+    const T* logits, int64_t rs, const int64_t* __restrict__ targets,  // logits may alias grad
     float* __restrict__ loss, float* __restrict__ lse_out, T* grad, int64_t grs,
     const float* __restrict__ grad_scale, int V, int64_t ignore_index) {
   constexpr int E = VEC ? 16 / int(sizeof(T)) : 1;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(
 // rewritten from there.
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void ce_rows_reg_kernel(
-    const T* logits, int64_t rs,  // may alias grad const int64_t* __restrict__ targets,
+    const T* logits, int64_t rs, const int64_t* __restrict__ targets,  // logits may alias grad
     float* __restrict__ loss, float* __restrict__ lse_out, T* grad, int64_t grs,
     const float* __restrict__ grad_scale, int V, int64_t ignore_index) {
   constexpr int E = 16 / int(sizeof(T));
