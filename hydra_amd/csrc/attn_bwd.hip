@@ -12,8 +12,8 @@
 //
 // Three launches on the bf16 path (v_mfma_f32_32x32x16_bf16):
 //  * attn_bwd_rowdot_kernel: D and lse * log2(e) per query row (fp32).
-//  * attn_bwd_dkdv_kernel: lanes own keys.  A workgroup is 4 waves, KB key
-//    blocks of 32 keys x HG = 4/KB head groups; a step stages 32 query rows
+//  * attn_bwd_dkdv_kernel: lanes own keys.  A workgroup is KB key blocks of
+//    32 keys x HG head groups (one wave each); a step stages 32 query rows
 //    of Q and dO for HG heads in LDS, row-major (A operand of S = Q K^T and
 //    dP = dO V^T) and transposed (A operand of dV^T += dO^T P and
 //    dK^T += Q^T dS), so the KB waves of a head group share each staged
@@ -803,9 +803,10 @@ int launch_rowdot(const BwdArgs& a, float* dvec, float* lse2) {
   return check_launch("attn_bwd: rowdot");
 }
 
-// Shape of the dK/dV launch.  Workgroup: KB blocks of 32 keys x HG head
-// groups (G % HG == 0): four head groups (8 waves) when the LDS ring fits
-// (hd <= 64), two when G is even, else one (four key blocks).  With fewer
+// Shape of the dK/dV launch.  Workgroup: KB = 4 blocks of 32 keys x HG
+// head groups (G % HG == 0): two head groups (8 waves) when G is even, else
+// one.  Four waves share each staged query tile (measured at config 3: 4 x 2
+// beats 2 x 4 by 10%, the LDS writes of the staging halve).  With fewer
 // than two key groups per CU the query range of each key group is cut into
 // chunks of ch tiles (fp32 partials + a reduce launch), so the long causal
 // walks of the first key groups spread over more CUs.
@@ -816,8 +817,8 @@ struct DkdvPlan {
 
 DkdvPlan plan_dkdv(int hd, int S, int G, int BHkv, bool causal) {
   DkdvPlan p{};
-  p.HG = (G % 4 == 0 && hd <= 64) ? 4 : (G % 2 == 0 ? 2 : 1);
-  p.KB = p.HG == 1 ? 4 : 2;
+  p.HG = G % 2 == 0 ? 2 : 1;
+  p.KB = 4;
   const int nkg = (S + 32 * p.KB - 1) / (32 * p.KB), nqt = (S + 31) / 32;
   p.ch = nqt;
   if (static_cast<int64_t>(nkg) * BHkv < 2 * static_cast<int64_t>(device_cus())) {
@@ -858,10 +859,8 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* p
             a.scale);                                                                            \
     if (int rc = check_launch("attn_bwd: dkdv reduce")) return rc;                              \
   }
-    if (pl.HG == 4) {
-      if constexpr (HD <= 64) { HYDRA_DKDV(2, 4) }
-    } else if (pl.HG == 2) {
-      HYDRA_DKDV(2, 2)
+    if (pl.HG == 2) {
+      HYDRA_DKDV(4, 2)
     } else {
       HYDRA_DKDV(4, 1)
     }
