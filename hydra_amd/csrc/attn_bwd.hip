@@ -41,6 +41,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kDqWaves = 4;    // query tasks (waves) per dQ workgroup
 constexpr int kVmcnt0 = 0x3f70;  // s_waitcnt vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
 
 __device__ __forceinline__ f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
@@ -479,8 +480,8 @@ struct DqLayout {
   static constexpr int STAGE = 2 * ROWS + TRS;  // K, V, K^T
 };
 
-template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
+template <int HD, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
     bf16* __restrict__ dq, int Hq, int Hkv, int S, int G, int ntasks, int items,
@@ -494,7 +495,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   constexpr int DT = HD / 32;
   constexpr int DC = HD / 8;
   constexpr int UNITS = (BN / 2) * DC;        // (key pair, chunk) staging units
-  constexpr int UPT = (UNITS + 255) / 256;
+  constexpr int NT = 64 * NW;
+  constexpr int UPT = (UNITS + NT - 1) / NT;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * L::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -504,7 +506,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   const int bk = blockIdx.x % BHkv;
   const int item = items - 1 - static_cast<int>(blockIdx.x / BHkv);  // longest first
   const int b = bk / Hkv, kvh = bk - b * Hkv;
-  const int task = 4 * item + wave;
+  const int task = NW * item + wave;
   const bool active = task < ntasks;
   const int qb = (active ? task : ntasks - 1) / G;
   const int h = kvh * G + (active ? task : ntasks - 1) % G;
@@ -535,7 +537,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
 
   // Keys the item needs: up to its last query (causal) or all of them.
-  const int last_task = min(4 * item + 3, ntasks - 1);
+  const int last_task = min(NW * item + NW - 1, ntasks - 1);
   const int qmax = min(32 * (last_task / G) + 31, S - 1);
   const int nkt = CAUSAL ? qmax / BN + 1 : (S + BN - 1) / BN;
   const int my_last = CAUSAL ? min(q0 + 31, S - 1) : S - 1;  // this wave's last visible key
@@ -549,8 +551,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   auto fetch = [&](int kt, Regs& R) {
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
-      const int unit = tid + 256 * u;
-      if (UNITS % 256 == 0 || unit < UNITS) {
+      const int unit = tid + NT * u;
+      if (UNITS % NT == 0 || unit < UNITS) {
         const int c = unit >> 5, p = unit & 31;  // p fastest: conflict-free transposed writes
         const int k0 = BN * kt + 2 * p;  // keys >= S read as zero
         const int ko = k0 * static_cast<int>(ks2) * 2 + 16 * c;
@@ -566,8 +568,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
     uint16_t* st = smem + buf * L::STAGE;
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
-      const int unit = tid + 256 * u;
-      if (UNITS % 256 == 0 || unit < UNITS) {
+      const int unit = tid + NT * u;
+      if (UNITS % NT == 0 || unit < UNITS) {
         const int c = unit >> 5, p = unit & 31;  // p fastest: conflict-free transposed writes
         *reinterpret_cast<uint4*>(&st[(2 * p) * L::KP + 8 * c]) = R.k[u][0];
         *reinterpret_cast<uint4*>(&st[(2 * p + 1) * L::KP + 8 * c]) = R.k[u][1];
@@ -866,9 +868,12 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* p
     }
 #undef HYDRA_DKDV
   }
+  // dQ: an item is NW query tasks (32 query rows of one head) sharing each
+  // staged K/V tile.
+  constexpr int NW = kDqWaves;
   const int ntasks = ((a.S + 31) / 32) * G;
-  const int items = (ntasks + 3) / 4;
-  attn_bwd_dq_kernel<HD, CAUSAL><<<dim3(static_cast<unsigned>(items * BHkv)), 256, 0, a.st>>>(
+  const int items = (ntasks + NW - 1) / NW;
+  attn_bwd_dq_kernel<HD, CAUSAL, NW><<<dim3(static_cast<unsigned>(items * BHkv)), 64 * NW, 0, a.st>>>(
       q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dq), a.Hq, a.Hkv, a.S, G, ntasks, items,
       a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2], a.dos[0],
       a.dos[1], a.dos[2], a.dqs[0], a.dqs[1], a.dqs[2], sl2, a.scale);
