@@ -226,6 +226,26 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
   const int nq = min(ch, nqt - qt0);
   const int rounds = G / HG;
   const int nsteps = rounds * nq;
+  // Step order: round-major over the chunk's query tiles, except that when
+  // the chunk starts with all KB tiles that hold the waves' diagonals
+  // (tiles KB kg .. KB kg + KB - 1), those come first for every round
+  // (steps [0, ediag)), so the remaining steps run the unmasked tile code
+  // only.  A chunk holding only part of that region (chunks shorter than
+  // KB tiles) takes the masking dispatch for every step.
+  const int dreg = CAUSAL ? max(0, min(KB * kg + KB - qt0, nq)) : 0;
+  const int nd = dreg == KB ? KB : 0;
+  const int nr = max(nq - nd, 1);
+  const int ediag = nd ? rounds * nd : (dreg > 0 ? nsteps : 0);
+  auto locate = [&](int step, int& hr, int& qt) {
+    if (step < rounds * nd) {
+      hr = step / nd;
+      qt = qt0 + (step - hr * nd);
+    } else {
+      const int s2 = step - rounds * nd;
+      hr = s2 / nr;
+      qt = qt0 + nd + (s2 - hr * nr);
+    }
+  };
 
   // Staging registers: per unit the chunk c of rows 2p, 2p+1 of Q and dO.
   struct Regs {
@@ -234,7 +254,8 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
   };
   Regs ra, rb;
   auto fetch = [&](int step, Regs& R) {
-    const int hr = step / nq, qt = qt0 + (step - hr * nq);
+    int hr, qt;
+    locate(step, hr, qt);
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int unit = tid + NT * u;
@@ -339,7 +360,8 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
     }
   };
   auto compute = [&](int step, int buf) {
-    const int hr = step / nq, qt = qt0 + (step - hr * nq);
+    int hr, qt;
+    locate(step, hr, qt);
     const int q0 = 32 * qt;
     // Causal: the tile reaches this wave's keys iff q0 + 31 >= kw0; only
     // the diagonal tile q0 == kw0 needs the key <= query mask.
@@ -356,14 +378,31 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
   land(0, ra);
   fetch(min(1, last), rb);
   __syncthreads();
+  // Past ediag every wave is strictly below the diagonal: tile<false> only,
+  // in a loop of its own (no masked path to join, so no accumulator copies).
+  auto unmasked = [&](int step, int buf) {
+    int hr, qt;
+    locate(step, hr, qt);
+    tile(std::false_type{}, 32 * qt, buf);
+  };
   int step = 0;
-  for (; step < last; step += 2) {
+  for (; step < last && step + 1 < ediag; step += 2) {  // ediag is even or nsteps
     fetch(min(step + 2, last), ra);
     compute(step, 0);
     land(1, rb);
     __syncthreads();
     fetch(min(step + 3, last), rb);
     compute(step + 1, 1);
+    land(0, ra);
+    __syncthreads();
+  }
+  for (; step < last; step += 2) {
+    fetch(min(step + 2, last), ra);
+    unmasked(step, 0);
+    land(1, rb);
+    __syncthreads();
+    fetch(min(step + 3, last), rb);
+    unmasked(step + 1, 1);
     land(0, ra);
     __syncthreads();
   }
