@@ -671,7 +671,22 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_kernel(
   land(0, ra);
   fetch(min(1, last), rb);
   __syncthreads();
+  // Tiles [0, kt_u) lie below the diagonal of the item's first task and
+  // before S, so every active wave takes the unmasked code there, in a loop
+  // of its own (kt_u even keeps the two-step pipeline aligned).
+  const int q0_first = 32 * ((NW * item) / G);
+  const int kt_u = (CAUSAL ? min((q0_first + 1) / BN, S / BN) : S / BN) & ~1;
   int kt = 0;
+  for (; kt < last && kt + 1 < kt_u; kt += 2) {
+    fetch(min(kt + 2, last), ra);
+    if (active) tile(std::false_type{}, BN * kt, 0);
+    land(1, rb);
+    __syncthreads();
+    fetch(min(kt + 3, last), rb);
+    if (active) tile(std::false_type{}, BN * (kt + 1), 1);
+    land(0, ra);
+    __syncthreads();
+  }
   for (; kt < last; kt += 2) {
     fetch(min(kt + 2, last), ra);
     compute(kt, 0);
