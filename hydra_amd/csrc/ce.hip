@@ -44,7 +44,8 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(
   float m = -INFINITY, s = 0.f;
   for (int e = tid * E; e < V; e += 256 * E) {
     float v[E];
-    if constexpr (VEC) load16<T>(x + e, v);
+    // Streamed once when no gradient pass follows: non-temporal loads.
+    if constexpr (VEC) load16<T, !GRAD>(x + e, v);
     else v[0] = to_f32(x[e]);
     float cm = v[0] * kLog2e;
 #pragma unroll
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(256) void ce_rows_reg_kernel(
   for (int c = 0; c < NCH; ++c) {
     const int e = (c * 256 + tid) * E;
     if (e < V) {
-      load16<T>(x + e, v[c]);
+      load16<T, true>(x + e, v[c]);  // read once: non-temporal
     } else {
 #pragma unroll
       for (int i = 0; i < E; ++i) v[c][i] = -INFINITY;
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256) void ce_rows_reg_kernel(
         const float p = __builtin_amdgcn_exp2f(fmaf(v[c][i], kLog2e, -lse2));
         o[i] = (p - (e + i == t ? 1.f : 0.f)) * sc;
       }
-      store16<T>(g + e, o);
+      store16<T, true>(g + e, o);
     }
   }
 }
