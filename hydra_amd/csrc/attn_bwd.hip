@@ -10,7 +10,7 @@
 // fp32 accumulation, one rounding per output, no atomics: every launch is
 // deterministic.
 //
-// Three launches on the bf16 path (v_mfma_f32_32x32x16_bf16):
+// Launches on the bf16 path (v_mfma_f32_32x32x16_bf16):
 //  * attn_bwd_rowdot_kernel: D and lse * log2(e) per query row (fp32).
 //  * attn_bwd_dkdv_kernel: lanes own keys.  A workgroup is KB key blocks of
 //    32 keys x HG head groups (one wave each); a step stages 32 query rows
@@ -19,7 +19,9 @@
 //    dK^T += Q^T dS), so the KB waves of a head group share each staged
 //    tile.  K and V fragments stay in registers for the whole walk; at the
 //    end the head groups' partial dK/dV are summed through LDS in a fixed
-//    order.  Workgroups start with the lowest keys (the longest causal walks).
+//    order.  Workgroups start with the lowest keys (the longest causal
+//    walks); with few key groups each one's query range is cut into
+//    chunks whose fp32 partials attn_bwd_dkdv_reduce_kernel sums in order.
 //  * attn_bwd_dq_kernel: lanes own queries, as in the forward: S^T = K Q^T,
 //    dP^T = V dO^T, dQ^T += K^T dS^T; a step stages 64 keys of K and V
 //    (row-major) and K^T in LDS, shared by the 4 query tasks of an item.
