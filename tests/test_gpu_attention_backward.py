@@ -136,3 +136,33 @@ def test_attention_backward_query_chunks(cuda, monkeypatch, shape, causal):
     for a, b in zip(first, second):
         assert torch.equal(a, b)
     _check(first, q, k, v, go, causal, TOL[torch.bfloat16])
+
+
+def test_attention_backward_in_hip_graph(cuda):
+    """After one eager call (which sizes the library workspace), the backward
+    captures into a HIP graph; three replays, with eager work and
+    synchronisations between them, each equal the eager gradients bit for
+    bit (no memset nodes: every output element is written by a kernel)."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+
+    q, k, v, go = (t.to(cuda) for t in _inputs(2, 4, 1, 1024, 64, torch.bfloat16, seed=9))
+    out, lse = attention_forward(q, k, v, causal=True, want_lse=True)
+    want = attention_backward(q, k, v, out, lse, go, causal=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        attention_backward(q, k, v, out, lse, go, causal=True)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = attention_backward(q, k, v, out, lse, go, causal=True)
+    for _ in range(3):
+        for t in got:
+            t.zero_()
+        attention_backward(q, k, v, out, lse, go * 2, causal=True)  # eager work in between
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
