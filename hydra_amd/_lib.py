@@ -24,7 +24,8 @@ CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_VALUE_SHIFT, CCGQA_QK_NORM, CCGQA_ROPE = 1, 2,
 CCGQA_V_TRANSPOSED = 32
 CCGQA_W_TILED = 64
 MASK_NONE, MASK_KEY_PADDING, MASK_REFERENCE_SDPA = 0, 1, 2
-SCATTER_ADD, SCATTER_REPLACE = 0, 1
+SCATTER_ADD, SCATTER_REPLACE, SCATTER_ADD_SEQ = 0, 1, 2
+NORM_NONE, NORM_RMS, NORM_ADA = 0, 1, 2
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -40,7 +41,7 @@ SIGNATURES = {
     "hydra_rope_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _I64, _I, _I, _P],
     "hydra_swiglu_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_qk_norm_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _P],
-    "hydra_rms_norm_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
+    "hydra_rms_norm_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
     "hydra_rope_bwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _I64, _I, _I, _P],
     "hydra_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_qk_norm_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _P],
@@ -52,6 +53,11 @@ SIGNATURES = {
                        _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
     "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],
     "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
+    "hydra_embedding_fwd": [_P, _I64, _P, _I64, _I64, _I64, _F, _P, _I64, _I, _P],
+    "hydra_residual_norm_fwd": [_P, _I64, _P, _I64, _F, _P, _P, _P, _F, _I, _P, _I64, _P, _I64,
+                                _I64, _I64, _I, _I, _P],
+    "hydra_mor_update": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I, _P],
+    "hydra_mor_route": [_P, _I64, _P, _P, _P, _I64, _I64, _I, _P],
     "hydra_mod_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P],
     "hydra_mod_gather": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_mod_scatter": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],

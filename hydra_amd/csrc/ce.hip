@@ -50,6 +50,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(
     float cm = v[0] * kLog2e;
 #pragma unroll
     for (int i = 1; i < E; ++i) cm = fmaxf(cm, v[i] * kLog2e);
+    if (cm == -INFINITY) continue;  // all -inf: adds nothing (and exp2(-inf + inf) is NaN)
     float cs = 0.f;
 #pragma unroll
     for (int i = 0; i < E; ++i) cs += __builtin_amdgcn_exp2f(fmaf(v[i], kLog2e, -cm));

@@ -423,9 +423,9 @@ static int launch_qk_norm(const void* q, const void* k, void* qo, void* ko,
 // (deterministic) and clamps.  The block walks rows
 // [blockIdx.x * RPB + i * gridDim.x * RPB, ..), RI row groups per wave per
 // step with all their loads issued first.
-template <typename T, int LPR, int CPL, int RI>
+template <typename T, typename WT, int LPR, int CPL, int RI>
 __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ gy,
+    const T* __restrict__ x, const WT* __restrict__ w, const T* __restrict__ gy,
     T* __restrict__ gx, float* __restrict__ part, int64_t rows, int nvec, int dim,
     int64_t x_rs, int64_t gy_rs, int64_t gx_rs, float eps) {
   constexpr int E = Vec<T>::N;
@@ -442,7 +442,9 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) accw[v][e] = 0.f;
     if (vi < nvec) {
-      load16<T>(w + vi * E, wf[v]);
+#pragma unroll
+      for (int q = 0; q < E * int(sizeof(WT)) / 16; ++q)
+        load16<WT>(w + vi * E + q * (16 / int(sizeof(WT))), wf[v] + q * (16 / int(sizeof(WT))));
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) wf[v][e] = 0.f;
@@ -525,9 +527,9 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
 // unrolled so several are in flight), then the 16 waves' sums in order;
 // clamped.  Deterministic.
 constexpr int kRmsBwdWaves = 16;
-template <typename T>
+template <typename GT>
 __global__ __launch_bounds__(64 * kRmsBwdWaves) void rms_norm_bwd_w_kernel(const float* __restrict__ part,
-                                                                          T* __restrict__ gw, int n, int dim) {
+                                                                          GT* __restrict__ gw, int n, int dim) {
   __shared__ float red[kRmsBwdWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
@@ -552,14 +554,14 @@ __global__ __launch_bounds__(64 * kRmsBwdWaves) void rms_norm_bwd_w_kernel(const
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < kRmsBwdWaves; ++w) t += red[w][lane];
-    gw[col] = from_f32<T>(fminf(fmaxf(t, -100.f), 100.f));
+    gw[col] = from_f32<GT>(fminf(fmaxf(t, -100.f), 100.f));
   }
 }
 
 // Rows of any width / alignment: one wave per row, scalar columns.
-template <typename T>
+template <typename T, typename WT>
 __global__ __launch_bounds__(kBlock) void rms_norm_bwd_scalar_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ gy,
+    const T* __restrict__ x, const WT* __restrict__ w, const T* __restrict__ gy,
     T* __restrict__ gx, float* __restrict__ part, int64_t rows, int dim, int64_t x_rs,
     int64_t gy_rs, int64_t gx_rs, float eps) {
   // part [gridDim.x * 4][dim]: one partial row per wave (wave-private, so
@@ -591,42 +593,43 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_scalar_kernel(
 }
 
 // The weight gradient from the n partial rows.
-template <typename T>
-static int rms_bwd_reduce_w(const float* part, T* gw, int n, int dim, hipStream_t st) {
+template <typename GT>
+static int rms_bwd_reduce_w(const float* part, GT* gw, int n, int dim, hipStream_t st) {
   const int rc0 = check_launch("rms_norm_bwd_kernel");
   if (rc0 != HYDRA_OK) return rc0;
-  rms_norm_bwd_w_kernel<T><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(part, gw, n, dim);
+  rms_norm_bwd_w_kernel<GT><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(part, gw, n, dim);
   return check_launch("rms_norm_bwd_w_kernel");
 }
 
-template <typename T, int LPR, int CPL>
-static int launch_rms_bwd_vec(const T* X, const T* W, const T* GY, T* GX, T* GW, int64_t rows, int nvec,
-                              int dim, int64_t x_rs, int64_t gy_rs, int64_t gx_rs, float eps,
-                              hipStream_t st) {
+// Partial rows of the weight gradient (fp32 [n][dim]) the two backward
+// paths write: at most kRmsBwdParts rows for any shape.
+constexpr int kRmsBwdParts = 512;
+
+template <typename T, typename WT, int LPR, int CPL>
+static int launch_rms_bwd_vec(const T* X, const WT* W, const T* GY, T* GX, WT* GW, float* part,
+                              int64_t rows, int nvec, int dim, int64_t x_rs, int64_t gy_rs,
+                              int64_t gx_rs, float eps, hipStream_t st) {
   constexpr int RI = CPL >= 4 ? 1 : (CPL >= 2 ? 2 : 4);  // row groups per wave per step
   constexpr int RPB = (kBlock / 64) * (64 / LPR) * RI;
   // A fixed number of blocks (from the shape only), so the summation order
   // of the weight gradient does not depend on the device.
-  const int nblk = static_cast<int>(std::min<int64_t>((rows + RPB - 1) / RPB, 512));
-  void* ws = nullptr;
-  const int rc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(nblk) * dim * sizeof(float), st, &ws);
-  if (rc != HYDRA_OK) return rc;
-  auto part = static_cast<float*>(ws);
-  rms_norm_bwd_kernel<T, LPR, CPL, RI><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, nvec, dim, x_rs,
-                                                                 gy_rs, gx_rs, eps);
+  const int nblk = static_cast<int>(std::min<int64_t>((rows + RPB - 1) / RPB, kRmsBwdParts));
+  rms_norm_bwd_kernel<T, WT, LPR, CPL, RI><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, nvec, dim,
+                                                                     x_rs, gy_rs, gx_rs, eps);
   return rms_bwd_reduce_w(part, GW, nblk, dim, st);
 }
 
-template <typename T>
+// part: fp32 scratch of at least kRmsBwdParts * dim elements.
+template <typename T, typename WT>
 static int launch_rms_norm_bwd(const void* x, const void* w, const void* gy, void* gx, void* gw,
-                               int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs, int64_t gx_rs,
-                               float eps, hipStream_t st) {
+                               float* part, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
+                               int64_t gx_rs, float eps, hipStream_t st) {
   constexpr int E = Vec<T>::N;
   auto X = static_cast<const T*>(x);
-  auto W = static_cast<const T*>(w);
+  auto W = static_cast<const WT*>(w);
   auto GY = static_cast<const T*>(gy);
   auto GX = static_cast<T*>(gx);
-  auto GW = static_cast<T*>(gw);
+  auto GW = static_cast<WT*>(gw);
   const bool vec_ok = dim % E == 0 && x_rs % E == 0 && gy_rs % E == 0 && gx_rs % E == 0 && aligned16(x) &&
                       aligned16(w) && aligned16(gy) && aligned16(gx);
   const int nvec = static_cast<int>(dim / E);
@@ -641,7 +644,8 @@ static int launch_rms_norm_bwd(const void* x, const void* w, const void* gy, voi
     const int cpl = (nvec + lpr - 1) / lpr;
 #define HYDRA_RMSB_CASE(LP, CP)                                                                           \
   if (lpr == LP && cpl <= CP)                                                                             \
-    return launch_rms_bwd_vec<T, LP, CP>(X, W, GY, GX, GW, rows, nvec, (int)dim, x_rs, gy_rs, gx_rs, eps, st);
+    return launch_rms_bwd_vec<T, WT, LP, CP>(X, W, GY, GX, GW, part, rows, nvec, (int)dim, x_rs, gy_rs, gx_rs, \
+                                             eps, st);
     HYDRA_RMSB_CASE(4, 1) HYDRA_RMSB_CASE(4, 2) HYDRA_RMSB_CASE(4, 4)
     HYDRA_RMSB_CASE(8, 1) HYDRA_RMSB_CASE(8, 2) HYDRA_RMSB_CASE(8, 4)
     HYDRA_RMSB_CASE(16, 1) HYDRA_RMSB_CASE(16, 2) HYDRA_RMSB_CASE(16, 4)
@@ -649,13 +653,9 @@ static int launch_rms_norm_bwd(const void* x, const void* w, const void* gy, voi
     HYDRA_RMSB_CASE(64, 1) HYDRA_RMSB_CASE(64, 2) HYDRA_RMSB_CASE(64, 3) HYDRA_RMSB_CASE(64, 4)
 #undef HYDRA_RMSB_CASE
   }
-  const int nblk = static_cast<int>(std::min<int64_t>((rows + 3) / 4, 128));
-  void* ws = nullptr;
-  const int rc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(nblk) * 4 * dim * sizeof(float), st, &ws);
-  if (rc != HYDRA_OK) return rc;
-  auto part = static_cast<float*>(ws);
-  rms_norm_bwd_scalar_kernel<T><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, (int)dim, x_rs, gy_rs,
-                                                              gx_rs, eps);
+  const int nblk = static_cast<int>(std::min<int64_t>((rows + 3) / 4, kRmsBwdParts / 4));
+  rms_norm_bwd_scalar_kernel<T, WT><<<dim3(nblk), kBlock, 0, st>>>(X, W, GY, GX, part, rows, (int)dim, x_rs,
+                                                                  gy_rs, gx_rs, eps);
   return rms_bwd_reduce_w(part, GW, nblk * 4, (int)dim, st);
 }
 
@@ -915,28 +915,59 @@ extern "C" int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out,
   });
 }
 
-extern "C" int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
-                                  void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
-                                  int64_t gx_rs, float eps, int dtype, void* stream) {
-  HYDRA_REQUIRE(rows >= 0 && dim >= 1, "rms_norm_bwd: rows must be >= 0 and dim >= 1");
-  HYDRA_REQUIRE(dim <= (int64_t(1) << 24), "rms_norm_bwd: dim too large");
-  HYDRA_REQUIRE(x_rs >= dim && gy_rs >= dim && gx_rs >= dim, "rms_norm_bwd: row stride smaller than dim");
-  HYDRA_REQUIRE(x && w && grad_y && grad_x && grad_w, "rms_norm_bwd: null pointer");
-  auto st = static_cast<hipStream_t>(stream);
+// The shared body of the RMSNorm backward entry points: argument checks, the
+// zero-row case, and the dtype dispatch with the weight-gradient partials
+// in `part` (kRmsBwdParts * dim fp32).
+static int rms_norm_bwd_body(const void* x, const void* w, const void* grad_y, void* grad_x,
+                             void* grad_w, float* part, int64_t rows, int64_t dim, int64_t x_rs,
+                             int64_t gy_rs, int64_t gx_rs, float eps, int dtype, int w_dtype,
+                             hipStream_t st) {
   if (rows == 0) {
-    const int64_t bytes = dim * dtype_size(dtype);
-    HYDRA_REQUIRE(bytes > 0, "rms_norm_bwd: unknown dtype code");
     // no rows: the weight gradient is zero (a fill kernel, not a memset, so
     // the call can sit in a captured graph)
-    return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
-      rms_norm_bwd_w_kernel<T><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(
-          nullptr, static_cast<T*>(grad_w), 0, static_cast<int>(dim));
+    return HYDRA_DISPATCH_DTYPE(w_dtype, GT, [&] {
+      rms_norm_bwd_w_kernel<GT><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(
+          nullptr, static_cast<GT*>(grad_w), 0, static_cast<int>(dim));
       return check_launch("rms_norm_bwd_w_kernel");
     });
   }
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
-    return launch_rms_norm_bwd<T>(x, w, grad_y, grad_x, grad_w, rows, dim, x_rs, gy_rs, gx_rs, eps, st);
+    if (w_dtype == HYDRA_F32 && !std::is_same<T, float>::value)
+      return launch_rms_norm_bwd<T, float>(x, w, grad_y, grad_x, grad_w, part, rows, dim, x_rs, gy_rs,
+                                           gx_rs, eps, st);
+    return launch_rms_norm_bwd<T, T>(x, w, grad_y, grad_x, grad_w, part, rows, dim, x_rs, gy_rs, gx_rs,
+                                     eps, st);
   });
+}
+
+static int rms_norm_bwd_check(const void* x, const void* w, const void* grad_y, void* grad_x,
+                              void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
+                              int64_t gx_rs, int dtype, int w_dtype) {
+  HYDRA_REQUIRE(rows >= 0 && dim >= 1, "rms_norm_bwd: rows must be >= 0 and dim >= 1");
+  HYDRA_REQUIRE(dim <= (int64_t(1) << 24), "rms_norm_bwd: dim too large");
+  HYDRA_REQUIRE(x_rs >= dim && gy_rs >= dim && gx_rs >= dim, "rms_norm_bwd: row stride smaller than dim");
+  HYDRA_REQUIRE(x && w && grad_y && grad_x && grad_w, "rms_norm_bwd: null pointer");
+  HYDRA_REQUIRE(dtype_size(dtype) > 0, "rms_norm_bwd: unknown dtype code");
+  HYDRA_REQUIRE(w_dtype == dtype || w_dtype == HYDRA_F32,
+                "rms_norm_bwd: the weight must be of x's dtype or fp32");
+  return HYDRA_OK;
+}
+
+extern "C" int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
+                                  void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
+                                  int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream) {
+  const int rc = rms_norm_bwd_check(x, w, grad_y, grad_x, grad_w, rows, dim, x_rs, gy_rs, gx_rs, dtype,
+                                    w_dtype);
+  if (rc != HYDRA_OK) return rc;
+  auto st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (rows > 0) {
+    const int wrc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(kRmsBwdParts) * dim * sizeof(float),
+                                     st, &ws);
+    if (wrc != HYDRA_OK) return wrc;
+  }
+  return rms_norm_bwd_body(x, w, grad_y, grad_x, grad_w, static_cast<float*>(ws), rows, dim, x_rs, gy_rs,
+                           gx_rs, eps, dtype, w_dtype, st);
 }
 
 extern "C" int hydra_rope_bwd(const void* grad_y, const void* cos, const void* sin, void* grad_x,

@@ -253,7 +253,12 @@ __global__ __launch_bounds__(256) void mod_scatter_kernel(
     const int64_t dst = idx[r];
     if (dst < 0 || dst >= L) continue;
     op[j] = out + b * o_bs + dst * o_ls + c * E;
-    load16<T, true>(y + static_cast<int64_t>(r) * cpr * E + c * E, yf[j]);
+    if (y) {
+      load16<T, true>(y + static_cast<int64_t>(r) * cpr * E + c * E, yf[j]);
+    } else {  // REPLACE without values: clear the rows
+#pragma unroll
+      for (int e = 0; e < E; ++e) yf[j][e] = 0.f;
+    }
     if (MODE == HYDRA_SCATTER_ADD) {
       wt[j] = w ? w[r] : 1.f;
       load16<T, true>(op[j], of[j]);
@@ -284,11 +289,34 @@ __global__ __launch_bounds__(256) void mod_scatter_scalar_kernel(
   const int64_t dst = idx[r];
   if (dst < 0 || dst >= L) return;
   T* op = out + b * o_bs + dst * o_ls + c;
-  const float yv = to_f32(y[t]);
+  const float yv = y ? to_f32(y[t]) : 0.f;
   if (MODE == HYDRA_SCATTER_ADD) {
     *op = from_f32<T>(w ? fmaf(w[r], yv, to_f32(*op)) : to_f32(*op) + yv);
   } else {
     *op = from_f32<T>(yv);
+  }
+}
+
+// Scatter-add that allows repeated indices (torch.scatter_add_ semantics on
+// the CPU): thread = (batch row, column); it walks j = 0..k-1 in order and
+// updates out[b, idx[b,j], c] += y[b,j,c], rounding after every add, so
+// repeats accumulate in index order, deterministically.  Not a hot path (the
+// routing wrappers use the distinct-index kernel above).
+template <typename T>
+__global__ __launch_bounds__(256) void mod_scatter_seq_kernel(
+    T* __restrict__ out, const T* __restrict__ y, const int64_t* __restrict__ idx,
+    int64_t B, int64_t D, int64_t k, int64_t L, int64_t o_bs, int64_t o_ls) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= B * D) return;
+  const int64_t b = t / D, c = t - b * D;
+  const int64_t* ir = idx + b * k;
+  const T* yr = y + b * k * D + c;
+  T* ob = out + b * o_bs + c;
+  for (int64_t j = 0; j < k; ++j) {
+    const int64_t dst = ir[j];
+    if (dst < 0 || dst >= L) continue;
+    T* op = ob + dst * o_ls;
+    *op = from_f32<T>(to_f32(*op) + to_f32(yr[j * D]));
   }
 }
 
@@ -405,8 +433,14 @@ static int launch_scatter(void* out, const void* y, const int64_t* idx, const fl
   const int64_t total_vec = B * k * cpr;
   auto O = static_cast<T*>(out);
   auto Y = static_cast<const T*>(y);
+  if (mode == HYDRA_SCATTER_ADD_SEQ) {
+    const dim3 grid(static_cast<unsigned>((B * D + 255) / 256));
+    mod_scatter_seq_kernel<T><<<grid, 256, 0, st>>>(O, Y, idx, B, D, k, L, o_bs, o_ls);
+    return check_launch("mod_scatter_seq_kernel");
+  }
   const bool vec_ok = D % E == 0 && o_bs % E == 0 && o_ls % E == 0 && aligned16(out) &&
-                      aligned16(y) && total_vec < (int64_t(1) << 31) && B * k < (int64_t(1) << 31);
+                      (y == nullptr || aligned16(y)) && total_vec < (int64_t(1) << 31) &&
+                      B * k < (int64_t(1) << 31);
   if (vec_ok) {
     constexpr int U = 1;
     const dim3 grid(static_cast<unsigned>((total_vec + 256 * U - 1) / (256 * U)));
@@ -434,12 +468,17 @@ extern "C" int hydra_mod_scatter(void* out, const void* y, const int64_t* idx,
                                  int64_t D, int64_t o_bs, int64_t o_ls, int mode,
                                  int dtype, void* stream) {
   HYDRA_REQUIRE(B >= 0 && L >= 0 && k >= 0 && D >= 0, "mod_scatter: negative size");
-  HYDRA_REQUIRE(mode == HYDRA_SCATTER_ADD || mode == HYDRA_SCATTER_REPLACE,
+  HYDRA_REQUIRE(mode == HYDRA_SCATTER_ADD || mode == HYDRA_SCATTER_REPLACE ||
+                    mode == HYDRA_SCATTER_ADD_SEQ,
                 "mod_scatter: unknown mode");
   HYDRA_REQUIRE(w == nullptr || mode == HYDRA_SCATTER_ADD,
                 "mod_scatter: weights apply to the ADD mode only");
   if (B * k * D == 0) return HYDRA_OK;
-  HYDRA_REQUIRE(out && y && idx, "mod_scatter: null pointer");
+  HYDRA_REQUIRE(out && idx, "mod_scatter: null pointer");
+  HYDRA_REQUIRE(y != nullptr || mode == HYDRA_SCATTER_REPLACE,
+                "mod_scatter: values may be NULL in the REPLACE mode only");
+  HYDRA_REQUIRE(mode != HYDRA_SCATTER_ADD_SEQ || B * D < (int64_t(1) << 40),
+                "mod_scatter: too large");
   HYDRA_REQUIRE(o_ls >= D, "mod_scatter: row stride smaller than D");
   HYDRA_REQUIRE((B * k * D + 255) / 256 < (int64_t(1) << 31), "mod_scatter: too large");
   auto st = static_cast<hipStream_t>(stream);

@@ -288,21 +288,35 @@ def fused_swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # 4. RMSNorm (fused_ops.py:1114-1172)
 # ---------------------------------------------------------------------------
+def _norm_weight(weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """The weight as the kernels take it: x's dtype, or fp32 (an fp32 master
+    weight is read in fp32, as the reference's kernel loads it,
+    fused_ops.py:994); other dtypes are converted to x's."""
+    w = weight if weight.dtype in (x.dtype, torch.float32) else weight.to(x.dtype)
+    return w.contiguous()
+
+
 class _RMSNormFunction(torch.autograd.Function):
     """FusedRMSNormFunction (fused_ops.py:1135-1172): forward
-    hydra_rms_norm_fwd, backward hydra_rms_norm_bwd.  A weight of another
-    dtype than x is used (and its gradient first rounded) in x's dtype."""
+    hydra_rms_norm_fwd (hydra_residual_norm_fwd for an fp32 weight with a
+    16-bit x), backward hydra_rms_norm_bwd.  An fp32 weight is used in fp32
+    and its gradient written in fp32 (the reference's fp32 sum,
+    :1244-1246)."""
 
     @staticmethod
     def forward(ctx, x, weight, eps):
         dim = x.shape[-1]
-        w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
-        w = w.contiguous()
+        w = _norm_weight(weight, x)
         x, xv = _as_rows(x)
         out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
         with torch.cuda.device(x.device):
-            _lib.call("hydra_rms_norm_fwd", x.data_ptr(), w.data_ptr(), out.data_ptr(),
-                      xv[0], dim, xv[1], dim, float(eps), _lib.dtype_code(x), _lib.stream(x))
+            if w.dtype == x.dtype:
+                _lib.call("hydra_rms_norm_fwd", x.data_ptr(), w.data_ptr(), out.data_ptr(),
+                          xv[0], dim, xv[1], dim, float(eps), _lib.dtype_code(x), _lib.stream(x))
+            else:
+                _lib.call("hydra_residual_norm_fwd", x.data_ptr(), xv[1], None, 0, 1.0, None, None,
+                          w.data_ptr(), float(eps), _lib.NORM_RMS, None, 0, out.data_ptr(), dim,
+                          xv[0], dim, _lib.dtype_code(x), _lib.dtype_code(w), _lib.stream(x))
         ctx.save_for_backward(x, w)
         ctx.eps = float(eps)
         ctx.w_dtype = weight.dtype
@@ -316,11 +330,11 @@ class _RMSNormFunction(torch.autograd.Function):
         _, xv = _as_rows(x)
         go, ov = _as_rows(grad_out.to(x.dtype))
         gx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-        gw = torch.empty((dim,), dtype=x.dtype, device=x.device)
+        gw = torch.empty((dim,), dtype=w.dtype, device=x.device)
         with torch.cuda.device(x.device):
             _lib.call("hydra_rms_norm_bwd", x.data_ptr(), w.data_ptr(), go.data_ptr(), gx.data_ptr(),
                       gw.data_ptr(), xv[0], dim, xv[1], ov[1], dim, ctx.eps, _lib.dtype_code(x),
-                      _lib.stream(x))
+                      _lib.dtype_code(w), _lib.stream(x))
         return gx, gw.to(ctx.w_dtype), None
 
 
@@ -363,16 +377,22 @@ class ChunkedCrossEntropyFunction(torch.autograd.Function):
     over tokens whose target is not ignore_index, computed chunk by chunk
     (logits of at most chunk_size tokens exist at a time); the backward
     recomputes each chunk's logits in fp32.  Out-of-range targets are
-    clamped into [0, vocab) as the reference does (:1407-1422, without its
-    warning, which needs a host synchronisation).  No valid token: loss 0
-    and zero gradients."""
+    handled as the reference does (:1407-1422): when any non-ignored target
+    lies outside [0, vocab), the whole target vector -- ignore_index entries
+    included -- is clamped into [0, vocab), and validity is taken from the
+    clamped vector (so clamped ignore entries count).  The decision is made
+    on the device (torch.where), without the reference's warning and its
+    host synchronisation.  No valid token: loss 0 and zero gradients."""
 
     @staticmethod
     def forward(ctx, hidden_states, weight, targets, ignore_index, chunk_size):
         _lib.require_gpu("chunked_cross_entropy", hidden_states, weight, targets)
         dim = hidden_states.shape[-1]
         h = hidden_states.reshape(-1, dim)
-        t = targets.reshape(-1).to(torch.int64).contiguous()
+        t = targets.reshape(-1).to(torch.int64)
+        V = weight.shape[0]
+        oob = ((t != ignore_index) & ((t < 0) | (t >= V))).any()
+        t = torch.where(oob, t.clamp(0, V - 1), t).contiguous()
         total = torch.zeros((), dtype=torch.float32, device=h.device)
         for s in range(0, h.shape[0], chunk_size):
             logits = F.linear(h[s:s + chunk_size], weight).contiguous()

@@ -1,5 +1,10 @@
 """Mixture-of-Depths routing ops on gfx950 (hydra/routing/ops.py:257-314,
-mixture_of_depths.py:179-191, model/framework/blocks.py:243-269)."""
+mixture_of_depths.py:179-191, model/framework/blocks.py:243-300).
+
+The row gather and the scatters are autograd Functions whose backward runs
+the same HIP kernels (a gather's gradient is a scatter of the incoming
+gradient rows, a scatter's is a gather), so the MoD wrappers train through
+them as the reference trains through torch.gather / scatter_."""
 from __future__ import annotations
 
 from typing import Optional, Tuple
@@ -7,7 +12,6 @@ from typing import Optional, Tuple
 import torch
 
 from .. import _lib
-from .._autograd import track
 
 
 def compute_capacity_k(seq_len: int, capacity_ratio: float) -> int:
@@ -56,65 +60,158 @@ def _bl_strides(x: torch.Tensor):
     return x.stride(0), x.stride(1)
 
 
-def gather_by_indices(x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-    """ops.py:257-272: out[b, j] = x[b, indices[b, j]] -> [B, k, D].
-    Indices outside [0, L) produce zero rows."""
-    _lib.require_gpu("gather_by_indices", x, indices)
+def _gather(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     B, L, D = x.shape
-    k = indices.shape[1]
-    if indices.shape[0] != B:
-        raise ValueError("gather_by_indices: batch mismatch")
+    k = idx.shape[1]
     st = _bl_strides(x)
     if st is None:
         x = x.contiguous()
         st = _bl_strides(x)
-    idx = indices.to(torch.int64).contiguous()
     out = torch.empty((B, k, D), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
         _lib.call("hydra_mod_gather", x.data_ptr(), idx.data_ptr(), out.data_ptr(), B, L, k, D,
                   st[0], st[1], _lib.dtype_code(x), _lib.stream(x))
-    return track(out, x)
+    return out
 
 
-def _scatter(output, values, indices, weights, mode):
-    _lib.require_gpu("scatter", output, values, indices, weights)
+def _scatter_raw(output: torch.Tensor, values: Optional[torch.Tensor], idx: torch.Tensor,
+                 weights: Optional[torch.Tensor], mode: int) -> torch.Tensor:
     B, L, D = output.shape
-    k = indices.shape[1]
-    if values.shape != (B, k, D):
-        raise ValueError(f"scatter: values shape {tuple(values.shape)} != {(B, k, D)}")
-    if values.dtype != output.dtype:
-        values = values.to(output.dtype)
+    k = idx.shape[1]
     st = _bl_strides(output)
     if st is None:
         raise ValueError("scatter: output must have unit stride on the last dim (it is written in place)")
-    vals = values.contiguous()
-    idx = indices.to(torch.int64).contiguous()
+    vals = None
+    if values is not None:
+        vals = values.to(output.dtype) if values.dtype != output.dtype else values
+        vals = vals.contiguous()
     w = None if weights is None else weights.to(torch.float32).contiguous()
     with torch.cuda.device(output.device):
-        _lib.call("hydra_mod_scatter", output.data_ptr(), vals.data_ptr(), idx.data_ptr(),
+        _lib.call("hydra_mod_scatter", output.data_ptr(), _lib.ptr(vals), idx.data_ptr(),
                   _lib.ptr(w), B, L, k, D, st[0], st[1], mode, _lib.dtype_code(output),
                   _lib.stream(output))
     return output
 
 
+def _index(indices: torch.Tensor, B: int, name: str) -> torch.Tensor:
+    if indices.dim() != 2 or indices.shape[0] != B:
+        raise ValueError(f"{name}: indices must be [B, k] with B = {B}")
+    return indices.to(torch.int64).contiguous()
+
+
+class _GatherRows(torch.autograd.Function):
+    """xs = x[b, idx[b, j]]; grad_x = scatter-add of grad_xs into zeros
+    (the gradient torch.gather gives)."""
+
+    @staticmethod
+    def forward(ctx, x, idx, distinct):
+        ctx.save_for_backward(idx)
+        ctx.shape, ctx.distinct = x.shape, distinct
+        return _gather(x, idx)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (idx,) = ctx.saved_tensors
+        gx = torch.zeros(ctx.shape, dtype=grad.dtype, device=grad.device)
+        mode = _lib.SCATTER_ADD if ctx.distinct else _lib.SCATTER_ADD_SEQ
+        _scatter_raw(gx, grad.contiguous(), idx, None, mode)
+        return gx, None, None
+
+
+class _ScatterRows(torch.autograd.Function):
+    """In-place row scatter into `output` (marked dirty):
+    ADD: output[b, idx] += w * values -> grad_output = g, grad_values = w * g[idx],
+         grad_w = <g[idx], values>;
+    REPLACE: output[b, idx] = values -> grad_output = g with rows idx cleared,
+         grad_values = g[idx];
+    ADD_SEQ: output[b, idx] += values, repeats accumulate -> grad_output = g,
+         grad_values = g[idx]."""
+
+    @staticmethod
+    def forward(ctx, output, values, idx, weights, mode):
+        _scatter_raw(output, values, idx, weights, mode)
+        ctx.mark_dirty(output)
+        ctx.mode = mode
+        ctx.save_for_backward(values, idx, weights)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad):
+        values, idx, weights = ctx.saved_tensors
+        grad = grad.contiguous()
+        g_sel = None
+        if ctx.needs_input_grad[1] or (weights is not None and ctx.needs_input_grad[3]):
+            g_sel = _gather(grad, idx)
+        g_vals = g_w = None
+        if ctx.needs_input_grad[1]:
+            g_vals = g_sel if weights is None else g_sel * weights.to(g_sel.dtype)[..., None]
+            g_vals = g_vals.to(values.dtype)
+        if weights is not None and ctx.needs_input_grad[3]:
+            g_w = (g_sel.float() * values.float()).sum(-1).to(weights.dtype)
+        g_out = None
+        if ctx.needs_input_grad[0]:
+            if ctx.mode == _lib.SCATTER_REPLACE:
+                g_out = _scatter_raw(grad.clone(), None, idx, None, _lib.SCATTER_REPLACE)
+            else:
+                g_out = grad
+        return g_out, g_vals, None, g_w, None
+
+
+def _scatter(output, values, indices, weights, mode):
+    _lib.require_gpu("scatter", output, values, indices, weights)
+    B, L, D = output.shape
+    idx = _index(indices, B, "scatter")
+    k = idx.shape[1]
+    if values.shape != (B, k, D):
+        raise ValueError(f"scatter: values shape {tuple(values.shape)} != {(B, k, D)}")
+    if weights is not None and weights.shape != (B, k):
+        raise ValueError(f"scatter: weights shape {tuple(weights.shape)} != {(B, k)}")
+    if _bl_strides(output) is None:
+        raise ValueError("scatter: output must have unit stride on the last dim (it is written in place)")
+    if torch.is_grad_enabled() and (output.requires_grad or values.requires_grad
+                                    or (weights is not None and weights.requires_grad)):
+        return _ScatterRows.apply(output, values, idx, weights, mode)
+    return _scatter_raw(output, values, idx, weights, mode)
+
+
+def gather_by_indices(x: torch.Tensor, indices: torch.Tensor, *,
+                      distinct: bool = False) -> torch.Tensor:
+    """ops.py:257-272: out[b, j] = x[b, indices[b, j]] -> [B, k, D].
+    Differentiable; `distinct=True` (indices known distinct per row, as top-k
+    indices are) lets the backward use the parallel scatter.  Indices outside
+    [0, L) give zero rows (torch.gather raises; checking would need a host
+    synchronisation)."""
+    _lib.require_gpu("gather_by_indices", x, indices)
+    if x.dim() != 3:
+        raise ValueError("gather_by_indices: x must be [B, L, D]")
+    idx = _index(indices, x.shape[0], "gather_by_indices")
+    if torch.is_grad_enabled() and x.requires_grad:
+        return _GatherRows.apply(x, idx, distinct)
+    return _gather(x, idx)
+
+
 def scatter_add_by_indices(output: torch.Tensor, values: torch.Tensor,
                            indices: torch.Tensor) -> torch.Tensor:
-    """ops.py:275-293: output[b, indices[b, j]] += values[b, j], in place.
-    Indices must be distinct within a row (as top-k indices are)."""
-    return _scatter(output, values, indices, None, _lib.SCATTER_ADD)
+    """ops.py:275-293: output[b, indices[b, j]] += values[b, j], in place,
+    with torch.scatter_add_'s semantics: repeated indices accumulate (in
+    index order, rounded after each add)."""
+    return _scatter(output, values, indices, None, _lib.SCATTER_ADD_SEQ)
 
 
 def weighted_residual_scatter(residual: torch.Tensor, values: torch.Tensor,
                               indices: torch.Tensor,
                               weights: Optional[torch.Tensor] = None) -> torch.Tensor:
     """residual[b, idx[b, j]] += w[b, j] * values[b, j] in place (w = 1 when
-    None): the fused form of `h + zeros_like(h).scatter_(idx, y)` of the MoD
-    MLP path (blocks.py:266-268 with the residual add at :603)."""
+    None; idx distinct per row): the fused form of
+    `h + zeros_like(h).scatter_(idx, y)` of the MoD MLP path (blocks.py:266-268
+    with the residual add at :603)."""
     return _scatter(residual, values, indices, weights, _lib.SCATTER_ADD)
 
 
 def scatter_replace(output: torch.Tensor, values: torch.Tensor,
                     indices: torch.Tensor) -> torch.Tensor:
-    """output[b, idx[b, j]] = values[b, j] in place (the clone + scatter_ of
-    MixtureOfDepthsBlock.forward, mixture_of_depths.py:291-295)."""
+    """output[b, idx[b, j]] = values[b, j] in place (idx distinct per row):
+    the clone + scatter_ of MixtureOfDepthsBlock.forward
+    (mixture_of_depths.py:291-295) and the zeros + scatter_ of
+    MoDMLPWrapper._forward_hard (blocks.py:266-268)."""
     return _scatter(output, values, indices, None, _lib.SCATTER_REPLACE)

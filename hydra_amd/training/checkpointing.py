@@ -18,13 +18,28 @@ import torch
 _COMPILE_PREFIX = "_orig_mod."
 
 
-def read_checkpoint(path: Union[str, Path]) -> dict:
-    """The checkpoint dict, loaded on the CPU with weights_only=True.  A file
-    the safe loader refuses (e.g. one whose rng_state pickles objects outside
-    torch's allow-list) raises, naming the file; pass its "model" dict from
-    a trusted loader to `module_state` instead."""
+def _numpy_rng_globals() -> list:
+    """The numpy types a reference checkpoint's rng_state["numpy"]
+    (np.random.get_state(), checkpointing.py:17-33) pickles: ndarray
+    reconstruction, dtype and the uint32 dtype class.  Allow-listing them
+    keeps the load weights-only: these rebuild arrays, they run no code."""
+    import numpy as np
+
     try:
-        return torch.load(str(path), map_location="cpu", weights_only=True)
+        from numpy._core.multiarray import _reconstruct
+    except ImportError:  # numpy < 2
+        from numpy.core.multiarray import _reconstruct
+    return [_reconstruct, np.ndarray, np.dtype, type(np.dtype(np.uint32))]
+
+
+def read_checkpoint(path: Union[str, Path]) -> dict:
+    """The checkpoint dict, loaded on the CPU with weights_only=True and
+    numpy's array types allow-listed (the reference stores numpy's RNG state
+    in every checkpoint).  A file the safe loader still refuses raises,
+    naming the file; pass its "model" dict to `module_state` instead."""
+    try:
+        with torch.serialization.safe_globals(_numpy_rng_globals()):
+            return torch.load(str(path), map_location="cpu", weights_only=True)
     except Exception as e:  # the safe unpickler's refusal, or a bad file
         raise RuntimeError(f"read_checkpoint: {path} cannot be read with weights_only=True ({e})") from e
 

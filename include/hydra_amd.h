@@ -94,13 +94,16 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
  * backward (hydra/kernels/fused_ops.py:1161-1172) with
  * _rms_norm_backward_pytorch (:1251-1281) / _fused_rms_norm_backward_kernel
  * (:1027-1111) + the grad_w reduction (:1244-1246).  x, grad_y, grad_x:
- * [rows, dim] with row strides x_rs, gy_rs, gx_rs; w, grad_w: [dim].  The
- * weight gradient is summed in a fixed order (deterministic); uses a
- * library-owned scratch buffer (grown on first use of a shape, so run a
+ * [rows, dim] with row strides x_rs, gy_rs, gx_rs; w, grad_w: [dim] of
+ * w_dtype (`dtype`, or HYDRA_F32 for an fp32 master weight, read and
+ * written in fp32 as the reference's kernel loads it,
+ * fused_ops.py:1072, and casts its fp32 sum, :1244-1246).  The weight
+ * gradient is summed in a fixed order (deterministic); uses a library-owned
+ * scratch buffer of 2 KiB * dim per stream (grown on first use, so run a
  * shape once before capturing it in a graph). */
 int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
                        void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
-                       int64_t gx_rs, float eps, int dtype, void* stream);
+                       int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream);
 
 /* RoPE backward: grad_x = the rotation of hydra_rope_fwd transposed,
  *   gx[..,2i] = g[..,2i]*cos + g[..,2i+1]*sin, gx[..,2i+1] = -g[..,2i]*sin + g[..,2i+1]*cos.
@@ -270,6 +273,68 @@ int hydra_ce_rows(const void* logits, int64_t rows, int64_t vocab, int64_t logit
                   void* grad, int64_t grad_rs, const float* grad_scale, int dtype,
                   void* stream);
 
+/* ---- block compositions (hydra/model/framework, hydra/layers) --------- */
+
+/* Token embedding: out[r, :] = table[clamp(ids[r], 0, vocab-1), :] * scale,
+ * one rounding into `dtype`.  Replaces _safe_embedding_lookup
+ * (hydra/model/framework/model.py:51-73: ids always clamped, embedding(x) *
+ * sqrt(dim)).  ids: int64 [n]; table: [vocab, dim] (row stride table_rs);
+ * out: [n, dim] (row stride out_rs). */
+int hydra_embedding_fwd(const int64_t* ids, int64_t n, const void* table, int64_t vocab,
+                        int64_t dim, int64_t table_rs, float scale, void* out, int64_t out_rs,
+                        int dtype, void* stream);
+
+#define HYDRA_NORM_NONE 0 /* residual only                                   */
+#define HYDRA_NORM_RMS  1 /* RMSNorm: fp32 math, one rounding                */
+#define HYDRA_NORM_ADA  2 /* AdaRMSNorm: the reference's input-dtype steps   */
+
+/* Residual add fused with the pre-norm of the next sublayer.  Per row, each
+ * step rounded into `dtype` as the reference's tensor ops are:
+ *   v = x + (alpha == 1 ? r : round(alpha * r))   (r optional)
+ *   v = v + b1;  v = v + b2                         ([dim] vectors, optional)
+ *   h_out = v                                       (optional)
+ *   y_out = norm(v):
+ *     RMS: v * rsqrt(mean(v^2) + eps) * w in fp32, one rounding
+ *          (RMSNorm, hydra/layers/common.py:74-118);
+ *     ADA: AdaRMSNorm._rmsnorm (common.py:153-157) in the input dtype:
+ *          m = round(mean(round(v^2))), s = round(rsqrt(round(m + eps))),
+ *          y = round(round(v * s) * w).
+ * Replaces, in HydraBlock.forward (hydra/model/framework/blocks.py:68-70),
+ * `h = x + attention(...)` with norm2(h); in HydraMoRBlock._forward_mor
+ * (blocks.py:614-633) `x + residual_scale * attention(...)`; and in
+ * MoRExecutor.forward (hydra/routing/mixture_of_recursions.py:459-465)
+ * `norm(current + recursion_bias[i] + recursion_embed[i])`.
+ * x, r, h_out, y_out: [rows, dim] with row strides; b1, b2: [dim] of dtype;
+ * w: [dim] of w_dtype (dtype, or HYDRA_F32 for an fp32 weight).
+ * y_out is required exactly when norm != NONE. */
+int hydra_residual_norm_fwd(const void* x, int64_t x_rs, const void* r, int64_t r_rs,
+                            float alpha, const void* b1, const void* b2, const void* w,
+                            float eps, int norm, void* h_out, int64_t h_rs, void* y_out,
+                            int64_t y_rs, int64_t rows, int64_t dim, int dtype, int w_dtype,
+                            void* stream);
+
+/* One recursion's update of MoRExecutor.forward
+ * (hydra/routing/mixture_of_recursions.py:466-476), in place, per token row
+ * with depth d = depth[row]:
+ *   current = current + round(delta * (d >= recursion))
+ *   output  = output + round(current * (d == recursion))
+ * (the straight-through factor (1 + ste_grad) is exactly 1 in the forward).
+ * current, delta, output: [rows, dim] with row strides; depth: int64 [rows]. */
+int hydra_mor_update(void* current, int64_t c_rs, const void* delta, int64_t d_rs,
+                     void* output, int64_t o_rs, const int64_t* depth, int64_t rows,
+                     int64_t dim, int64_t recursion, int dtype, void* stream);
+
+/* MoR depth routing from the router's logits (MoRRouter.forward,
+ * hydra/routing/mixture_of_recursions.py:259-288), per token, each step
+ * rounded into `dtype`:
+ *   l = round(round(tanh(round(logit / 2))) * 3);  p = round(sigmoid(l));
+ *   dc = round(p * (R - 1)), or round(min_d + round(p * (R - 1 - min_d)))
+ *   depth = clamp(round_half_even(dc), min_d, R - 1).
+ * logits: [n]; probs, logits_out: [n] of dtype (optional); depth: int64 [n]. */
+int hydra_mor_route(const void* logits, int64_t n, void* probs, void* logits_out,
+                    int64_t* depth, int64_t n_recursions, int64_t min_depth, int dtype,
+                    void* stream);
+
 /* ---- Mixture-of-Depths hard routing (hydra/routing, model/framework) --- */
 
 /* Per-row top-k of router scores, ties broken by the lower index, in the
@@ -297,14 +362,20 @@ int hydra_mod_gather(const void* x, const int64_t* idx, void* xs,
 
 #define HYDRA_SCATTER_ADD     0 /* out[b,idx] += w * y  (residual add)    */
 #define HYDRA_SCATTER_REPLACE 1 /* out[b,idx]  = y      (clone + scatter) */
+#define HYDRA_SCATTER_ADD_SEQ 2 /* out[b,idx] += y, repeated idx allowed  */
 
 /* In-place weighted residual scatter into out: [B, L, D] (strides o_bs,
- * o_ls), from y: contiguous [B, k, D], at idx: int64 [B, k] (distinct per
- * row).  w: optional fp32 [B, k] per-row weights (NULL = 1).  ADD replaces
- * the zeros_like + scatter_ + residual add of MoDMLPWrapper._forward_hard
- * and its caller (blocks.py:266-268, :603); REPLACE replaces the
- * clone + scatter_ of MixtureOfDepthsBlock.forward
- * (mixture_of_depths.py:291-295).  Sums are fp32, one rounding. */
+ * o_ls), from y: contiguous [B, k, D], at idx: int64 [B, k].
+ * w: optional fp32 [B, k] per-row weights (NULL = 1; ADD only).
+ * ADD (idx distinct per row) replaces the zeros_like + scatter_ + residual
+ * add of MoDMLPWrapper._forward_hard and its caller (blocks.py:266-268,
+ * :603); sums are fp32, one rounding.  REPLACE (idx distinct per row)
+ * replaces the clone + scatter_ of MixtureOfDepthsBlock.forward
+ * (mixture_of_depths.py:291-295); with y == NULL it clears the rows.
+ * ADD_SEQ replaces scatter_add_by_indices (hydra/routing/ops.py:275-293,
+ * torch.scatter_add_): repeated indices accumulate in index order, rounded
+ * after every add, one thread per (row, column) (not a hot path).
+ * Indices outside [0, L) are skipped. */
 int hydra_mod_scatter(void* out, const void* y, const int64_t* idx,
                       const float* w, int64_t B, int64_t L, int64_t k,
                       int64_t D, int64_t o_bs, int64_t o_ls, int mode,

@@ -140,19 +140,25 @@ def rope_backward(grad_out: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) 
 
 def chunked_cross_entropy(hidden, weight, targets, ignore_index=-100, grad_output=1.0):
     """fp64 restatement of ChunkedCrossEntropyFunction (fused_ops.py:1382-1531):
-    logits = h W^T; targets other than ignore_index clamped into [0, V)
-    (:1407-1422); loss = mean over valid tokens of logsumexp(x) - x[t]
+    logits = h W^T; when any target other than ignore_index lies outside
+    [0, V), the whole target vector (ignore_index entries included) is
+    clamped into [0, V) and validity is recomputed from it (:1407-1422,
+    :1440-1441); loss = mean over valid tokens of logsumexp(x) - x[t]
     (0 with none); grad_x = (softmax(x) - onehot(t)) * grad_output / n_valid
     on valid rows, 0 on ignored rows; grad_h = grad_x W, grad_W = grad_x^T h.
     Returns (loss, grad_h, grad_W) in fp64.  Pinned against autograd of
-    F.cross_entropy in tests/test_oracle_pins.py."""
+    F.cross_entropy and against the reference's own outputs
+    (tests/golden/chunked_ce_cpu.npz) in tests/test_oracle_pins.py."""
     dim = hidden.shape[-1]
     h = hidden.reshape(-1, dim).double()
     w = weight.double()
     t = targets.reshape(-1).long()
     V = w.shape[0]
     valid = t != ignore_index
-    tc = torch.where(valid, t.clamp(0, V - 1), torch.zeros_like(t))
+    if bool((valid & ((t < 0) | (t >= V))).any()):
+        t = t.clamp(0, V - 1)
+        valid = t != ignore_index
+    tc = torch.where(valid, t, torch.zeros_like(t))
     x = h @ w.t()
     lse = torch.logsumexp(x, -1)
     rows = lse - x.gather(1, tc[:, None])[:, 0]

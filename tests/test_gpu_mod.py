@@ -168,3 +168,146 @@ def test_mod_mlp_hard_path(cuda):
 
     assert max_rel_err(out, want) < 1e-5
     assert max_rel_err(hr, h + want) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_scatter_add_repeated_indices(cuda, dtype):
+    """scatter_add_by_indices keeps torch.scatter_add_'s semantics when
+    indices repeat (ops.py:275-293): repeats accumulate in index order."""
+    from hydra_amd.routing import scatter_add_by_indices
+
+    g = torch.Generator().manual_seed(11)
+    out = torch.randn(2, 40, 24, generator=g).to(dtype)
+    vals = torch.randn(2, 60, 24, generator=g).to(dtype)
+    idx = torch.randint(0, 40, (2, 60), generator=g)
+    assert len(torch.unique(idx[0])) < 60  # repeats present
+    want = out.clone().scatter_add_(1, idx.unsqueeze(-1).expand(-1, -1, 24), vals)
+    got = out.to(cuda)
+    scatter_add_by_indices(got, vals.to(cuda), idx.to(cuda))
+    if dtype == torch.float32:
+        assert torch.equal(got.cpu(), want)
+    else:
+        from conftest import max_rel_err
+
+        assert max_rel_err(got.cpu(), want) < 2e-2
+
+
+def test_gather_scatter_backward(cuda):
+    """Gradients through gather_by_indices, scatter_replace and
+    weighted_residual_scatter (weights included) equal autograd through
+    torch.gather / scatter / index-add on the CPU (fp64 reference)."""
+    from hydra_amd.routing import gather_by_indices, scatter_replace, weighted_residual_scatter
+
+    g = torch.Generator().manual_seed(12)
+    B, L, D, k = 2, 50, 16, 30
+    x0 = torch.randn(B, L, D, generator=g)
+    idx = torch.stack([torch.randperm(L, generator=g)[:k] for _ in range(B)])
+    w0 = torch.rand(B, k, generator=g)
+    G = torch.randn(B, L, D, generator=g)
+    G2 = torch.randn(B, L, D, generator=g)
+
+    def run(x, w, gather, scat_rep, scat_add, ix):
+        xs = gather(x, ix) * 2.0 + 1.0
+        out = x * 3.0
+        out = scat_rep(out, xs, ix)
+        h = x * 0.5
+        h = scat_add(h, torch.tanh(xs), ix, w)
+        return (out * G.to(out)).sum() + (h * G2.to(h)).sum()
+
+    xd = x0.to(cuda).requires_grad_()
+    wd = w0.to(cuda).requires_grad_()
+    run(xd, wd, gather_by_indices, scatter_replace, weighted_residual_scatter, idx.to(cuda)).backward()
+
+    def t_gather(x, ix):
+        return torch.gather(x, 1, ix.unsqueeze(-1).expand(-1, -1, x.shape[-1]))
+
+    def t_rep(out, v, ix):
+        return out.scatter(1, ix.unsqueeze(-1).expand(-1, -1, out.shape[-1]), v)
+
+    def t_add(h, v, ix, w):
+        return h.scatter_add(1, ix.unsqueeze(-1).expand(-1, -1, h.shape[-1]), v * w[..., None])
+
+    xr = x0.double().requires_grad_()
+    wr = w0.double().requires_grad_()
+    run(xr, wr, t_gather, t_rep, t_add, idx).backward()
+    from conftest import max_rel_err
+
+    assert max_rel_err(xd.grad.cpu(), xr.grad) < 1e-5
+    assert max_rel_err(wd.grad.cpu(), wr.grad) < 1e-5
+
+
+def test_mixture_of_depths_block_backward(cuda):
+    """MixtureOfDepthsBlock (mixture_of_depths.py:283-297) trains: x and the
+    wrapped block's weights get the gradients autograd gives the reference's
+    gather / clone / scatter_ on the same selection."""
+    from hydra_amd.routing import MixtureOfDepthsBlock
+
+    g = torch.Generator().manual_seed(13)
+    D = 32
+    blk = torch.nn.Linear(D, D)
+    mod = MixtureOfDepthsBlock(blk, D, capacity_ratio=0.5)
+    with torch.no_grad():
+        for p in mod.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.1)
+    x0 = torch.randn(2, 64, D, generator=g)
+    G = torch.randn(2, 64, D, generator=g)
+    mod = mod.to(cuda)
+    xd = x0.to(cuda).requires_grad_()
+    (mod(xd) * G.to(cuda)).sum().backward()
+    with torch.no_grad():
+        _, idx, _ = mod.router(x0.to(cuda))
+    idx = idx.cpu()
+    ref_blk = torch.nn.Linear(D, D).double()
+    ref_blk.load_state_dict({k: v.double().cpu() for k, v in blk.state_dict().items()})
+    xr = x0.double().requires_grad_()
+    ie = idx.unsqueeze(-1).expand(-1, -1, D)
+    out = xr.clone().scatter(1, ie, ref_blk(torch.gather(xr, 1, ie)))
+    (out * G.double()).sum().backward()
+    from conftest import max_rel_err
+
+    assert max_rel_err(xd.grad.cpu(), xr.grad) < 1e-5
+    assert max_rel_err(blk.weight.grad.cpu(), ref_blk.weight.grad) < 1e-5
+    assert max_rel_err(blk.bias.grad.cpu(), ref_blk.bias.grad) < 1e-5
+
+
+def test_mod_mlp_ste_training_backward(cuda):
+    """MoDMLPWrapper in training (the STE path, blocks.py:271-300): the MLP
+    weights and x get the hard path's gradients, and the router gets exactly
+    the aux loss's gradient (the straight-through term is multiplied by 0)."""
+    from hydra_amd.layers import SwiGLUMLPFused
+    from hydra_amd.routing import MoDMLPWrapper
+
+    g = torch.Generator().manual_seed(14)
+    D, Hd, L = 32, 48, 64
+    mlp = SwiGLUMLPFused(D, Hd)
+    wrap = MoDMLPWrapper(mlp, D, capacity_ratio=0.75, warmup_steps=0, aux_loss_weight=0.1)
+    with torch.no_grad():
+        for p in wrap.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.1)
+    wrap.set_global_step(1)
+    wrap = wrap.to(cuda).train()
+    x0 = torch.randn(2, L, D, generator=g)
+    G = torch.randn(2, L, D, generator=g)
+    xd = x0.to(cuda).requires_grad_()
+    out = wrap(xd)
+    ((out * G.to(cuda)).sum() + wrap.get_aux_loss()).backward()
+    idx = wrap._last_indices.cpu()
+
+    ref = {k: v.double().cpu().requires_grad_() for k, v in wrap.state_dict().items()
+           if v.is_floating_point() and not k.endswith("_aux_loss")}
+    xr = x0.double().requires_grad_()
+    ie = idx.unsqueeze(-1).expand(-1, -1, D)
+    xs = torch.gather(xr, 1, ie)
+    gate, up = torch.nn.functional.linear(xs, ref["mlp.gate_up.weight"]).chunk(2, -1)
+    y = torch.nn.functional.linear(torch.nn.functional.silu(gate) * up, ref["mlp.down.weight"])
+    o = torch.zeros_like(xr).scatter(1, ie, y)
+    scores = torch.nn.functional.linear(xr, ref["mod_router.router.weight"],
+                                        ref["mod_router.router.bias"]).squeeze(-1)
+    probs = torch.sigmoid(scores.clamp(-10, 10))
+    aux = 0.1 * ((probs.mean() - 0.75) ** 2 + 0.5 * torch.exp(-probs.var() / max(0.75 * 0.25 * 0.5, 0.01) * 5.0))
+    ((o * G.double()).sum() + aux).backward()
+    from conftest import max_rel_err
+
+    assert max_rel_err(xd.grad.cpu(), xr.grad) < 1e-5
+    for name, p in wrap.named_parameters():
+        assert max_rel_err(p.grad.cpu(), ref[name].grad) < 1e-5, name

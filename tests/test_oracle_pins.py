@@ -492,8 +492,10 @@ def test_attention_backward_autograd(causal, shape):
 
 def test_chunked_cross_entropy_autograd():
     """The restated chunked CE against autograd of F.cross_entropy (fp64) with
-    ignore_index, including clamped out-of-range targets and the all-ignored
-    case (loss 0, zero gradients)."""
+    ignore_index, including out-of-range targets (then the whole target
+    vector is clamped, ignore entries included, fused_ops.py:1407-1422), the
+    same targets without the out-of-range ones (ignore entries stay ignored)
+    and the all-ignored case (loss 0, zero gradients)."""
     g = torch.Generator().manual_seed(11)
     h = torch.randn(3, 7, 16, generator=g, dtype=torch.float64, requires_grad=True)
     w = torch.randn(50, 16, generator=g, dtype=torch.float64, requires_grad=True)
@@ -502,13 +504,15 @@ def test_chunked_cross_entropy_autograd():
     t[2, 3] = -100
     t[1, 2] = 57   # clamped to 49
     t[1, 4] = -7   # clamped to 0
-    tc = torch.where(t == -100, t, t.clamp(0, 49))
-    ref = F.cross_entropy((h.reshape(-1, 16) @ w.t()), tc.reshape(-1), ignore_index=-100)
-    ref.backward(torch.tensor(0.7, dtype=torch.float64))
-    loss, gh, gw = ofo.chunked_cross_entropy(h.detach(), w.detach(), t, grad_output=0.7)
-    assert torch.allclose(loss, ref.detach(), rtol=1e-12)
-    assert torch.allclose(gh, h.grad, rtol=1e-10, atol=1e-13)
-    assert torch.allclose(gw, w.grad, rtol=1e-10, atol=1e-13)
+    for tt, tc in ((t, t.clamp(0, 49)),
+                   (torch.where((t < 0) & (t != -100), 0, torch.where(t > 49, 49, t)),) * 2):
+        h.grad = w.grad = None
+        ref = F.cross_entropy((h.reshape(-1, 16) @ w.t()), tc.reshape(-1), ignore_index=-100)
+        ref.backward(torch.tensor(0.7, dtype=torch.float64))
+        loss, gh, gw = ofo.chunked_cross_entropy(h.detach(), w.detach(), tt, grad_output=0.7)
+        assert torch.allclose(loss, ref.detach(), rtol=1e-12)
+        assert torch.allclose(gh, h.grad, rtol=1e-10, atol=1e-13)
+        assert torch.allclose(gw, w.grad, rtol=1e-10, atol=1e-13)
     loss0, gh0, gw0 = ofo.chunked_cross_entropy(h.detach(), w.detach(), torch.full((3, 7), -100))
     assert loss0 == 0 and gh0.abs().max() == 0 and gw0.abs().max() == 0
 
