@@ -42,6 +42,7 @@ SIGNATURES = {
     "hydra_swiglu_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_qk_norm_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _P],
     "hydra_rms_norm_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
+    "hydra_rms_norm_bwd_noalloc": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
     "hydra_rope_bwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _I64, _I, _I, _P],
     "hydra_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_qk_norm_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _P],

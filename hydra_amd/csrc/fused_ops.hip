@@ -5,6 +5,8 @@
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 namespace hydra {
 
@@ -951,6 +953,58 @@ static int rms_norm_bwd_check(const void* x, const void* w, const void* grad_y, 
   HYDRA_REQUIRE(w_dtype == dtype || w_dtype == HYDRA_F32,
                 "rms_norm_bwd: the weight must be of x's dtype or fp32");
   return HYDRA_OK;
+}
+
+// ---- allocation-free variant ----------------------------------------------
+// hydra_rms_norm_bwd_noalloc keeps the weight-gradient partial rows in this
+// file-scope device array instead of the library's growable workspace, so
+// the call allocates nothing.  8 MiB per device (kRmsBwdParts rows of up to
+// kNoAllocMaxDim fp32), held until the process ends.  Every partial row the
+// reduction reads is written earlier in the same call, so nothing has to be
+// cleared between calls; calls that overlap on one device share the array and
+// race.
+constexpr int64_t kNoAllocMaxDim = 4096;
+static __device__ __align__(256) float scratch[kRmsBwdParts * kNoAllocMaxDim];
+
+// The device address of `scratch` on the current device, looked up once per
+// device (each device holds its own copy of the array).  In host code the
+// name `scratch` is only a handle for the runtime, never an address.
+static int noalloc_scratch(float** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static float* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(HYDRA_ERR_LAUNCH, "rms_norm_bwd_noalloc: no usable current device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(HYDRA_ERR_LAUNCH, std::string("rms_norm_bwd_noalloc: hipGetSymbolAddress failed: ") +
+                                        hipGetErrorString(e));
+    ptrs[dev] = static_cast<float*>(p);
+  }
+  *out = ptrs[dev];
+  return HYDRA_OK;
+}
+
+extern "C" int hydra_rms_norm_bwd_noalloc(const void* x, const void* w, const void* grad_y, void* grad_x,
+                                          void* grad_w, int64_t rows, int64_t dim, int64_t x_rs,
+                                          int64_t gy_rs, int64_t gx_rs, float eps, int dtype, int w_dtype,
+                                          void* stream) {
+  const int rc = rms_norm_bwd_check(x, w, grad_y, grad_x, grad_w, rows, dim, x_rs, gy_rs, gx_rs, dtype,
+                                    w_dtype);
+  if (rc != HYDRA_OK) return rc;
+  if (dim > kNoAllocMaxDim)
+    return fail(HYDRA_ERR_ARG, "rms_norm_bwd_noalloc: dim " + std::to_string(dim) +
+                                   " exceeds the fixed scratch's maximum of " +
+                                   std::to_string(kNoAllocMaxDim) + "; use hydra_rms_norm_bwd");
+  float* part = nullptr;
+  const int src = noalloc_scratch(&part);
+  if (src != HYDRA_OK) return src;
+  return rms_norm_bwd_body(x, w, grad_y, grad_x, grad_w, part, rows, dim, x_rs, gy_rs, gx_rs, eps, dtype,
+                           w_dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,

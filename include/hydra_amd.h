@@ -105,6 +105,18 @@ int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* g
                        void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
                        int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream);
 
+/* hydra_rms_norm_bwd without any allocation: the same kernels and results
+ * (bit for bit), with the weight-gradient partials in a fixed 8 MiB device
+ * array of the library (one per device, held until the process ends) instead
+ * of the growable workspace.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Limit: dim <= 4096
+ * (HYDRA_ERR_ARG beyond).  Calls that overlap on one device share the array
+ * and race; calls on one stream are ordered. */
+int hydra_rms_norm_bwd_noalloc(const void* x, const void* w, const void* grad_y, void* grad_x,
+                               void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
+                               int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream);
+
 /* RoPE backward: grad_x = the rotation of hydra_rope_fwd transposed,
  *   gx[..,2i] = g[..,2i]*cos + g[..,2i+1]*sin, gx[..,2i+1] = -g[..,2i]*sin + g[..,2i+1]*cos.
  * The reference's Triton RoPE records no gradient (fused_ops.py:256-297);
