@@ -21,10 +21,19 @@ Also reported on the same line:
                 (buffers rotated over > 512 MB so the 256 MB MALL cannot
                 serve repeats);
   mod           config 4 top-k / gather / residual scatter;
+  c1_block      config 1: embedding + HydraBlock (CCGQA dim 512, 8/2 heads
+                of 16, SwiGLU hidden 1365) forward in fp32, B2 x S512,
+                tokens/s (a HIP graph of the steps), with the oracle's CPU
+                figure for the same workload;
+  c5_model      config 5: HydraModel forward in bf16 at the 1B shape (dim
+                1792, 20 MoR blocks x 4 recursions, MoD 0.75 in the middle
+                blocks, vocab 32000), B4 x S4096, tokens/s;
   cpu_baseline  the oracle (the reference's PyTorch CPU path restated) on a
-                bounded sample of the same workload, on this host's cores.
+                bounded sample of the same workload, on this host's cores;
+                cpu_baselines adds configs 1, 2 and 4 the same way.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                      [--only-c3] [--no-c5]
 """
 from __future__ import annotations
 
@@ -413,42 +422,245 @@ def bench_mod(dev, iters=50):
 
 
 # ------------------------------------------------------------- CPU baseline
-def cpu_baseline(budget_s=12.0):
+def host_cpu() -> dict:
+    """This host's CPU as the baseline reports it: model name, physical and
+    logical cores, the CPUs this process may run on, ISA extensions that
+    matter for torch's CPU kernels, and the threads the baselines use.
+    Threads: the CPUs this process may use, capped by OMP_NUM_THREADS when
+    the environment sets it (a GPU box shares its host between GPUs) and by
+    the physical core count (no SMT siblings)."""
+    info = {"model": "unknown", "physical_cores": None, "logical_cores": os.cpu_count(),
+            "usable_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+    flags, cores = set(), set()
+    phys = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and info["model"] == "unknown":
+                info["model"] = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+                cores.add((phys, core))
+            elif key == "flags" and not flags:
+                flags = set(val.split())
+    except OSError:
+        pass
+    info["physical_cores"] = len(cores) or None
+    info["isa"] = {f: f in flags for f in ("avx2", "avx512f", "avx512_bf16", "amx_bf16", "amx_tile")}
+    threads = info["usable_cpus"] or info["logical_cores"] or 1
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    if info["physical_cores"]:
+        threads = min(threads, info["physical_cores"])
+    info["threads"] = max(1, threads)
+    info["torch"] = torch.__version__
+    return info
+
+
+def _median_time(fn, budget_s, min_runs=5, max_runs=200, warmup=2):
+    for _ in range(warmup):
+        fn()
+    times = []
+    start = time.perf_counter()
+    while len(times) < min_runs or ((time.perf_counter() - start) < budget_s and len(times) < max_runs):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return sorted(times)[len(times) // 2], len(times), time.perf_counter() - start
+
+
+def cpu_baseline(host: dict, budget_s=12.0):
     """The oracle (reference PyTorch CPU path restated) on the config 3
     workload (B=4 x S=4096, bf16): tokens/s on this host, median over repeats
     bounded by budget_s seconds."""
     from oracle import ccgqa as occ
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    torch.set_num_threads(host["threads"])
     cfg = occ.CCGQAConfig(dim=1024, n_heads=4, n_kv_heads=1, compression_factor=4, max_seq_len=4096)
     g = torch.Generator().manual_seed(0)
     params = {k: v.to(torch.bfloat16) for k, v in occ.init_params(cfg, g, temperature=1.0).items()}
     B, S = 4, 4096
     x = torch.randn(B, S, 1024, generator=g).to(torch.bfloat16)
     with torch.no_grad():
-        for _ in range(2):
-            occ.forward(params, x, cfg)  # warmup
-        times = []
-        start = time.perf_counter()
-        while len(times) < 5 or ((time.perf_counter() - start) < budget_s and len(times) < 200):
-            t = time.perf_counter()
-            occ.forward(params, x, cfg)
-            times.append(time.perf_counter() - t)
-    med = sorted(times)[len(times) // 2]
-    cpu_name = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_name = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": B * S / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+        med, n, el = _median_time(lambda: occ.forward(params, x, cfg), budget_s)
+    return {"value": B * S / med, "unit": "tokens/s", "cores": host["threads"], "kind": "port",
             "sample": f"oracle CCGQA forward (attention.py:201-331 restated on torch CPU ops), "
-                      f"full config 3 (B=4 x S=4096, bf16); median of {len(times)} runs in "
-                      f"{time.perf_counter() - start:.1f} s, {threads} threads on '{cpu_name}', "
-                      f"torch {torch.__version__}"}
+                      f"full config 3 (B=4 x S=4096, bf16); median of {n} runs in {el:.1f} s",
+            "host": host}
+
+
+def cpu_baselines(host: dict, budget_s=6.0) -> dict:
+    """Configs 1, 2 and 4 on the oracle (the reference's CPU ops) in their
+    own dtypes, same host and threads as cpu_baseline."""
+    import math
+
+    from oracle import blocks as ob
+    from oracle import ccgqa as occ
+    from oracle import fused_ops as ofo
+    from oracle import mod as omod
+
+    torch.set_num_threads(host["threads"])
+    res = {}
+    g = torch.Generator().manual_seed(0)
+    # config 1: embedding + HydraBlock, fp32, B2 x S512
+    cfg = occ.CCGQAConfig(dim=512, n_heads=8, n_kv_heads=2, compression_factor=4, max_seq_len=512)
+    p = {"attention." + k: v for k, v in occ.init_params(cfg, g, temperature=4.0).items()}
+    p.update({"norm1.weight": torch.ones(512), "norm2.weight": torch.ones(512),
+              "mlp.gate_up.weight": torch.randn(2 * 1365, 512, generator=g) * 0.02,
+              "mlp.down.weight": torch.randn(512, 1365, generator=g) * 0.02,
+              "tok_emb.weight": torch.randn(32000, 512, generator=g) * 0.02})
+    ids = torch.randint(0, 32000, (2, 512), generator=g)
+    with torch.no_grad():
+        med, n, _ = _median_time(lambda: ob.c1_forward(p, ids, cfg), budget_s)
+    res["c1_block"] = {"value": 1024 / med, "unit": "tokens/s", "dtype": "fp32",
+                       "sample": f"full config 1 (B2 x S512), median of {n}"}
+    # config 2: RMSNorm / RoPE / SwiGLU activation, bf16, full shapes
+    bf = torch.bfloat16
+    x = torch.randn(8, 2048, 768, generator=g).to(bf)
+    w = (1 + 0.1 * torch.randn(768, generator=g)).to(bf)
+    xr = torch.randn(8, 12, 2048, 64, generator=g).to(bf)
+    cos, sin = ofo.rope_cache(64, 2048)
+    gate = torch.randn(8, 2048, 2048, generator=g).to(bf)
+    up = torch.randn(8, 2048, 2048, generator=g).to(bf)
+    for name, fn, nbytes in (
+            ("rms_norm", lambda: ob.rms_norm(x, w, 1e-6), 50_333_184),
+            ("rope", lambda: ofo.rope(xr, cos, sin), 50_855_936),
+            ("swiglu", lambda: F.silu(gate) * up, 201_326_592)):
+        med, n, _ = _median_time(fn, budget_s / 3)
+        res[name] = {"ms": med * 1e3, "GBs": nbytes / med / 1e9, "dtype": "bf16",
+                     "sample": f"full config 2 shape, median of {n}"}
+    # config 4: top-k (torch.topk + mask), gather, residual scatter, bf16 rows
+    scores = omod.make_tied_logits(8, 4096, 0.05, g)
+    xs = torch.randn(8, 4096, 1280, generator=g).to(bf)
+    ys = torch.randn(8, 3072, 1280, generator=g).to(bf)
+    idx = torch.topk(scores, 3072, dim=-1).indices.sort(dim=1).values
+    ie = idx.unsqueeze(-1).expand(-1, -1, 1280)
+
+    def topk():
+        _, ti = torch.topk(scores, 3072, dim=-1)
+        torch.zeros(8, 4096).scatter_(1, ti, 1.0)
+        return torch.sort(ti, dim=1)
+
+    for name, fn in (("topk", topk), ("gather", lambda: torch.gather(xs, 1, ie)),
+                     ("scatter", lambda: xs + torch.zeros_like(xs).scatter_(1, ie, ys))):
+        med, n, _ = _median_time(fn, budget_s / 3)
+        res["mod_" + name] = {"ms": med * 1e3, "dtype": "bf16" if name != "topk" else "fp32",
+                              "sample": f"full config 4 shape, median of {n}"}
+    res["host"] = host
+    res["kind"] = "port"
+    return res
+
+
+# ----------------------------------------------------------------- config 1
+def bench_c1(dev, steps=50):
+    """Config 1 on the GPU: embedding (vocab 32000) * sqrt(512) then
+    HydraBlock (CCGQA dim 512, 8/2 heads of 16, 4x compression, conv k=3,
+    QK-mean, QK-norm, SwiGLU hidden 1365), fp32, ids [2, 512], N(0, 0.02)
+    weights.  The steps are captured in one HIP graph (launch-bound
+    workload: ~15 small launches), replayed untimed once, then timed."""
+    import math
+
+    from hydra_amd.layers import SwiGLUMLPFused
+    from hydra_amd.model.framework import HydraBlock, embedding_lookup
+
+    g = torch.Generator().manual_seed(0)
+    with torch.device(dev):
+        blk = HydraBlock(dim=512, n_heads=8, n_kv_heads=2, compression_factor=4, max_seq_len=512)
+        blk.mlp = SwiGLUMLPFused(512, 1365)
+        table = torch.empty(32000, 512)
+    with torch.no_grad():
+        for name, prm in blk.named_parameters():
+            if name.endswith("key_temperature"):
+                prm.fill_(4.0)
+            elif "norm" in name:
+                prm.fill_(1.0)
+            else:
+                prm.copy_(torch.randn(prm.shape, generator=g) * 0.02)
+        table.copy_(torch.randn(table.shape, generator=g) * 0.02)
+    blk.eval()
+    ids = torch.randint(0, 32000, (2, 512), generator=g).to(dev)
+
+    def step():
+        with torch.no_grad():
+            return blk(embedding_lookup(table, ids, math.sqrt(512)))
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = _events(2)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    del graph
+    from oracle import blocks as ob
+    from oracle import ccgqa as occ
+
+    fl = ob.flops_c1(occ.CCGQAConfig(dim=512, n_heads=8, n_kv_heads=2, compression_factor=4), 2, 512, 1365)
+    return {"value": 1024 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "steps": steps,
+            "dtype": "fp32", "flops": fl, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+            "workload": "config 1: embedding + HydraBlock, dim 512, 8/2 heads x hd 16, SwiGLU 1365, "
+                        "ids [2, 512] over vocab 32000, fp32, HIP graph of the steps"}
+
+
+# ----------------------------------------------------------------- config 5
+def bench_c5(dev, steps=3, warmup=1):
+    """Config 5: HydraModel forward at the 1B shape in bf16 -- dim 1792, 20
+    MoR blocks x 4 recursions (80 effective layers), CCGQA 4x compression
+    (latent 448) with the reference's 1B preset heads 28 / 4 KV (7:1; 8:1
+    does not divide 448 into even head dims with a power-of-two-friendly
+    layout), SwiGLU mlp_ratio 3.6 (the trainer's, hidden 6656), MoD capacity
+    0.75 on the MLP of blocks 1..18 (hard routing: global step past the MoD
+    warmup), MoR depth routing with the code's layer-aware router target
+    0.2 -> 0.5, tied LM head over vocab 32000; ids [4, 4096]; random N(0,
+    0.02) weights from the model's own init.  Eager launches; events
+    bracket the K steps."""
+    from hydra_amd.model.framework import HydraModel
+
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = HydraModel(vocab_size=32000, dim=1792, n_mor_blocks=20, recursions_per_block=4,
+                           n_heads=28, n_kv_heads=4, compression_factor=4, mlp_ratio=3.6,
+                           max_seq_len=4096, mod_capacity=0.75, adaptive=True, tie_weights=True)
+    model = model.to(torch.bfloat16).eval()
+    model.set_global_step(10_000)
+    n_params = sum(p.numel() for p in model.parameters())
+    g = torch.Generator(device=dev).manual_seed(0)
+    ids = torch.randint(0, 32000, (4, 4096), device=dev, generator=g)
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(ids)
+        torch.cuda.synchronize()
+        a, b = _events(2)
+        a.record()
+        for _ in range(steps):
+            out = model(ids)
+        b.record()
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    assert out.shape == (4, 4096, 32000) and torch.isfinite(out[0, :4].float()).all()
+    del model, out
+    torch.cuda.empty_cache()
+    return {"value": 4 * 4096 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "steps": steps,
+            "warmup": warmup, "dtype": "bf16", "params": n_params,
+            "workload": "config 5: HydraModel 1B shape (dim 1792, 20 MoR blocks x 4 recursions, "
+                        "28/4 heads x hd 16, mlp 3.6, MoD 0.75 middle blocks, vocab 32000), "
+                        "B4 x S4096, bf16, eager"}
 
 
 def calibrate_copy(mib=512, reps=3):
@@ -481,7 +693,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only-c3", action="store_true", help="skip the fused-op and MoD sections")
+    ap.add_argument("--only-c3", action="store_true", help="skip every section but config 3")
+    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 model forward")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 512 MiB device copy (traffic-counter calibration)")
     args = ap.parse_args()
@@ -533,8 +746,15 @@ def main():
         line["mod"] = bench_mod(dev)
         line["attention_backward"] = bench_attention_backward(dev)
         line["cross_entropy"] = bench_cross_entropy(dev)
+        line["c1_block"] = bench_c1(dev)
+        if not args.no_c5:
+            line["c5_model"] = bench_c5(dev)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline()
+        host = host_cpu()
+        line["cpu_baseline"] = cpu_baseline(host)
+        if not args.only_c3:
+            line["cpu_baselines"] = cpu_baselines(host)
+            line["c1_block"]["cpu_tokens_per_s"] = line["cpu_baselines"]["c1_block"]["value"]
     print(json.dumps(line))
 
 

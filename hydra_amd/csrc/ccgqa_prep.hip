@@ -23,7 +23,7 @@
 // [out, in/groups, 3] permuted (2, 0, 1)), so a row of input channels for one
 // (tap, output channel) is contiguous.
 //
-// Two variants: ccgqa_prep_mfma_kernel (bf16, head_dim in {32, 64, 128}) runs
+// Two variants: ccgqa_prep_mfma_kernel (bf16, head_dim in {16, 32, 64, 128}) runs
 // both convs as v_mfma_f32_32x32x16_bf16 tiles over LDS-staged token rows;
 // ccgqa_prep_generic_kernel (VALU, fp32 arithmetic) takes every other case.
 #include "common.h"
@@ -279,6 +279,7 @@ __device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int w
                                           const uint16_t* bbase, BRow brow,
                                           f32x16_p (&acc)[NT]) {
   switch (CS) {  // CS is uniform: a scalar branch
+    case 1: return conv_task_fixed<NT, 1>(wbase, wtap, wstep, bbase, brow, acc);
     case 2: return conv_task_fixed<NT, 2>(wbase, wtap, wstep, bbase, brow, acc);
     case 4: return conv_task_fixed<NT, 4>(wbase, wtap, wstep, bbase, brow, acc);
     case 8: return conv_task_fixed<NT, 8>(wbase, wtap, wstep, bbase, brow, acc);
@@ -298,6 +299,33 @@ __device__ __forceinline__ void conv_task(const bf16* wbase, int64_t wtap, int w
         const bf16x8_p bb = ld_bf16x8(bt[j] + 16 * c);
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bb, acc[j], 0, 0, 0);
       }
+    }
+  }
+}
+
+// conv1 of an m-tile when head_dim is 16: its 32 output channels are two
+// groups of 16 with different inputs (channels cbase..cbase+15 for rows
+// 0..15, cbase+16..cbase+31 for rows 16..31), i.e. a block-diagonal 32 x 32
+// weight.  Each tap runs two k-steps over the 32 inputs with the A fragment
+// (lane row n, which the weight layout gives as W[o0+n][8 hf .. 8 hf + 8])
+// zeroed in the step of the other group.
+template <int NT, typename BRow>
+__device__ __forceinline__ void conv1_task_hd16(const bf16* wbase, int64_t wtap,
+                                                const uint16_t* bbase, BRow brow, int n,
+                                                f32x16_p (&acc)[NT]) {
+  const bf16x8_p zero = {};
+  bf16x8_p a[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) a[t] = ld_bf16x8(wbase + t * wtap);
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const bf16x8_p a0 = n < 16 ? a[t] : zero, a1 = n < 16 ? zero : a[t];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const bf16x8_p b0 = ld_bf16x8(bbase + brow(j, t));
+      const bf16x8_p b1 = ld_bf16x8(bbase + brow(j, t) + 16);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[j], 0, 0, 0);
     }
   }
 }
@@ -538,8 +566,11 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
       for (int j = 0; j < NT1; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-      conv_task<NT1>(wbase, static_cast<int64_t>(O) * HD, wstep, HD / 16, X + cbase + 8 * hf,
-                     [&](int j, int t) { return min(32 * j + n + t, TT + 3) * RS; }, acc);
+      auto brow1 = [&](int j, int t) { return min(32 * j + n + t, TT + 3) * RS; };
+      if constexpr (HD == 16)
+        conv1_task_hd16<NT1>(wbase, static_cast<int64_t>(O) * HD, X + cbase + 8 * hf, brow1, n, acc);
+      else
+        conv_task<NT1>(wbase, static_cast<int64_t>(O) * HD, wstep, HD / 16, X + cbase + 8 * hf, brow1, acc);
 #pragma unroll
       for (int j = 0; j < NT1; ++j) {
         const int i = 32 * j + n;
@@ -570,8 +601,12 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
   // side work are done with X).  Without convs, Y2 is X's rows 4.. as is.
   uint16_t* Y2 = convs ? X : X + 4 * RS;  // row r <-> token s0 + r
   if (convs) {
-    constexpr int MT = HD / 32;
-    for (int hh = wave; hh < Hq + Hkv; hh += kPrepThreads / 64) {
+    // A task covers 32 * MT output channels: one head when HD >= 32, one
+    // 32-channel m-tile (32 / HD heads; L and K are multiples of 32) when
+    // HD = 16.
+    constexpr int MT = HD >= 32 ? HD / 32 : 1;
+    constexpr int HPT = HD >= 32 ? 1 : 32 / HD;  // heads per task
+    for (int hh = wave * HPT; hh < Hq + Hkv; hh += HPT * (kPrepThreads / 64)) {
       const bool is_k = hh >= Hq;
       const int head = is_k ? hh - Hq : hh;
       const int C = is_k ? K : L;
@@ -734,7 +769,8 @@ using namespace hydra;
 
 extern "C" int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype) {
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
-  if (dtype != HYDRA_BF16 || !(hd == 32 || hd == 64 || hd == 128)) return 0;
+  if (dtype != HYDRA_BF16 || !(hd == 16 || hd == 32 || hd == 64 || hd == 128)) return 0;
+  if ((Hq * hd) % 32 != 0 || (Hkv * hd) % 32 != 0) return 0;
   int dev = 0, max_lds = 65536;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
@@ -768,7 +804,8 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
   auto st = static_cast<hipStream_t>(stream);
   const bool rope = flags & HYDRA_CCGQA_ROPE;
   const bool mfma_ok =
-      dtype == HYDRA_BF16 && (hd == 32 || hd == 64 || hd == 128) && K % 32 == 0 &&
+      dtype == HYDRA_BF16 && (hd == 16 || hd == 32 || hd == 64 || hd == 128) && K % 32 == 0 &&
+      L % 32 == 0 &&
       qkv_rs % 8 == 0 && aligned16(qkv) && aligned16(q_out) && aligned16(k_out) &&
       aligned16(v_out) &&
       (!(flags & HYDRA_CCGQA_CONVS) || (aligned16(wq1) && aligned16(wq2) && aligned16(wk1) &&
@@ -782,6 +819,7 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
       max_lds = 65536;
     int rc = -1;
     switch (hd) {
+      case 16: rc = launch_prep_mfma<16>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
       case 32: rc = launch_prep_mfma<32>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
       case 64: rc = launch_prep_mfma<64>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
       default: rc = launch_prep_mfma<128>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs, q_out, k_out, v_out, B, S, Hq, Hkv, flags, max_lds, st); break;
@@ -790,7 +828,7 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
   }
   if (flags & HYDRA_CCGQA_W_TILED)
     return fail(HYDRA_ERR_UNSUPPORTED,
-                "ccgqa_prep: MFMA-tiled conv weights need the MFMA path (bf16, head_dim 32/64/128, "
+                "ccgqa_prep: MFMA-tiled conv weights need the MFMA path (bf16, head_dim 16/32/64/128, "
                 "16-byte aligned pointers, S % 8 == 0 with V_TRANSPOSED)");
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     return launch_prep_generic<T>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs,

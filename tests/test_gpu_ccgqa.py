@@ -49,6 +49,11 @@ PREP_CASES = [
     dict(dim=2048, n_heads=4, n_kv_heads=2, compression_factor=4, B=1, S=200),
     # head_dim 32, one q head per kv head (QK-mean (q0 + k0) / 2), no convs
     dict(dim=512, n_heads=4, n_kv_heads=4, compression_factor=4, B=2, S=96, use_convs=False),
+    # config 5's layout: latent 448, 28 q / 4 kv heads of 16 (MFMA path, two
+    # heads per conv m-tile, block-diagonal conv1)
+    dict(dim=1792, n_heads=28, n_kv_heads=4, compression_factor=4, B=1, S=264),
+    # head_dim 16 with a ragged last tile
+    dict(dim=256, n_heads=4, n_kv_heads=2, compression_factor=4, B=2, S=77),
 ]
 
 
