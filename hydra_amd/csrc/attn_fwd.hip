@@ -26,8 +26,10 @@
 //  * Schedule: stream-K (equal key-tile ranges over one resident wave of
 //    workgroups, split items folded by attn_merge_kernel) when items are
 //    few, else one workgroup per item, longest first.
-// Generic path (attn_fwd_generic_kernel): one thread per query row, fp32
-// math, any element type, even head_dim <= 256.
+// VALU paths (fp32 math, any element type): attn_fwd_split_kernel for
+// head_dim in {8, 16, 32, 64, 128} (16 lanes per query row, key-split), and
+// attn_fwd_generic_kernel (one thread per query row) for any other
+// head_dim <= 256.
 #include "common.h"
 #include "lds_dma.h"
 
@@ -1102,6 +1104,160 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   return use_fixed ? go(F_(), M0(), T_()) : go(F_(), M0(), F_());
 }
 
+// ---------------------------------------------------------------------------
+// Key-split VALU kernel (fp32 / fp16, and bf16 shapes the MFMA kernel does
+// not take), head_dim a compile-time HD in {8, 16, 32, 64, 128}: a
+// workgroup takes 16 consecutive query rows of one (batch, head) and stages
+// 64-key tiles of K and V (fp32, rows padded by one word so the 16 keys a
+// row's lanes read fall in distinct banks) in LDS; each row is split over 16
+// lanes, lane l taking keys l, l+16, .. of every tile with its own online
+// softmax (exp2 domain, one rescale per tile), and the 16 partial states are
+// merged by shuffles at the end.  Same semantics as attn_fwd_generic_kernel
+// (mask modes, lse), the rows spread over 16x the threads.
+// ---------------------------------------------------------------------------
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void attn_fwd_split_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    T* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
+    int B, int S, int Hq, int Hkv, int causal, int mask_mode,
+    int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2, int64_t vs3, int64_t os0, int64_t os1, int64_t os2,
+    float scale) {
+  constexpr int KL = 16;            // lanes per query row
+  constexpr int RW = 256 / KL;      // query rows per workgroup
+  constexpr int TK = 64;            // keys per staged tile
+  constexpr int KPT = TK / KL;      // keys per lane per tile
+  constexpr int KP = HD + 1;        // padded LDS row (words)
+  __shared__ float Ks[TK * KP], Vs[TK * KP];
+  __shared__ int Vis[TK];           // key usable under the key mask (modes 1, 2)
+  const int BH = B * Hq;
+  const int nsb = (S + RW - 1) / RW;
+  // longest rows first: blocks of the last query rows are dispatched first
+  const int bh = blockIdx.x % BH;
+  const int sb = nsb - 1 - static_cast<int>(blockIdx.x / BH);
+  const int b = bh / Hq, h = bh - b * Hq;
+  const int j = h / (Hq / Hkv);
+  const int tid = threadIdx.x, row = tid / KL, kl = tid % KL;
+  const int s = sb * RW + row;
+  const bool live = s < S;
+  const float qscale = scale * kLog2e;
+  float qv[HD], acc[HD];
+  {
+    const T* qr = q + b * qs0 + h * qs1 + static_cast<int64_t>(live ? s : 0) * qs2;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) {
+      qv[d] = to_f32(qr[d]) * qscale;
+      acc[d] = 0.f;
+    }
+  }
+  float m = -INFINITY, l = 0.f;
+  const bool walk = causal && mask_mode != HYDRA_MASK_REFERENCE_SDPA;
+  const int kend = walk ? min(S, sb * RW + RW) : S;
+  const T* kb = k + b * ks0 + j * ks1;
+  const T* vb = v + b * vs0 + j * vs1;
+  for (int t0 = 0; t0 < kend; t0 += TK) {
+    __syncthreads();
+    for (int i = tid; i < TK * HD; i += 256) {
+      const int kk = i / HD, d = i - kk * HD;
+      const int t = t0 + kk;
+      const bool in = t < S;
+      Ks[kk * KP + d] = in ? to_f32(kb[static_cast<int64_t>(t) * ks2 + d]) : 0.f;
+      Vs[kk * KP + d] = in ? to_f32(vb[static_cast<int64_t>(t) * vs2 + d * vs3]) : 0.f;
+    }
+    if (mask_mode != HYDRA_MASK_NONE && tid < TK) {
+      const int t = t0 + tid;
+      Vis[tid] = t < S ? (kmask[static_cast<int64_t>(b) * S + t] != 0) : 0;
+    }
+    __syncthreads();
+    float x[KPT];
+    float mt = m;
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int kk = kl + KL * u;
+      const int t = t0 + kk;
+      bool vis = live && t < S;
+      if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) vis = vis && (t > s || Vis[kk] == 0);
+      else {
+        if (causal) vis = vis && t <= s;
+        if (mask_mode == HYDRA_MASK_KEY_PADDING) vis = vis && Vis[kk] != 0;
+      }
+      float dot = 0.f;
+      const float* kr = Ks + kk * KP;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) dot = fmaf(qv[d], kr[d], dot);
+      x[u] = vis ? dot : -INFINITY;
+      mt = fmaxf(mt, x[u]);
+    }
+    if (mt == -INFINITY) continue;  // nothing visible to this lane yet
+    if (mt > m) {
+      const float alpha = __builtin_amdgcn_exp2f(m - mt);  // m = -inf -> 0
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) acc[d] *= alpha;
+      m = mt;
+    }
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const float pu = __builtin_amdgcn_exp2f(x[u] - m);  // -inf -> 0
+      l += pu;
+      const float* vr = Vs + (kl + KL * u) * KP;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) acc[d] = fmaf(pu, vr[d], acc[d]);
+    }
+  }
+  // merge the KL lanes of the row
+  float mg = m;
+#pragma unroll
+  for (int off = KL / 2; off > 0; off >>= 1) mg = fmaxf(mg, __shfl_xor(mg, off, KL));
+  const float f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mg);
+  l *= f;
+#pragma unroll
+  for (int off = KL / 2; off > 0; off >>= 1) l += __shfl_xor(l, off, KL);
+#pragma unroll
+  for (int d = 0; d < HD; ++d) {
+    float a = acc[d] * f;
+#pragma unroll
+    for (int off = KL / 2; off > 0; off >>= 1) a += __shfl_xor(a, off, KL);
+    acc[d] = a;
+  }
+  if (!live) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = o + b * os0 + h * os1 + static_cast<int64_t>(s) * os2;
+#pragma unroll
+  for (int d = 0; d < HD; ++d)
+    if (d % KL == kl) orow[d] = from_f32<T>(acc[d] * inv);
+  if (lse && kl == 0)
+    lse[(static_cast<int64_t>(b) * Hq + h) * S + s] = l > 0.f ? (mg + __log2f(l)) * kLn2 : -INFINITY;
+}
+
+template <typename T>
+static int launch_split(const void* q, const void* k, const void* v, void* o, float* lse,
+                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq, int64_t Hkv,
+                        int64_t S, int64_t hd, const int64_t* qs, const int64_t* ks,
+                        const int64_t* vs, const int64_t* os, bool causal, float scale,
+                        hipStream_t st) {
+  const int64_t nblk = B * Hq * ((S + 15) / 16);
+  const dim3 grid(static_cast<unsigned>(nblk));
+  auto Q = static_cast<const T*>(q);
+  auto K = static_cast<const T*>(k);
+  auto V = static_cast<const T*>(v);
+  auto O = static_cast<T*>(o);
+#define HYDRA_SPLIT_LAUNCH(HD)                                                              \
+  attn_fwd_split_kernel<T, HD><<<grid, 256, 0, st>>>(                                       \
+      Q, K, V, O, lse, kmask, (int)B, (int)S, (int)Hq, (int)Hkv, causal ? 1 : 0, mask_mode, \
+      qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], vs[3], os[0], os[1],   \
+      os[2], scale)
+  switch (hd) {
+    case 8: HYDRA_SPLIT_LAUNCH(8); break;
+    case 16: HYDRA_SPLIT_LAUNCH(16); break;
+    case 32: HYDRA_SPLIT_LAUNCH(32); break;
+    case 64: HYDRA_SPLIT_LAUNCH(64); break;
+    default: HYDRA_SPLIT_LAUNCH(128); break;
+  }
+#undef HYDRA_SPLIT_LAUNCH
+  return check_launch("attn_fwd_split_kernel");
+}
+
 template <typename T>
 static int launch_generic(const void* q, const void* k, const void* v, void* o, float* lse,
                           const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
@@ -1181,7 +1337,11 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
     }
   }
   HYDRA_REQUIRE(B * Hq * S / 256 < (int64_t(1) << 31), "attn_fwd: too many rows");
+  const bool split_shape = hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128;
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    if (split_shape && getenv("HYDRA_ATTN_GENERIC") == nullptr)
+      return launch_split<T>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, hd, qs, ks, vs, os,
+                             causal != 0, scale, st);
     return launch_generic<T>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, hd, qs, ks, vs,
                              os, causal != 0, scale, st);
   });

@@ -28,6 +28,7 @@
 // ccgqa_prep_generic_kernel (VALU, fp32 arithmetic) takes every other case.
 #include "common.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -204,6 +205,198 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
   }
 }
 
+
+// ===========================================================================
+// VALU variant for the shapes the MFMA kernel does not take (fp32, fp16,
+// odd head layouts): TT = 8 tokens per workgroup, fp32 LDS rows.  A thread
+// owns one output channel at a time and keeps the tile's TT (conv2) or
+// TT + 2 (conv1) token accumulators in registers, so each weight element it
+// reads (tap-major rows, 4 consecutive input channels per step) feeds TT
+// FMAs, and the token rows come from LDS as 16-byte broadcast reads.
+// Rounding points as in ccgqa_prep_generic_kernel.
+// ===========================================================================
+constexpr int kPrepVecTT = 8;
+
+template <typename T>
+__device__ __forceinline__ void ld4(const T* p, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    T a, b2, c, d;
+    a.bits = v.x & 0xffffu; b2.bits = v.x >> 16; c.bits = v.y & 0xffffu; d.bits = v.y >> 16;
+    out[0] = to_f32(a); out[1] = to_f32(b2); out[2] = to_f32(c); out[3] = to_f32(d);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void ccgqa_prep_vec_kernel(
+    const T* __restrict__ qkv, int64_t qkv_rs, const T* __restrict__ wq1,
+    const T* __restrict__ wq2, const T* __restrict__ wk1, const T* __restrict__ wk2,
+    const T* __restrict__ temp, const float* __restrict__ cs, const float* __restrict__ sn,
+    int64_t cs_rs, T* __restrict__ qo, T* __restrict__ ko, T* __restrict__ vo, int S,
+    int Hq, int Hkv, int hd, int flags) {
+  constexpr int TT = kPrepVecTT;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  float* sm = reinterpret_cast<float*>(smem_raw);
+  const int L = Hq * hd, K = Hkv * hd, CW = L + K;
+  float* xs = sm;                    // rows: tokens s0-4 .. s0+TT-1
+  float* y1 = xs + (TT + 4) * CW;    // rows: tokens s0-2 .. s0+TT-1
+  float* y2 = y1 + (TT + 2) * CW;    // rows: tokens s0   .. s0+TT-1
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int b = blockIdx.y;
+  const int s0 = blockIdx.x * TT;
+  const bool convs = flags & HYDRA_CCGQA_CONVS;
+  const bool qk_mean = flags & HYDRA_CCGQA_QK_MEAN;
+  const bool vshift = flags & HYDRA_CCGQA_VALUE_SHIFT;
+  const bool qk_norm = flags & HYDRA_CCGQA_QK_NORM;
+  const bool rope = flags & HYDRA_CCGQA_ROPE;
+  const T* xb = qkv + static_cast<int64_t>(b) * S * qkv_rs;
+
+  for (int i = tid; i < (TT + 4) * CW; i += nth) {
+    const int r = i / CW, c = i - r * CW;
+    const int s = s0 - 4 + r;
+    xs[i] = (s >= 0 && s < S) ? to_f32(xb[static_cast<int64_t>(s) * qkv_rs + c]) : 0.f;
+  }
+  __syncthreads();
+
+  if (convs) {
+    // conv1 (grouped): output o of group g reads channels g*hd .. g*hd+hd-1
+    // of rows r .. r+2 (tap t = row offset); outputs of tokens < 0 stay 0
+    // (conv2's causal padding).
+    for (int o = tid; o < CW; o += nth) {
+      const bool is_q = o < L;
+      const int oo = is_q ? o : o - L, O = is_q ? L : K;
+      const int col0 = (is_q ? 0 : L) + (oo / hd) * hd;
+      float acc[TT + 2];
+#pragma unroll
+      for (int r = 0; r < TT + 2; ++r) acc[r] = 0.f;
+      for (int t = 0; t < 3; ++t) {
+        const T* w = (is_q ? wq1 : wk1) + (static_cast<int64_t>(t) * O + oo) * hd;
+        for (int c = 0; c < hd; c += 4) {
+          float wv[4];
+          ld4(w + c, wv);
+#pragma unroll
+          for (int r = 0; r < TT + 2; ++r) {
+            const float4 xv = *reinterpret_cast<const float4*>(xs + (r + t) * CW + col0 + c);
+            acc[r] = fmaf(wv[0], xv.x, fmaf(wv[1], xv.y, fmaf(wv[2], xv.z, fmaf(wv[3], xv.w, acc[r]))));
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < TT + 2; ++r) {
+        const int s = s0 - 2 + r;
+        y1[r * CW + o] = (s >= 0 && s < S) ? rnd<T>(acc[r]) : 0.f;
+      }
+    }
+    __syncthreads();
+    // conv2 (dense over the q or the k channels)
+    for (int o = tid; o < CW; o += nth) {
+      const bool is_q = o < L;
+      const int oo = is_q ? o : o - L, C = is_q ? L : K;
+      const int col0 = is_q ? 0 : L;
+      float acc[TT];
+#pragma unroll
+      for (int r = 0; r < TT; ++r) acc[r] = 0.f;
+      for (int t = 0; t < 3; ++t) {
+        const T* w = (is_q ? wq2 : wk2) + (static_cast<int64_t>(t) * C + oo) * C;
+        for (int c = 0; c < C; c += 4) {
+          float wv[4];
+          ld4(w + c, wv);
+#pragma unroll
+          for (int r = 0; r < TT; ++r) {
+            const float4 yv = *reinterpret_cast<const float4*>(y1 + (r + t) * CW + col0 + c);
+            acc[r] = fmaf(wv[0], yv.x, fmaf(wv[1], yv.y, fmaf(wv[2], yv.z, fmaf(wv[3], yv.w, acc[r]))));
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < TT; ++r) y2[r * CW + o] = rnd<T>(acc[r]);
+    }
+  } else {
+    for (int i = tid; i < TT * CW; i += nth) y2[i] = xs[4 * CW + i];
+  }
+  __syncthreads();
+
+  const int G = Hq / Hkv;
+  const float tval = (qk_norm && temp) ? to_f32(temp[0]) : 1.f;
+  // Epilogue: one thread per (token, head); q heads first, then k heads.
+  for (int i = tid; i < TT * (Hq + Hkv); i += nth) {
+    const int r = i / (Hq + Hkv), hh = i - r * (Hq + Hkv);
+    const int s = s0 + r;
+    if (s >= S) continue;
+    const bool is_k = hh >= Hq;
+    const int head = is_k ? hh - Hq : hh;
+    float* row = y2 + r * CW + (is_k ? L : 0) + head * hd;
+    const float* x0 = xs + (r + 4) * CW;  // pre-conv q0 | k0 of this token
+    if (qk_mean) {
+      for (int d = 0; d < hd; ++d) {
+        float add;
+        if (G == 1) {
+          const int c = head * hd + d;
+          add = rnd<T>(0.5f * rnd<T>(x0[c] + x0[L + c]));
+        } else if (is_k) {
+          float acc = 0.f;
+          for (int hq = 0; hq < Hq; ++hq) acc += x0[hq * hd + d];
+          add = rnd<T>(0.5f * rnd<T>(acc / static_cast<float>(Hq)));
+        } else {
+          float acc = 0.f;
+          for (int hk = 0; hk < Hkv; ++hk) acc += x0[L + hk * hd + d];
+          add = rnd<T>(0.5f * rnd<T>(acc / static_cast<float>(Hkv)));
+        }
+        row[d] = rnd<T>(row[d] + add);
+      }
+    }
+    float fac = 1.f;
+    if (qk_norm) {
+      float ss = 0.f;
+      for (int d = 0; d < hd; ++d) ss = fmaf(row[d], row[d], ss);
+      fac = fmaxf(rnd<T>(sqrtf(ss)), 1e-12f);
+    }
+    T* dst = (is_k ? ko : qo) + ((static_cast<int64_t>(b) * (is_k ? Hkv : Hq) + head) * S + s) * hd;
+    const float* cr = cs + static_cast<int64_t>(s) * cs_rs;
+    const float* sr = sn + static_cast<int64_t>(s) * cs_rs;
+    for (int pp = 0; pp < hd / 2; ++pp) {
+      float x1 = row[2 * pp], x2 = row[2 * pp + 1];
+      if (qk_norm) {
+        x1 = rnd<T>(x1 / fac);
+        x2 = rnd<T>(x2 / fac);
+        if (is_k) {
+          x1 = rnd<T>(x1 * tval);
+          x2 = rnd<T>(x2 * tval);
+        }
+      }
+      if (rope) {
+        const float c = cr[pp], sv = sr[pp];
+        const float o1 = x1 * c - x2 * sv;
+        const float o2 = x1 * sv + x2 * c;
+        x1 = o1;
+        x2 = o2;
+      }
+      dst[2 * pp] = from_f32<T>(x1);
+      dst[2 * pp + 1] = from_f32<T>(x2);
+    }
+  }
+
+  // v with the value shift, written per kv head.
+  for (int i = tid; i < TT * K; i += nth) {
+    const int r = i / K, c = i - r * K;
+    const int s = s0 + r;
+    if (s >= S) continue;
+    T val;
+    if (vshift && c >= K / 2) {
+      val = s > 0 ? xb[static_cast<int64_t>(s - 1) * qkv_rs + L + K + c] : from_f32<T>(0.f);
+    } else {
+      val = xb[static_cast<int64_t>(s) * qkv_rs + L + K + c];
+    }
+    const int j = c / hd, d = c - j * hd;
+    if (flags & HYDRA_CCGQA_V_TRANSPOSED)
+      vo[((static_cast<int64_t>(b) * Hkv + j) * hd + d) * S + s] = val;
+    else
+      vo[((static_cast<int64_t>(b) * Hkv + j) * S + s) * hd + d] = val;
+  }
+}
 
 // ===========================================================================
 // bf16 MFMA variant.
@@ -742,6 +935,31 @@ static int launch_prep_mfma(const void* qkv, int64_t qkv_rs, const void* wq1, co
 }
 
 template <typename T>
+static int launch_prep_vec(const void* qkv, int64_t qkv_rs, const void* wq1, const void* wq2,
+                           const void* wk1, const void* wk2, const void* temp, const float* cs,
+                           const float* sn, int64_t cs_rs, void* qo, void* ko, void* vo, int64_t B,
+                           int64_t S, int64_t Hq, int64_t Hkv, int64_t hd, int flags,
+                           size_t max_lds, hipStream_t st) {
+  constexpr int TT = kPrepVecTT;
+  const int64_t CW = (Hq + Hkv) * hd;
+  const size_t lds = static_cast<size_t>(3 * TT + 6) * CW * sizeof(float);
+  if (lds > max_lds) return -1;
+  auto kern = ccgqa_prep_vec_kernel<T>;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess)
+    return -1;
+  const int threads = static_cast<int>(std::min<int64_t>(256, (CW + 63) / 64 * 64));
+  const dim3 grid(static_cast<unsigned>((S + TT - 1) / TT), static_cast<unsigned>(B));
+  kern<<<grid, threads, lds, st>>>(
+      static_cast<const T*>(qkv), qkv_rs, static_cast<const T*>(wq1), static_cast<const T*>(wq2),
+      static_cast<const T*>(wk1), static_cast<const T*>(wk2), static_cast<const T*>(temp), cs, sn,
+      cs_rs, static_cast<T*>(qo), static_cast<T*>(ko), static_cast<T*>(vo), (int)S, (int)Hq,
+      (int)Hkv, (int)hd, flags);
+  return check_launch("ccgqa_prep_vec_kernel");
+}
+
+template <typename T>
 static int launch_prep_generic(const void* qkv, int64_t qkv_rs, const void* wq1,
                                const void* wq2, const void* wk1, const void* wk2,
                                const void* temp, const float* cs, const float* sn,
@@ -830,7 +1048,25 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
     return fail(HYDRA_ERR_UNSUPPORTED,
                 "ccgqa_prep: MFMA-tiled conv weights need the MFMA path (bf16, head_dim 16/32/64/128, "
                 "16-byte aligned pointers, S % 8 == 0 with V_TRANSPOSED)");
+  int dev = 0, max_lds = 65536;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+    max_lds = 65536;
+  // 4-element weight and LDS steps: every channel count a multiple of 4.
+  const int esz = dtype_size(dtype);
+  const bool vec_ok = hd % 4 == 0 && aligned16(qkv) &&
+                      (!(flags & HYDRA_CCGQA_CONVS) ||
+                       ((reinterpret_cast<uintptr_t>(wq1) | reinterpret_cast<uintptr_t>(wq2) |
+                         reinterpret_cast<uintptr_t>(wk1) | reinterpret_cast<uintptr_t>(wk2)) %
+                            (4 * esz) == 0)) &&
+                      getenv("HYDRA_PREP_GENERIC") == nullptr;
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
+    if (vec_ok) {
+      const int rc = launch_prep_vec<T>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs,
+                                        q_out, k_out, v_out, B, S, Hq, Hkv, hd, flags,
+                                        static_cast<size_t>(max_lds), st);
+      if (rc >= 0) return rc;
+    }
     return launch_prep_generic<T>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs,
                                   q_out, k_out, v_out, B, S, Hq, Hkv, hd, flags, st);
   });

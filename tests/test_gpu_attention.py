@@ -55,15 +55,30 @@ def test_attention_bf16_mfma(cuda, case, causal):
     assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2
 
 
+@pytest.mark.parametrize("generic", [False, True])
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-@pytest.mark.parametrize("case", [(2, 8, 2, 512, 16), (1, 4, 1, 77, 64), (1, 2, 1, 19, 6)])
-def test_attention_generic(cuda, dtype, case):
+@pytest.mark.parametrize("case", [(2, 8, 2, 512, 16), (1, 4, 1, 77, 64), (1, 2, 1, 19, 6),
+                                  (2, 4, 2, 130, 8), (1, 2, 1, 70, 128), (1, 3, 3, 33, 32)])
+def test_attention_valu(cuda, monkeypatch, dtype, case, causal, generic):
+    """The VALU kernels (fp32 / fp16): the key-split kernel (head_dim 8..128)
+    and the one-thread-per-row kernel (odd head dims, or forced), output and
+    LSE."""
     from hydra_amd.attention.backends.ccgqa.ops import attention_forward
 
+    if generic:
+        monkeypatch.setenv("HYDRA_ATTN_GENERIC", "1")
+    B, Hq, Hkv, S, hd = case
     q, k, v = _qkv(*case, seed=3)
-    out, _ = attention_forward(*(t.to(cuda, dtype) for t in (q, k, v)), causal=True)
-    ref = occ.attention(q, k, v, causal=True)
-    assert max_rel_err(out.cpu(), ref) < (1e-5 if dtype == torch.float32 else 2e-2)
+    out, lse = attention_forward(*(t.to(cuda, dtype) for t in (q, k, v)), causal=causal, want_lse=True)
+    ref = occ.attention(q, k, v, causal=causal)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert max_rel_err(out.cpu(), ref) < tol
+    kk = k.repeat_interleave(Hq // Hkv, 1)
+    logits = (q.double() @ kk.double().transpose(-1, -2)) / math.sqrt(hd)
+    if causal:
+        logits = logits.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    assert (lse.cpu().double() - torch.logsumexp(logits, -1)).abs().max().item() < 10 * tol
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

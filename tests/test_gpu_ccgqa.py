@@ -156,3 +156,24 @@ def test_backward_raises(cuda):
     y = m(x.to(cuda).requires_grad_())
     with pytest.raises(NotImplementedError):
         y.sum().backward()
+
+
+def test_prep_generic_kernel_fallback(cuda, monkeypatch):
+    """The one-thread-per-output VALU prep kernel (forced; otherwise taken
+    only by layouts the other kernels reject) against the oracle, fp32."""
+    from hydra_amd.attention.backends.ccgqa.ops import ccgqa_prep, prep_flags
+
+    monkeypatch.setenv("HYDRA_PREP_GENERIC", "1")
+    cfg = occ.CCGQAConfig(dim=512, n_heads=8, n_kv_heads=2, compression_factor=4, max_seq_len=256)
+    g = torch.Generator().manual_seed(32)
+    params = occ.init_params(cfg, g, temperature=1.0)
+    qkv = torch.randn(2, 70, cfg.latent_dim + 2 * cfg.kv_dim, generator=g)
+    ref = occ.prep(params, qkv, cfg)
+    cos, sin = occ.fused_ops.rope_cache(cfg.head_dim, 70)
+    conv = [params[n].to(cuda) for n in ("q_conv.conv1.weight", "q_conv.conv2.weight",
+                                          "k_conv.conv1.weight", "k_conv.conv2.weight")]
+    q, k, v = ccgqa_prep(qkv.to(cuda), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                         prep_flags(True, True, True, True, True), *conv,
+                         temperature=params["key_temperature"].to(cuda), cos=cos.to(cuda), sin=sin.to(cuda))
+    for got, want in zip((q, k, v), ref):
+        assert max_rel_err(got.cpu(), want) < 1e-5
