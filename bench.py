@@ -687,6 +687,46 @@ def measured_traffic(kernel_key):
         return None
 
 
+def rocpd_summary(paths, kernel_regex=None):
+    """Per-kernel means from rocprofv3 result databases (rocpd SQLite): the
+    number of dispatches, the mean duration, and the mean of each collected
+    counter per dispatch.  Prints one block per kernel, for the profile
+    summaries committed under profiles/."""
+    import collections
+    import re
+    import sqlite3
+
+    pat = re.compile(kernel_regex) if kernel_regex else None
+    short = lambda n: re.sub(r"\(.*", "", (n or "").replace("(anonymous namespace)", "anon"))[:120]
+    dur = collections.defaultdict(list)
+    ctr = collections.defaultdict(lambda: collections.defaultdict(list))
+    for path in paths:
+        con = sqlite3.connect(path)
+        views = {r[0] for r in con.execute("select name from sqlite_master where type in ('table','view')")}
+        if "kernels" in views:
+            cols = [r[1] for r in con.execute("pragma table_info(kernels)")]
+            for row in con.execute("select * from kernels"):
+                d = dict(zip(cols, row))
+                name = short(d.get("name") or d.get("kernel_name"))
+                if pat is None or pat.search(name):
+                    dur[name].append((d["end"] - d["start"]) / 1000.0)
+        if "counters_collection" in views:
+            cols = [r[1] for r in con.execute("pragma table_info(counters_collection)")]
+            for row in con.execute("select * from counters_collection"):
+                d = dict(zip(cols, row))
+                name = short(d.get("kernel_name") or d.get("name"))
+                if pat is None or pat.search(name):
+                    ctr[name][d["counter_name"]].append(d["value"])
+    for name in sorted(set(dur) | set(ctr), key=lambda n: -sum(dur.get(n, [0]))):
+        v = dur.get(name, [])
+        head = f"{name}: {len(v)} dispatches"
+        if v:
+            head += f", mean {sum(v) / len(v):.2f} us"
+        print(head)
+        for cn, vals in sorted(ctr[name].items()):
+            print(f"    {cn:34s} {sum(vals) / len(vals):.6g} per dispatch (n={len(vals)})")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -697,7 +737,13 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 model forward")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 512 MiB device copy (traffic-counter calibration)")
+    ap.add_argument("--rocpd-summary", nargs="+", metavar="DB",
+                    help="summarise rocprofv3 result databases (no GPU work) and exit")
+    ap.add_argument("--kernel-regex", default=None, help="with --rocpd-summary: kernels to keep")
     args = ap.parse_args()
+    if args.rocpd_summary:
+        rocpd_summary(args.rocpd_summary, args.kernel_regex)
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the hot path has no multi-GPU "
               "component); run with --gpus 1", file=sys.stderr)

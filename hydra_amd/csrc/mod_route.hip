@@ -13,6 +13,7 @@
 // through LDS, so a 4096-key row needs 10 barriers instead of 78.
 #include "common.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace hydra {
@@ -26,6 +27,12 @@ __device__ __forceinline__ uint32_t score_key_asc(float f) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN
   if (u == 0x80000000u) u = 0u;                               // -0.0 -> +0.0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off)));
+  return v;
 }
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
@@ -181,6 +188,248 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_kernel(
       m &= m - 1;
       if (pos < k) orow[pos] = static_cast<int64_t>(w * 32 + b);
       ++pos;
+    }
+  }
+}
+
+// ---- bucketed top-k (rows of up to kBucketMaxL keys) ---------------------
+// R workgroups per row (R = ceil(L / 1024)), each running:
+//  1. keys: desc(score) = ~score_key_asc(score) (ascending desc <-> value-
+//     descending, NaN first, -0.0 == +0.0); histogram of its top kBinBits
+//     bits in LDS (atomic adds; each key keeps its slot within its bin);
+//  2. exclusive scan of the histogram -> the first position of every bin in
+//     the value-descending order; the largest bin, and the bin holding
+//     position k-1 (the threshold bin);
+//  3. every key written to its bin's segment as the 64-bit composite
+//     (desc << 32) | index;
+//  4. the rank of a key = first position of its bin + the keys of its bin
+//     with a smaller composite (a larger score, or an equal score at a lower
+//     index) -- exact, the order of a stable descending sort.  Keys below the
+//     threshold bin are selected, keys above are not, keys in it are
+//     selected when their rank is < k; the workgroup ranks the selected keys
+//     of its 1024-key part and writes idx_desc[rank] = index;
+//  5. the selection bitmap of the whole row (only the threshold bin needs
+//     ranks), prefix counts over its words, then the mask and the ascending
+//     list entries of the workgroup's part.
+// Steps 1-3 are repeated by each of a row's workgroups (cheap); the ranks,
+// the expensive part, are split between them.  Bins are small for real
+// score distributions (tens of keys for N(0, 1) scores at L = 4096); when the
+// largest bin exceeds kBucketMaxBin keys (e.g. many equal scores) the row's
+// first workgroup sorts the whole row with the bitonic sort instead and the
+// others leave, so the cost stays bounded.
+constexpr int kBinBits = 14;
+constexpr int kBins = 1 << kBinBits;
+// Bins live in LDS with 4 pad words after every 16 (kBinWords in all), so
+// the scan's per-thread runs of 16 bins (16-byte reads, 80 bytes apart) fall
+// in distinct banks.
+constexpr int kBinWords = kBins + kBins / 4;
+__device__ __forceinline__ uint32_t bin_slot(uint32_t b) { return b + 4 * (b >> 4); }
+constexpr int kBucketMaxL = 8192;
+constexpr int kBucketMaxBin = 512;
+
+// Rank of composite `me` within the bin segment keys[b0, b1): b0 + the keys
+// smaller than it (8 independent LDS reads in flight per step; the tail
+// reads clamp to the segment's last key and count 0).
+__device__ __forceinline__ int bin_rank(const uint64_t* keys, int b0, int b1, uint64_t me) {
+  int r = b0;
+  for (int j = b0; j < b1; j += 8) {
+    uint64_t kv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) kv[u] = keys[min(j + u, b1 - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r += (j + u < b1 && kv[u] < me) ? 1 : 0;
+  }
+  return r;
+}
+
+template <typename S, int EPT>
+__global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
+    const S* __restrict__ scores, int L, int64_t s_rs, int k, int R,
+    int64_t* __restrict__ idx_desc, int64_t* __restrict__ idx_sorted,
+    void* __restrict__ mask, int mask_dtype) {
+  constexpr int P = EPT * kTopkThreads;
+  extern __shared__ unsigned char smem[];
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);                         // [P] composites
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + sizeof(uint64_t) * P);  // [kBinWords]
+  uint32_t* bits = hist + kBinWords;                                          // [L/32] selection
+  uint32_t* wpre = bits + P / 32;                                             // [L/32] word prefixes
+  __shared__ int wave_tot[kTopkThreads / 64];
+  __shared__ int wave_max[kTopkThreads / 64];
+  __shared__ int thr[2];  // threshold bin, its first position
+
+  const int row = blockIdx.x / R, part = blockIdx.x - row * R;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const S* sr = scores + static_cast<int64_t>(row) * s_rs;
+  for (int i = tid; i < kBinWords; i += kTopkThreads) hist[i] = 0u;
+  const int nwords = (L + 31) / 32;
+  for (int i = tid; i < nwords; i += kTopkThreads) bits[i] = 0u;
+  __syncthreads();
+
+  // 1. keys and histogram; element e of this thread is i = tid + 1024 e
+  uint32_t dk[EPT], slot[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = tid + kTopkThreads * e;
+    dk[e] = 0u;
+    slot[e] = 0u;
+    if (i < L) {
+      dk[e] = ~score_key_asc(to_f32(sr[i]));
+      slot[e] = atomicAdd(&hist[bin_slot(dk[e] >> (32 - kBinBits))], 1u);
+    }
+  }
+  __syncthreads();
+
+  // 2. exclusive scan of the bins: thread t owns bins [16 t, 16 t + 16)
+  constexpr int BPT = kBins / kTopkThreads;
+  static_assert(BPT == 16, "a thread's bins are one padded run of 16");
+  uint32_t hv[BPT];
+  uint4* hrun = reinterpret_cast<uint4*>(hist + 20 * tid);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 w = hrun[q];
+    hv[4 * q] = w.x; hv[4 * q + 1] = w.y; hv[4 * q + 2] = w.z; hv[4 * q + 3] = w.w;
+  }
+  int cnt = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    cnt += static_cast<int>(hv[j]);
+    mx = max(mx, static_cast<int>(hv[j]));
+  }
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int n = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += n;
+  }
+  mx = static_cast<int>(wave_max_u(static_cast<uint32_t>(mx)));
+  if (lane == 63) wave_tot[wave] = incl;
+  if (lane == 0) wave_max[wave] = mx;
+  __syncthreads();
+  int base = 0, gmx = 0;
+  for (int w = 0; w < kTopkThreads / 64; ++w) {
+    if (w < wave) base += wave_tot[w];
+    gmx = max(gmx, wave_max[w]);
+  }
+  if (gmx > kBucketMaxBin) {
+    // Degenerate bins: the row's first workgroup sorts the whole row (ties
+    // by index, as above) and writes every output; the others leave.
+    if (part != 0) return;
+    uint64_t v[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = EPT * tid + j;
+      v[j] = ~uint64_t(0);
+      if (i < L) v[j] = (static_cast<uint64_t>(~score_key_asc(to_f32(sr[i]))) << 32) | static_cast<uint32_t>(i);
+    }
+    bitonic_sort<EPT>(v, keys, tid);  // leaves the sorted row in keys[]
+    for (int j = tid; j < k; j += kTopkThreads) {
+      const uint32_t i = static_cast<uint32_t>(keys[j] & 0xffffffffu);
+      if (idx_desc) idx_desc[static_cast<int64_t>(row) * k + j] = static_cast<int64_t>(i);
+      atomicOr(&bits[i >> 5], 1u << (i & 31));
+    }
+  } else {
+    int pos = base + incl - cnt;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int c = static_cast<int>(hv[j]);
+      if (pos <= k - 1 && k - 1 < pos + c) {  // exactly one bin holds position k-1
+        thr[0] = tid * BPT + j;
+        thr[1] = pos;
+      }
+      hv[j] = static_cast<uint32_t>(pos);  // first position of the bin
+      pos += c;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hrun[q] = make_uint4(hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]);
+    __syncthreads();
+    // 3. composites into their bins' segments
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = tid + kTopkThreads * e;
+      if (i < L)
+        keys[hist[bin_slot(dk[e] >> (32 - kBinBits))] + slot[e]] =
+            (static_cast<uint64_t>(dk[e]) << 32) | static_cast<uint32_t>(i);
+    }
+    __syncthreads();
+    const uint32_t tb = static_cast<uint32_t>(thr[0]);
+    const int tb0 = thr[1];
+    const int tb1 = tb + 1 < kBins ? static_cast<int>(hist[bin_slot(tb + 1)]) : L;
+    // 4. ranks of this part's selected keys (element tid + 1024 * part)
+    {
+      const int e = part;
+      const int i = tid + kTopkThreads * e;
+      uint32_t d = 0u;
+#pragma unroll
+      for (int x = 0; x < EPT; ++x)
+        if (x == e) d = dk[x];
+      const uint32_t b = d >> (32 - kBinBits);
+      if (i < L && b <= tb) {
+        const int b0 = static_cast<int>(hist[bin_slot(b)]);
+        const int b1 = b == tb ? tb1 : static_cast<int>(hist[bin_slot(b + 1)]);
+        const int r = bin_rank(keys, b0, b1, (static_cast<uint64_t>(d) << 32) | static_cast<uint32_t>(i));
+        if (r < k && idx_desc) idx_desc[static_cast<int64_t>(row) * k + r] = static_cast<int64_t>(i);
+      }
+    }
+    // 5. the whole row's selection: every key below the threshold bin (a
+    // wave's 64 consecutive keys -> two bitmap words by ballot, one plain
+    // store each), then the threshold bin's keys of rank < k
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = tid + kTopkThreads * e;
+      const uint64_t sel = __ballot(i < L && (dk[e] >> (32 - kBinBits)) < tb);
+      const int w0 = (kTopkThreads * e + 64 * wave) >> 5;
+      if (lane == 0 && w0 < nwords) bits[w0] = static_cast<uint32_t>(sel);
+      if (lane == 0 && w0 + 1 < nwords) bits[w0 + 1] = static_cast<uint32_t>(sel >> 32);
+    }
+    __syncthreads();
+    for (int p = tb0 + tid; p < tb1; p += kTopkThreads) {
+      const uint64_t me = keys[p];
+      if (bin_rank(keys, tb0, tb1, me) < k) {
+        const uint32_t i = static_cast<uint32_t>(me & 0xffffffffu);
+        atomicOr(&bits[i >> 5], 1u << (i & 31));
+      }
+    }
+  }
+  __syncthreads();
+
+  // mask and ascending list of this part: elements [1024 part, 1024 part + 1024)
+  const int i0 = kTopkThreads * part;
+  if (mask) {
+    const int64_t mrow = static_cast<int64_t>(row) * L;
+    const int hi = gmx > kBucketMaxBin ? L : min(L, i0 + kTopkThreads);
+    for (int i = (gmx > kBucketMaxBin ? 0 : i0) + tid; i < hi; i += kTopkThreads) {
+      const float v = (bits[i >> 5] >> (i & 31)) & 1u ? 1.f : 0.f;
+      switch (mask_dtype) {
+        case HYDRA_F32: static_cast<float*>(mask)[mrow + i] = v; break;
+        case HYDRA_BF16: static_cast<bf16*>(mask)[mrow + i] = from_f32<bf16>(v); break;
+        default: static_cast<f16*>(mask)[mrow + i] = from_f32<f16>(v); break;
+      }
+    }
+  }
+  if (!idx_sorted) return;
+  // word prefixes: exclusive scan of the popcounts of the row's words
+  // (nwords <= 256 < 1024: thread t owns word t)
+  const int pc = tid < nwords ? __popc(bits[tid]) : 0;
+  int pincl = pc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int n = __shfl_up(pincl, off, 64);
+    if (lane >= off) pincl += n;
+  }
+  __syncthreads();  // wave_tot reuse
+  if (lane == 63) wave_tot[wave] = pincl;
+  __syncthreads();
+  int pbase = 0;
+  for (int w = 0; w < wave; ++w) pbase += wave_tot[w];
+  if (tid < nwords) wpre[tid] = static_cast<uint32_t>(pbase + pincl - pc);
+  __syncthreads();
+  int64_t* orow = idx_sorted + static_cast<int64_t>(row) * k;
+  const int hi = gmx > kBucketMaxBin ? L : min(L, i0 + kTopkThreads);
+  for (int i = (gmx > kBucketMaxBin ? 0 : i0) + tid; i < hi; i += kTopkThreads) {
+    const uint32_t wbits = bits[i >> 5];
+    if ((wbits >> (i & 31)) & 1u) {
+      const int o = static_cast<int>(wpre[i >> 5]) + __popc(wbits & ((1u << (i & 31)) - 1u));
+      if (o < k) orow[o] = static_cast<int64_t>(i);
     }
   }
 }
@@ -348,7 +597,10 @@ extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t 
   int ept = 1;
   while (ept * kTopkThreads < L) ept <<= 1;
   const int P = ept * kTopkThreads;
-  const size_t lds = sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);
+  const bool bucket = L <= kBucketMaxL && getenv("HYDRA_TOPK_BITONIC") == nullptr;
+  const size_t lds = bucket ? sizeof(uint64_t) * P + sizeof(uint32_t) * kBinWords + 2 * sizeof(uint32_t) * (P / 32)
+                            : sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);
+  const int R = static_cast<int>((L + kTopkThreads - 1) / kTopkThreads);  // bucket kernel: parts per row
   if (lds + 1024 > static_cast<size_t>(max_lds_per_block()))
     return fail(HYDRA_ERR_UNSUPPORTED, "mod_topk: row does not fit in LDS on this device");
   auto st = static_cast<hipStream_t>(stream);
@@ -356,6 +608,15 @@ extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t 
   auto go = [&](auto s_tag, auto e_tag) {
     using ST = decltype(s_tag);
     constexpr int E = decltype(e_tag)::value;
+    if (bucket) {
+      auto kern = mod_topk_bucket_kernel<ST, (E < 8 ? E : 8)>;
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(lds)) != hipSuccess)
+        return false;
+      kern<<<dim3(static_cast<unsigned>(B * R)), kTopkThreads, lds, st>>>(
+          static_cast<const ST*>(scores), (int)L, s_rs, (int)k, R, idx_desc, idx_sorted, mask, mask_dtype);
+      return true;
+    }
     auto kern = mod_topk_kernel<ST, E>;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess)

@@ -34,11 +34,36 @@ def test_topk_c4(cuda):
     _check_topk(s, omod.router_k(4096, 0.75), cuda)
 
 
+@pytest.mark.parametrize("bitonic", [False, True])
 @pytest.mark.parametrize("B,L,k", [(1, 1, 1), (3, 64, 1), (3, 64, 64), (2, 1000, 999),
-                                   (2, 16384, 12288), (5, 333, 100), (70, 128, 96)])
-def test_topk_sizes(cuda, B, L, k):
+                                   (2, 16384, 12288), (5, 333, 100), (70, 128, 96),
+                                   (3, 8192, 6144), (2, 8193, 7000), (4, 4096, 1)])
+def test_topk_sizes(cuda, monkeypatch, B, L, k, bitonic):
+    """Rows up to 8192 take the bucketed rank kernel (forced bitonic sort as
+    well); longer rows the bitonic kernel."""
+    if bitonic:
+        monkeypatch.setenv("HYDRA_TOPK_BITONIC", "1")
     g = torch.Generator().manual_seed(L + k)
     _check_topk(omod.make_tied_logits(B, L, 0.05, g), k, cuda)
+
+
+@pytest.mark.parametrize("pattern", ["all_equal", "two_values", "one_bin_wide", "ramp"])
+def test_topk_degenerate_bins(cuda, pattern):
+    """Score sets that fill one histogram bin (all equal, two values, many
+    distinct values sharing their top bits) take the bucketed kernel's
+    whole-row sort; a ramp spreads over many bins."""
+    g = torch.Generator().manual_seed(11)
+    L = 4096
+    if pattern == "all_equal":
+        s = torch.full((3, L), 0.25)
+    elif pattern == "two_values":
+        s = torch.where(torch.rand(3, L, generator=g) > 0.5, 1.0, -1.0)
+    elif pattern == "one_bin_wide":
+        s = 1.0 + torch.rand(3, L, generator=g) * 1e-3  # same top 14 key bits
+    else:
+        s = torch.linspace(-5, 5, L).repeat(3, 1)
+    for k in (1, 1000, 3072, L):
+        _check_topk(s, k, cuda)
 
 
 def test_topk_special_values(cuda):
