@@ -51,7 +51,7 @@ def test_rms_norm_strided_rows(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(8, 12, 2048, 64), (2, 8, 512, 16), (1, 3, 17, 6), (2, 2, 5, 128)])
+@pytest.mark.parametrize("shape", [(8, 12, 2048, 64), (2, 8, 512, 16), (1, 3, 17, 6), (2, 2, 5, 128), (1, 18, 33, 32)])
 def test_rope(cuda, dtype, shape):
     from hydra_amd.kernels import fused_rope
 
@@ -63,6 +63,22 @@ def test_rope(cuda, dtype, shape):
     assert y.dtype == dtype and y.shape == x.shape and y.is_contiguous()
     ref = ofo.rope(x.float(), cos, sin)
     assert max_rel_err(y, ref) < TOL[dtype]
+
+
+def test_rope_cache_row_stride_not_vector_aligned(cuda):
+    """cos/sin rows 35 elements apart: the per-element cos/sin loads."""
+    from hydra_amd.kernels import fused_rope
+
+    g = _gen(5)
+    x = torch.randn(2, 12, 40, 64, generator=g).to(torch.bfloat16)
+    cos, sin = ofo.rope_cache(64, 40)
+    cw = torch.zeros(40, 35)
+    sw = torch.zeros(40, 35)
+    cw[:, :32], sw[:, :32] = cos[0, 0], sin[0, 0]
+    cd, sd = cw.to(cuda)[:, :32], sw.to(cuda)[:, :32]
+    assert cd.stride(0) == 35
+    y = fused_rope(x.to(cuda), cd, sd).cpu()
+    assert max_rel_err(y, ofo.rope(x.float(), cos, sin)) < 2e-2
 
 
 def test_rope_strided_view_and_2d_cache(cuda):
