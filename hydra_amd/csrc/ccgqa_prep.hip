@@ -616,11 +616,16 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
   constexpr int CSR = HD / 2 + 2;
   float* CSl = reinterpret_cast<float*>(Y1 + (TT + 2) * RS);
   float* SNl = CSl + TT * CSR;
-  uint16_t* QA = reinterpret_cast<uint16_t*>(SNl + TT * CSR);  // bf16 [TT][NQA][HD]
+  uint16_t* QA = reinterpret_cast<uint16_t*>(SNl + TT * CSR);  // bf16 [TT][QAS]
   // v columns of tokens [s0-1, s0+TT), row r <-> token s0 - 1 + r (the
   // value shift reads the previous token), rows padded by 8 elements
   const int VR = K + 8;
-  uint16_t* Vs = QA + TT * NQA * HD;
+  // QK-mean term rows padded by 8 elements: with NQA*HD a multiple of 64
+  // the epilogue's reads of 32 consecutive tokens would share one bank.
+  const int QAS = NQA * HD + 8;
+  uint16_t* Vs = QA + TT * QAS;
+  // count of waves done with the QK-mean terms (see the conv2 phase)
+  int* qa_done = reinterpret_cast<int*>(Vs + ((TT + 1) * VR + 7) / 8 * 8);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, hf = lane >> 5;
   const int b = blockIdx.y;
@@ -637,76 +642,137 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
   const int wstep = tiled ? 512 : 16;  // elements between k-steps
   const bf16* xb = qkv + static_cast<int64_t>(b) * S * qkv_rs;
 
-  // ---- stage q0|k0 rows, RoPE angles ---------------------------------------
-  const int cw8 = CW / 8;
-  for (int i = tid; i < (TT + 4) * cw8; i += kPrepThreads) {
-    const int r = i / cw8, c = (i - r * cw8) * 8;
-    const int s = s0 - 4 + r;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (s >= 0 && s < S) v = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + c);
-    *reinterpret_cast<uint4*>(X + r * RS + c) = v;
-  }
-  for (int i = tid; i < (TT + 1) * (K / 8); i += kPrepThreads) {
-    const int r = i / (K / 8), c = (i - r * (K / 8)) * 8;
-    const int s = s0 - 1 + r;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (s >= 0 && s < S) v = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + c);
-    *reinterpret_cast<uint4*>(Vs + r * VR + c) = v;
-  }
-  if (rope) {
+  // ---- stage q0|k0 rows, v rows, RoPE angles --------------------------------
+  if (tid == 0) *qa_done = 0;
+  // Each round issues all of a thread's 16-byte global loads of the three
+  // regions (up to 8 + 2 + 2) before it writes any of them to LDS, so the
+  // whole tile is in flight at once; (row, chunk) advance incrementally, with
+  // no division per item.
+  {
+    constexpr int KX = 8, KV = 2, KC = 2;
     constexpr int Q4 = HD / 8;  // float4 chunks per cos (or sin) row
-    for (int i = tid; i < 2 * TT * Q4; i += kPrepThreads) {
-      const int which = i / (TT * Q4), rem = i - which * (TT * Q4);
-      const int r = rem / Q4, c4 = (rem - r * Q4) * 4;
-      const int s = s0 + r;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (s < S) v = *reinterpret_cast<const float4*>((which ? sn : cs) + static_cast<int64_t>(s) * cs_rs + c4);
-      float* d = (which ? SNl : CSl) + r * CSR + c4;  // 8-byte aligned rows
-      *reinterpret_cast<float2*>(d) = make_float2(v.x, v.y);
-      *reinterpret_cast<float2*>(d + 2) = make_float2(v.z, v.w);
+    const int cw8 = CW / 8, k8 = K / 8;
+    const int nx = (TT + 4) * cw8, nv = (TT + 1) * k8, nc = rope ? 2 * TT * Q4 : 0;
+    const int xq = kPrepThreads / cw8, xm = kPrepThreads - xq * cw8;
+    const int vq = kPrepThreads / k8, vm = kPrepThreads - vq * k8;
+    int xr = tid / cw8, xc = tid - xr * cw8;
+    int vr = tid / k8, vc = tid - vr * k8;
+    for (int round = 0;; ++round) {
+      const int bx = round * KX * kPrepThreads, bv = round * KV * kPrepThreads,
+                bc = round * KC * kPrepThreads;
+      if (bx >= nx && bv >= nv && bc >= nc) break;
+      uint4 xval[KX], vval[KV], cval[KC];
+      int xrr[KX], xcc[KX], vrr[KV], vcc[KV];
+#pragma unroll
+      for (int j = 0; j < KX; ++j) {
+        xrr[j] = xr;
+        xcc[j] = xc;
+        const int s = s0 - 4 + xr;
+        xval[j] = make_uint4(0, 0, 0, 0);
+        if (bx + j * kPrepThreads + tid < nx && s >= 0 && s < S)
+          xval[j] = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + 8 * xc);
+        xr += xq;
+        xc += xm;
+        if (xc >= cw8) { xc -= cw8; ++xr; }
+      }
+#pragma unroll
+      for (int j = 0; j < KV; ++j) {
+        vrr[j] = vr;
+        vcc[j] = vc;
+        const int s = s0 - 1 + vr;
+        vval[j] = make_uint4(0, 0, 0, 0);
+        if (bv + j * kPrepThreads + tid < nv && s >= 0 && s < S)
+          vval[j] = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(s) * qkv_rs + L + K + 8 * vc);
+        vr += vq;
+        vc += vm;
+        if (vc >= k8) { vc -= k8; ++vr; }
+      }
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const int i = bc + j * kPrepThreads + tid;
+        const int which = i / (TT * Q4), rem = i - which * (TT * Q4);
+        const int r = rem / Q4, c4 = (rem - r * Q4) * 4;
+        const int s = s0 + r;
+        cval[j] = make_uint4(0, 0, 0, 0);
+        if (i < nc && s < S)
+          cval[j] = *reinterpret_cast<const uint4*>((which ? sn : cs) + static_cast<int64_t>(s) * cs_rs + c4);
+      }
+#pragma unroll
+      for (int j = 0; j < KX; ++j)
+        if (bx + j * kPrepThreads + tid < nx)
+          *reinterpret_cast<uint4*>(X + xrr[j] * RS + 8 * xcc[j]) = xval[j];
+#pragma unroll
+      for (int j = 0; j < KV; ++j)
+        if (bv + j * kPrepThreads + tid < nv)
+          *reinterpret_cast<uint4*>(Vs + vrr[j] * VR + 8 * vcc[j]) = vval[j];
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const int i = bc + j * kPrepThreads + tid;
+        if (i < nc) {
+          const int which = i / (TT * Q4), rem = i - which * (TT * Q4);
+          const int r = rem / Q4, c4 = (rem - r * Q4) * 4;
+          float* d = (which ? SNl : CSl) + r * CSR + c4;  // 8-byte aligned rows
+          *reinterpret_cast<uint2*>(d) = make_uint2(cval[j].x, cval[j].y);
+          *reinterpret_cast<uint2*>(d + 2) = make_uint2(cval[j].z, cval[j].w);
+        }
+      }
     }
   }
   __syncthreads();
 
-  // ---- side work: QK-mean terms into QA, and v (value shift) to global ----
+  // ---- side work: QK-mean terms into QA ---------------------------------------
   // Shared by the waves [hw0, 8); they run it while the others still have
   // MFMA tasks, so it stays off the critical path.
-  auto side_work = [&](int hw0) {
+  auto qa_work = [&](int hw0) {
+    if (!qk_mean) return;
     const int hl = (wave - hw0) * 64 + lane, nhl = (kPrepThreads / 64 - hw0) * 64;
-    if (qk_mean) {
-      constexpr int C8 = HD / 8;
-      for (int it = hl; it < TT * NQA * C8; it += nhl) {
-        const int r = it / (NQA * C8), rem = it - r * (NQA * C8);
-        const int q = rem / C8, c8 = (rem - q * C8) * 8;
-        const bf16* x0 = reinterpret_cast<const bf16*>(X + (r + 4) * RS);
-        float add[8];
-        if (G == 1) {
-          float a[8], c[8];
-          load16<bf16>(x0 + q * HD + c8, a);
-          load16<bf16>(x0 + L + q * HD + c8, c);
+    constexpr int C8 = HD / 8;
+    const float inv_q = 1.f / static_cast<float>(Hq), inv_k = 1.f / static_cast<float>(Hkv);
+    // items ordered [term q][token r][chunk c8]: a wave's lanes share q, so
+    // the head loop below does not diverge
+    for (int it = hl; it < TT * NQA * C8; it += nhl) {
+      const int q = it / (TT * C8), rem = it - q * (TT * C8);
+      const int r = rem / C8, c8 = (rem - r * C8) * 8;
+      const bf16* x0 = reinterpret_cast<const bf16*>(X + (r + 4) * RS);
+      float sum[8];
+      float scale;
+      if (G == 1) {
+        // (q0_h + k0_h) / 2
+        float c[8];
+        load16<bf16>(x0 + q * HD + c8, sum);
+        load16<bf16>(x0 + L + q * HD + c8, c);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(a[e] + c[e]));
-        } else {
-          // term 0 (for q heads): mean of the k heads; term 1: of the q heads
-          const int nh = q ? Hq : Hkv;
-          const bf16* src = x0 + (q ? 0 : L) + c8;
-          float sum[8];
-          load16<bf16>(src, sum);
-          for (int hx = 1; hx < nh; ++hx) {
-            float a[8];
-            load16<bf16>(src + hx * HD, a);
+        for (int e = 0; e < 8; ++e) sum[e] += c[e];
+        scale = 1.f;
+      } else {
+        // term 0 (for q heads): mean of the k heads; term 1: of the q heads
+        const int nh = q ? Hq : Hkv;
+        const bf16* src = x0 + (q ? 0 : L) + c8;
+        load16<bf16>(src, sum);
+#pragma unroll 4
+        for (int hx = 1; hx < nh; ++hx) {
+          float a[8];
+          load16<bf16>(src + hx * HD, a);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sum[e] += a[e];
-          }
-          const float inv = 1.f / static_cast<float>(nh);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) add[e] = rnd<bf16>(0.5f * rnd<bf16>(sum[e] * inv));
+          for (int e = 0; e < 8; ++e) sum[e] += a[e];
         }
-        store16<bf16>(reinterpret_cast<bf16*>(QA + (r * NQA + q) * HD + c8), add);
+        scale = q ? inv_q : inv_k;
       }
+      // rnd(0.5 * rnd(mean)), two values per conversion
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t m = pack2<bf16>(sum[e] * scale, sum[e + 1] * scale);
+        w[e / 2] = pack2<bf16>(0.5f * __uint_as_float(m << 16), 0.5f * __uint_as_float(m & 0xffff0000u));
+      }
+      *reinterpret_cast<uint4*>(QA + r * QAS + q * HD + c8) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    // v from the staged rows: channels of the second half take the previous
-    // token with the value shift (row r of token s, row r+1 otherwise)
+  };
+  // v from the staged rows to global: channels of the second half take the
+  // previous token with the value shift (row r of token s, row r+1
+  // otherwise).  Shared by the waves [hw0, 8).
+  auto v_work = [&](int hw0) {
+    const int hl = (wave - hw0) * 64 + lane, nhl = (kPrepThreads / 64 - hw0) * 64;
     if (flags & HYDRA_CCGQA_V_TRANSPOSED) {
       // v^T [B, Hkv, hd, S]: 8 consecutive tokens of one channel per
       // 16-byte store
@@ -737,13 +803,84 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
       }
     }
   };
+  const float tval = (qk_norm && temp) ? to_f32(temp[0]) : 1.f;
 
-  if (convs) {
-    // ---- conv1 on MFMA ------------------------------------------------------
-    // Output row i in [0, TT+2) <-> token s0-2+i reads X rows i..i+2.  The
-    // rows are covered by NT+1 token tiles; the last holds the two rows past
-    // TT (its other lanes read clamped rows and are discarded).  Rows of
-    // tokens < 0 come out 0 (their X rows are 0): conv2's causal padding.
+  if (!convs) {
+    // ---- no convs: QK-mean terms and v, then the row epilogue over X --------
+    qa_work(0);
+    v_work(0);
+    __syncthreads();
+    // HD/8 lanes per (token, head) row, 8 channels each; a wave covers 8
+    // rows, i.e. the heads of consecutive tokens, so RoPE angles are shared
+    // reads and every row leaves as one contiguous 2*HD-byte store.
+    // Roundings follow the reference: the QK-mean sum, the norm, the
+    // normalised vector, the temperature product.
+    uint16_t* Y2 = X + 4 * RS;  // row r <-> token s0 + r
+    constexpr int LPR = HD / 8;
+    const int nheads = Hq + Hkv;
+    const int rows = TT * nheads;
+    for (int base = 0; base < rows * LPR; base += kPrepThreads) {
+      const int i = base + tid;
+      const bool live = i < rows * LPR;
+      const int row = live ? i / LPR : 0, c8 = (i % LPR) * 8;
+      const int r = row / nheads, hh = row - r * nheads;
+      const int s = s0 + r;
+      const bool is_k = hh >= Hq;
+      const int head = is_k ? hh - Hq : hh;
+      float v[8];
+      load16<bf16>(reinterpret_cast<const bf16*>(Y2 + r * RS + (is_k ? L : 0) + head * HD + c8), v);
+      if (qk_mean) {
+        float add[8];
+        const int q = G == 1 ? head : (is_k ? 1 : 0);
+        load16<bf16>(reinterpret_cast<const bf16*>(QA + r * QAS + q * HD + c8), add);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += add[e];
+        rnd8(v);
+      }
+      if (qk_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+        ss = wave_sum<LPR>(ss);
+        const float rinv = 1.f / fmaxf(rnd<bf16>(__builtin_sqrtf(ss)), 1e-12f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] *= rinv;
+        rnd8(v);
+        if (is_k) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] *= tval;
+          rnd8(v);
+        }
+      }
+      if (rope) {
+        const float* cr = CSl + r * CSR + c8 / 2;
+        const float* sr = SNl + r * CSR + c8 / 2;
+#pragma unroll
+        for (int p2 = 0; p2 < 2; ++p2) {
+          const float2 cv = *reinterpret_cast<const float2*>(cr + 2 * p2);
+          const float2 sv = *reinterpret_cast<const float2*>(sr + 2 * p2);
+          const float x0 = v[4 * p2 + 0], x1 = v[4 * p2 + 1], x2 = v[4 * p2 + 2], x3 = v[4 * p2 + 3];
+          v[4 * p2 + 0] = x0 * cv.x - x1 * sv.x;
+          v[4 * p2 + 1] = x0 * sv.x + x1 * cv.x;
+          v[4 * p2 + 2] = x2 * cv.y - x3 * sv.y;
+          v[4 * p2 + 3] = x2 * sv.y + x3 * cv.y;
+        }
+      }
+      if (live && s < S) {
+        bf16* dst = (is_k ? ko : qo) +
+                    ((static_cast<int64_t>(b) * (is_k ? Hkv : Hq) + head) * S + s) * HD + c8;
+        store16<bf16>(dst, v);
+      }
+    }
+    return;
+  }
+
+  // ---- conv1 on MFMA ----------------------------------------------------------
+  // Output row i in [0, TT+2) <-> token s0-2+i reads X rows i..i+2.  The
+  // rows are covered by NT+1 token tiles; the last holds the two rows past
+  // TT (its other lanes read clamped rows and are discarded).  Rows of
+  // tokens < 0 come out 0 (their X rows are 0): conv2's causal padding.
+  {
     constexpr int NT1 = NT + 1;
     const int nm1 = CW / 32;
     for (int mt = wave; mt < nm1; mt += kPrepThreads / 64) {
@@ -778,119 +915,186 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
         }
       }
     }
-    // waves with one m-tile fewer take the side work
+    // With at least one conv2 task per wave, the waves with one conv1
+    // m-tile fewer compute the QK-mean terms here; otherwise the waves
+    // without a conv2 task do it during conv2.
+    const int HPT2 = HD >= 32 ? 1 : 32 / HD;
     const int extra = nm1 % (kPrepThreads / 64);
-    const int hw0 = extra == 0 ? 0 : extra;
-    if (wave >= hw0) side_work(hw0);
-  } else {
-    side_work(0);
+    if ((Hq + Hkv) / HPT2 >= kPrepThreads / 64 && wave >= extra) qa_work(extra);
   }
   __syncthreads();
 
-  // ---- conv2 on MFMA: one head (HD/32 m-tiles) x all token tiles per task,
-  // so each weight fragment is read once per workgroup and each token-row
-  // fragment feeds HD/32 MFMAs.  Output token s0+32j+n, tap t reads Y1 row
-  // 32j+n+t.  Rounded to bf16 into Y2, which reuses X's rows (conv1 and the
-  // side work are done with X).  Without convs, Y2 is X's rows 4.. as is.
-  uint16_t* Y2 = convs ? X : X + 4 * RS;  // row r <-> token s0 + r
-  if (convs) {
-    // A task covers 32 * MT output channels: one head when HD >= 32, one
-    // 32-channel m-tile (32 / HD heads; L and K are multiples of 32) when
-    // HD = 16.
+  // ---- conv2 on MFMA with the epilogue on its accumulators ---------------------
+  // A task is 32 * MT output channels (one head when HD >= 32, one 32-channel
+  // m-tile of two heads when HD = 16) times all NT token tiles, so each
+  // weight fragment is read once per workgroup.  Output token s0+32j+n, tap
+  // t reads Y1 row 32j+n+t.  In the 32x32 MFMA result lane (n, hf) holds
+  // token 32j+n, channels 32m + 8*g4 + 4*hf + e (e < 4): the epilogue
+  // (rounding of the conv output, QK-mean term, L2 norm with the partner
+  // lane's half (lane ^ 32), temperature, RoPE on the (e0,e1), (e2,e3)
+  // pairs) runs in registers, and channel groups are regrouped across the
+  // half-waves (v_permlane32_swap) so each lane writes 16 contiguous bytes.
+  // When there are fewer tasks than waves, the waves without one compute the
+  // QK-mean terms meanwhile (one barrier before the epilogues) and then v.
+  {
     constexpr int MT = HD >= 32 ? HD / 32 : 1;
     constexpr int HPT = HD >= 32 ? 1 : 32 / HD;  // heads per task
-    for (int hh = wave * HPT; hh < Hq + Hkv; hh += HPT * (kPrepThreads / 64)) {
+    constexpr int NHL = HD >= 32 ? 1 : 2;         // heads in a lane's channels
+    constexpr int NW = kPrepThreads / 64;
+    const int ntask = (Hq + Hkv) / HPT;
+    auto mfma = [&](int task, f32x16_p (&acc)[MT][NT]) {
+      const int hh = task * HPT;
       const bool is_k = hh >= Hq;
-      const int head = is_k ? hh - Hq : hh;
+      const int head0 = is_k ? hh - Hq : hh;
       const int C = is_k ? K : L;
-      f32x16_p acc[MT][NT];
 #pragma unroll
       for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[m][j][r] = 0.f;
-      conv2_task<MT, NT>((is_k ? wk2 : wq2) + static_cast<int64_t>(head * HD) * C +
+      conv2_task<MT, NT>((is_k ? wk2 : wq2) + static_cast<int64_t>(head0 * HD) * C +
                              (tiled ? 8 * lane : n * C + 8 * hf),
                          static_cast<int64_t>(C) * C, static_cast<int64_t>(32) * C, wstep, C / 16,
                          Y1 + n * RS + (is_k ? L : 0) + 8 * hf, RS, acc);
-      const int o0 = (is_k ? L : 0) + head * HD;
+    };
+    auto epilogue = [&](int task, f32x16_p (&acc)[MT][NT]) {
+      const int hh = task * HPT;
+      const bool is_k = hh >= Hq;
+      const int head0 = is_k ? hh - Hq : hh;
+      const int Hn = is_k ? Hkv : Hq;
+      const int q0 = G == 1 ? head0 : (is_k ? 1 : 0);  // QK-mean term row
+      bf16* obase = (is_k ? ko : qo) + ((static_cast<int64_t>(b) * Hn + head0) * S + s0) * HD;
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
+      for (int j = 0; j < NT; ++j) {
+        const int t = 32 * j + n;
+        // conv output rounded to bf16 (the reference materialises it)
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
+        for (int m = 0; m < MT; ++m)
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            uint2 w;
-            w.x = pack2<bf16>(acc[m][j][4 * g4 + 0], acc[m][j][4 * g4 + 1]);
-            w.y = pack2<bf16>(acc[m][j][4 * g4 + 2], acc[m][j][4 * g4 + 3]);
-            *reinterpret_cast<uint2*>(Y2 + (32 * j + n) * RS + o0 + 32 * m + 8 * g4 + 4 * hf) = w;
+          for (int i = 0; i < 16; i += 2) {
+            const uint32_t p = pack2<bf16>(acc[m][j][i], acc[m][j][i + 1]);
+            acc[m][j][i] = __uint_as_float(p << 16);
+            acc[m][j][i + 1] = __uint_as_float(p & 0xffff0000u);
           }
-    }
-    __syncthreads();
-  }
-
-  // ---- epilogue: QK-mean, L2-norm (+temperature), RoPE, store -------------
-  // HD/8 lanes per (token, head) row, 8 channels each; a wave covers 8 rows,
-  // i.e. the heads of consecutive tokens, so RoPE angles are shared reads
-  // and every row leaves as one contiguous 2*HD-byte store.  Roundings
-  // follow the reference: the QK-mean sum, the norm, the normalised vector,
-  // the temperature product (conv2 output and QK-mean terms are bf16).
-  constexpr int LPR = HD / 8;
-  const float tval = (qk_norm && temp) ? to_f32(temp[0]) : 1.f;
-  const int nheads = Hq + Hkv;
-  const int rows = TT * nheads;
-  for (int base = 0; base < rows * LPR; base += kPrepThreads) {
-    const int i = base + tid;
-    const bool live = i < rows * LPR;
-    const int row = live ? i / LPR : 0, c8 = (i % LPR) * 8;
-    const int r = row / nheads, hh = row - r * nheads;
-    const int s = s0 + r;
-    const bool is_k = hh >= Hq;
-    const int head = is_k ? hh - Hq : hh;
-    float v[8];
-    load16<bf16>(reinterpret_cast<const bf16*>(Y2 + r * RS + (is_k ? L : 0) + head * HD + c8), v);
-    if (qk_mean) {
-      float add[8];
-      const int q = G == 1 ? head : (is_k ? 1 : 0);
-      load16<bf16>(reinterpret_cast<const bf16*>(QA + (r * NQA + q) * HD + c8), add);
+        if (qk_mean) {
+          const uint16_t* qa = QA + t * QAS + q0 * HD + 4 * hf;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] += add[e];
-      rnd8(v);
-    }
-    if (qk_norm) {
-      float ss = 0.f;
+          for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-      ss = wave_sum<LPR>(ss);
-      const float rinv = 1.f / fmaxf(rnd<bf16>(__builtin_sqrtf(ss)), 1e-12f);
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int tc = 32 * m + 8 * g4;
+              const int off = (G == 1 ? (tc / HD) * HD : 0) + tc % HD;
+              const uint2 w = *reinterpret_cast<const uint2*>(qa + off);
+              f32x16_p& a = acc[m][j];
+              const uint32_t p0 = pack2<bf16>(a[4 * g4 + 0] + __uint_as_float(w.x << 16),
+                                              a[4 * g4 + 1] + __uint_as_float(w.x & 0xffff0000u));
+              const uint32_t p1 = pack2<bf16>(a[4 * g4 + 2] + __uint_as_float(w.y << 16),
+                                              a[4 * g4 + 3] + __uint_as_float(w.y & 0xffff0000u));
+              a[4 * g4 + 0] = __uint_as_float(p0 << 16);
+              a[4 * g4 + 1] = __uint_as_float(p0 & 0xffff0000u);
+              a[4 * g4 + 2] = __uint_as_float(p1 << 16);
+              a[4 * g4 + 3] = __uint_as_float(p1 & 0xffff0000u);
+            }
+        }
+        if (qk_norm) {
+          float ss[NHL];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] *= rinv;
-      rnd8(v);
-      if (is_k) {
+          for (int h = 0; h < NHL; ++h) ss[h] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] *= tval;
-        rnd8(v);
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int h = NHL == 1 ? 0 : (i / 4) / 2;
+              ss[h] = fmaf(acc[m][j][i], acc[m][j][i], ss[h]);
+            }
+          float rinv[NHL];
+#pragma unroll
+          for (int h = 0; h < NHL; ++h)
+            rinv[h] = 1.f / fmaxf(rnd<bf16>(__builtin_sqrtf(halves_sum(ss[h]))), 1e-12f);
+#pragma unroll
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+              const int h = NHL == 1 ? 0 : (i / 4) / 2;
+              uint32_t p = pack2<bf16>(acc[m][j][i] * rinv[h], acc[m][j][i + 1] * rinv[h]);
+              if (is_k)
+                p = pack2<bf16>(__uint_as_float(p << 16) * tval, __uint_as_float(p & 0xffff0000u) * tval);
+              acc[m][j][i] = __uint_as_float(p << 16);
+              acc[m][j][i + 1] = __uint_as_float(p & 0xffff0000u);
+            }
+        }
+        if (rope) {
+          const float* cr = CSl + t * CSR + 2 * hf;
+          const float* sr = SNl + t * CSR + 2 * hf;
+#pragma unroll
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int off = ((32 * m + 8 * g4) % HD) / 2;
+              const float2 cv = *reinterpret_cast<const float2*>(cr + off);
+              const float2 sv = *reinterpret_cast<const float2*>(sr + off);
+              f32x16_p& a = acc[m][j];
+              const float x0 = a[4 * g4 + 0], x1 = a[4 * g4 + 1];
+              const float x2 = a[4 * g4 + 2], x3 = a[4 * g4 + 3];
+              a[4 * g4 + 0] = x0 * cv.x - x1 * sv.x;
+              a[4 * g4 + 1] = x0 * sv.x + x1 * cv.x;
+              a[4 * g4 + 2] = x2 * cv.y - x3 * sv.y;
+              a[4 * g4 + 3] = x2 * sv.y + x3 * cv.y;
+            }
+        }
+        // groups g4 = 2p and 2p+1 swap halves: lane hf ends with the 8
+        // channels 32m + 8*(2p+hf) .. +7 of token t
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const f32x16_p& a = acc[m][j];
+            const uint32_t r0x = pack2<bf16>(a[8 * p + 0], a[8 * p + 1]);
+            const uint32_t r0y = pack2<bf16>(a[8 * p + 2], a[8 * p + 3]);
+            const uint32_t r1x = pack2<bf16>(a[8 * p + 4], a[8 * p + 5]);
+            const uint32_t r1y = pack2<bf16>(a[8 * p + 6], a[8 * p + 7]);
+            const auto sx = __builtin_amdgcn_permlane32_swap(r0x, r1x, false, false);
+            const auto sy = __builtin_amdgcn_permlane32_swap(r0y, r1y, false, false);
+            const int tc = 32 * m + 8 * (2 * p + hf);
+            if (s0 + t < S)
+              *reinterpret_cast<uint4*>(obase + (static_cast<int64_t>(tc / HD) * S + t) * HD + tc % HD) =
+                  make_uint4(sx[0], sy[0], sx[1], sy[1]);
+          }
       }
-    }
-    if (rope) {
-      const float* cr = CSl + r * CSR + c8 / 2;
-      const float* sr = SNl + r * CSR + c8 / 2;
-#pragma unroll
-      for (int p2 = 0; p2 < 2; ++p2) {
-        const float2 cv = *reinterpret_cast<const float2*>(cr + 2 * p2);
-        const float2 sv = *reinterpret_cast<const float2*>(sr + 2 * p2);
-        const float x0 = v[4 * p2 + 0], x1 = v[4 * p2 + 1], x2 = v[4 * p2 + 2], x3 = v[4 * p2 + 3];
-        v[4 * p2 + 0] = x0 * cv.x - x1 * sv.x;
-        v[4 * p2 + 1] = x0 * sv.x + x1 * cv.x;
-        v[4 * p2 + 2] = x2 * cv.y - x3 * sv.y;
-        v[4 * p2 + 3] = x2 * sv.y + x3 * cv.y;
+    };
+    if (ntask < NW) {
+      // One task per wave; the waves [ntask, NW) compute the QK-mean terms
+      // and count themselves done in *qa_done, which a task wave waits for
+      // (bounded: the counter only depends on waves that wait for nothing)
+      // before its epilogue, so an early task (a short k head) does not wait
+      // for the others.
+      f32x16_p acc[MT][NT];
+      if (wave < ntask) {
+        mfma(wave, acc);
+        if (qk_mean) {
+          for (int spin = 0; spin < (1 << 22); ++spin) {
+            if (__hip_atomic_load(qa_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW - ntask)
+              break;
+            __builtin_amdgcn_s_sleep(2);
+          }
+        }
+        epilogue(wave, acc);
+      } else {
+        qa_work(ntask);
+        // LDS operations of one wave complete in order: the QA writes land
+        // before the count does
+        if (lane == 0) atomicAdd(qa_done, 1);
+        v_work(ntask);
       }
-    }
-    if (live && s < S) {
-      bf16* dst = (is_k ? ko : qo) +
-                  ((static_cast<int64_t>(b) * (is_k ? Hkv : Hq) + head) * S + s) * HD + c8;
-      store16<bf16>(dst, v);
+    } else {
+      for (int task = wave; task < ntask; task += NW) {
+        f32x16_p acc[MT][NT];
+        mfma(task, acc);
+        epilogue(task, acc);
+      }
+      const int extra = ntask % NW;  // waves with one task fewer write v
+      if (wave >= extra) v_work(extra);
     }
   }
 }
@@ -899,7 +1103,8 @@ static size_t prep_mfma_lds(int64_t Hq, int64_t Hkv, int64_t hd, int TT) {
   const int64_t RS = (Hq + Hkv) * hd + 8;
   const int64_t nqa = Hq == Hkv ? Hq : 2;  // QK-mean terms per token
   return static_cast<size_t>(2 * TT + 6) * RS * 2 + static_cast<size_t>(TT) * (hd + 4) * 4 +
-         static_cast<size_t>(TT) * nqa * hd * 2 + static_cast<size_t>(TT + 1) * (Hkv * hd + 8) * 2;
+         static_cast<size_t>(TT) * (nqa * hd + 8) * 2 +
+         static_cast<size_t>(((TT + 1) * (Hkv * hd + 8) + 7) / 8 * 8) * 2 + 16;
 }
 
 template <int HD>

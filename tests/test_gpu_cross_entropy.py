@@ -77,3 +77,47 @@ def test_token_losses_from_hidden(cuda, oob):
     assert got.dtype == torch.float32 and got.shape == (2, 150)
     assert max_rel_err(got.cpu(), ref) < 1e-5
     assert (got.cpu()[ref == 0] == 0).all()
+
+
+@pytest.mark.parametrize("V", [1000, 1001, 32000])
+@pytest.mark.parametrize("with_grad", [False, True])
+def test_ce_rows_masked_logits(cuda, V, with_grad):
+    """hydra_ce_rows on logits holding -inf (masked vocabulary entries): whole
+    16-byte chunks and single entries.  Loss and gradient must be those of
+    F.cross_entropy in fp64 (finite; masked entries get zero gradient)."""
+    from hydra_amd import _lib
+
+    rows = 6
+    g = torch.Generator().manual_seed(V)
+    x = torch.randn(rows, V, generator=g)
+    x[0, :64] = -float("inf")          # leading chunks fully masked
+    x[1, 8:16] = -float("inf")         # one 16-byte chunk (fp32: two)
+    x[2, torch.randperm(V, generator=g)[: V // 3]] = -float("inf")
+    x[3, V - 5:] = -float("inf")       # ragged tail
+    t = torch.randint(0, V, (rows,), generator=g)
+    for r in range(4):
+        while torch.isinf(x[r, t[r]]):
+            t[r] = (t[r] + 1) % V
+    t[5] = -100
+    xd, td = x.to(cuda), t.to(cuda)
+    loss = torch.empty(rows, device=cuda)
+    grad = torch.empty_like(xd) if with_grad else None
+    scale = torch.full((1,), 0.25, device=cuda)
+    _lib.call("hydra_ce_rows", xd.data_ptr(), rows, V, V, td.data_ptr(), -100, loss.data_ptr(), None,
+              grad.data_ptr() if with_grad else None, V, scale.data_ptr() if with_grad else None,
+              _lib.dtype_code(xd), _lib.stream(xd))
+    x64 = x.double()
+    ref = torch.nn.functional.cross_entropy(x64, t, ignore_index=-100, reduction="none")
+    assert torch.isfinite(loss.cpu()).all()
+    assert max_rel_err(loss.cpu(), ref) < 1e-5
+    if with_grad:
+        p = torch.softmax(x64, -1)
+        gr = p.clone()
+        valid = t != -100
+        gr[valid, t[valid]] -= 1
+        gr[~valid] = 0
+        gr *= 0.25
+        gc = grad.cpu()
+        assert torch.isfinite(gc).all()
+        assert max_rel_err(gc, gr) < 1e-5
+        assert (gc[torch.isinf(x)] == 0).all()
