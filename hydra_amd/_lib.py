@@ -54,6 +54,10 @@ SIGNATURES = {
                        _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
     "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],
     "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
+    "hydra_ccgqa_prep_bwd": [_P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P,
+                             _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
+    "hydra_causal_im2col": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P],
+    "hydra_causal_col2im": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_embedding_fwd": [_P, _I64, _P, _I64, _I64, _I64, _F, _P, _I64, _I, _P],
     "hydra_residual_norm_fwd": [_P, _I64, _P, _I64, _F, _P, _P, _P, _F, _I, _P, _I64, _P, _I64,
                                 _I64, _I64, _I, _I, _P],

@@ -14,6 +14,10 @@ non-persistent RoPE buffers (cos_cached, sin_cached).  The forward is
                                                     written as [B, S, L]
     out  = o @ W_o^T * output_scale                 torch GEMM
 
+With autograd recording (and no padding mask) the forward goes through
+CCGQAPrepFunction and CCGQAAttentionFused instead, whose backwards are the
+HIP prep backward (plus the convs' GEMMs) and the HIP attention backward.
+
 The reference's precomputed [max_seq_len, max_seq_len] causal mask buffer is
 not kept: the kernel derives causality from indices.
 """
@@ -28,6 +32,8 @@ import torch.nn.functional as F
 
 from ...._autograd import track
 from ...._lib import CCGQA_V_TRANSPOSED, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_REFERENCE_SDPA
+from .autograd import ccgqa_prep_train
+from .kernels.fused_attention import CCGQAAttentionFused
 from .kernels.fused_conv import OptimizedConvSequence
 from .ops import (attention_forward, ccgqa_prep, pack_conv_weight, prep_flags,
                   qk_norm_score_bound, tiled_weights_ok)
@@ -49,7 +55,7 @@ def _mask_mode() -> int:
 
 
 class CCGQAAttention(nn.Module):
-    """Compressed Convolutional Grouped Query Attention (forward on gfx950)."""
+    """Compressed Convolutional Grouped Query Attention on gfx950."""
 
     def __init__(self, dim: int, n_heads: int = 16, n_kv_heads: int = 4,
                  compression_factor: int = 4, max_seq_len: int = 8192, use_rope: bool = True,
@@ -112,11 +118,14 @@ class CCGQAAttention(nn.Module):
         qkv = F.linear(x, self.qkv_proj.weight)
         flags = prep_flags(self.use_convs, self.use_qk_mean, self.use_value_shift,
                            self.use_qk_norm, self.use_rope)
-        if x.dtype == torch.bfloat16 and S % 8 == 0 and self.head_dim in (16, 32, 64, 128):
-            flags |= CCGQA_V_TRANSPOSED  # V^T feeds the MFMA attention without a transpose
         convw = ((self.q_conv.conv1.weight, self.q_conv.conv2.weight,
                   self.k_conv.conv1.weight, self.k_conv.conv2.weight)
                  if self.use_convs else ())
+        if mask is None and torch.is_grad_enabled() and (
+                x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return self._forward_train(qkv, flags, convw)
+        if x.dtype == torch.bfloat16 and S % 8 == 0 and self.head_dim in (16, 32, 64, 128):
+            flags |= CCGQA_V_TRANSPOSED  # V^T feeds the MFMA attention without a transpose
         tiled = self.use_convs and tiled_weights_ok(self.n_heads, self.n_kv_heads, self.head_dim, x.dtype)
         if tiled:
             flags |= CCGQA_W_TILED  # conv weights in MFMA-fragment order
@@ -132,8 +141,29 @@ class CCGQAAttention(nn.Module):
             attention_forward(q, k, v, causal=True, scale=self.scale,
                               key_mask=mask, mask_mode=_mask_mode() if mask is not None else 0,
                               out=o_view, score_bound=self._score_bound())
+        # A padding mask has no backward here (the attention backward takes
+        # none): a recorded graph through it raises instead of going silent.
         out = track(out, x, self.qkv_proj.weight, self.key_temperature, *convw)
         out = F.linear(out, self.o_proj.weight)
+        if self.output_scale != 1.0:
+            out = out * self.output_scale
+        return out
+
+    def _forward_train(self, qkv: torch.Tensor, flags: int, convw) -> torch.Tensor:
+        """The forward with autograd (no padding mask): CCGQAPrepFunction
+        (prep kernel forward; pointwise backward kernel plus the convs'
+        backward as GEMMs), then CCGQAAttentionFused (the HIP attention
+        forward and backward), as the reference trains attention.py:201-331
+        through autograd."""
+        B, S, _ = qkv.shape
+        w = tuple(convw) if self.use_convs else (None,) * 4
+        q, k, v = ccgqa_prep_train(
+            qkv, self.n_heads, self.n_kv_heads, self.head_dim, flags, *w,
+            temperature=self.key_temperature if self.use_qk_norm else None,
+            cos=self.cos_cached if self.use_rope else None,
+            sin=self.sin_cached if self.use_rope else None)
+        o = CCGQAAttentionFused.apply(q, k, v, True, True)
+        out = F.linear(o.transpose(1, 2).reshape(B, S, self.latent_dim), self.o_proj.weight)
         if self.output_scale != 1.0:
             out = out * self.output_scale
         return out

@@ -205,3 +205,80 @@ def conv_sequence(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, groups1: 
 
 __all__ = ["prep_flags", "pack_conv_weight", "ccgqa_prep", "attention_forward", "conv_sequence",
            "qk_norm_score_bound", "MASK_NONE", "MASK_KEY_PADDING", "MASK_REFERENCE_SDPA"]
+
+
+def causal_im2col(x: torch.Tensor, groups: int) -> torch.Tensor:
+    """[B,S,G*cg] (unit channel stride, any row stride) -> [G, B*S, 3*cg]:
+    row b*S+s of group g holds x[b, s+t-2, g*cg:(g+1)*cg] for taps t = 0..2
+    (zero before the row start), the operand of the k=3 causal conv as a
+    GEMM (hydra_causal_im2col)."""
+    _lib.require_gpu("causal_im2col", x)
+    B, S, C = x.shape
+    if C % groups != 0:
+        raise ValueError(f"causal_im2col: {C} channels not divisible by {groups} groups")
+    if x.stride(-1) != 1 or (B > 1 and x.stride(0) != S * x.stride(1)):
+        x = x.contiguous()
+    cg = C // groups
+    out = torch.empty((groups, B * S, 3 * cg), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call("hydra_causal_im2col", x.data_ptr(), x.stride(1), out.data_ptr(), B, S, groups, cg,
+                  _lib.dtype_code(x), _lib.stream(x))
+    return out
+
+
+def causal_col2im(cols: torch.Tensor, out: torch.Tensor, accumulate: bool = False) -> torch.Tensor:
+    """The transpose of causal_im2col: cols [G, B*S, 3*cg] summed over taps
+    into out [B,S,G*cg] (unit channel stride; added to its contents with
+    `accumulate`).  Returns out."""
+    _lib.require_gpu("causal_col2im", cols, out)
+    B, S, C = out.shape
+    G = cols.shape[0]
+    if C % G != 0 or cols.shape != (G, B * S, 3 * (C // G)) or cols.dtype != out.dtype:
+        raise ValueError(f"causal_col2im: cols {tuple(cols.shape)} do not match out {tuple(out.shape)}")
+    if out.stride(-1) != 1 or (B > 1 and out.stride(0) != S * out.stride(1)):
+        raise ValueError("causal_col2im: out needs unit channel stride and uniform row stride")
+    cols = cols.contiguous()
+    with torch.cuda.device(out.device):
+        _lib.call("hydra_causal_col2im", cols.data_ptr(), out.data_ptr(), out.stride(1), B, S, G,
+                  C // G, 1 if accumulate else 0, _lib.dtype_code(out), _lib.stream(out))
+    return out
+
+
+def ccgqa_prep_backward(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, flags: int,
+                        dq: torch.Tensor, dk: torch.Tensor, dv: torch.Tensor, y2q=None, y2k=None,
+                        temperature=None, cos=None, sin=None):
+    """Pointwise backward of ccgqa_prep (hydra_ccgqa_prep_bwd): returns
+    (dy [B,S,L+K] or None, dqkv [B,S,L+2K], dtemp_tok fp32 [B*S] or None).
+    dy is the gradient of the conv outputs (CCGQA_CONVS); dqkv holds the
+    QK-mean and v parts of grad(qkv) (and the direct q0/k0 part without
+    convs)."""
+    _lib.require_gpu("ccgqa_prep_backward", qkv, dq, dk, dv, y2q, y2k, temperature, cos, sin)
+    B, S, W = qkv.shape
+    L, K = n_heads * head_dim, n_kv_heads * head_dim
+    if W != L + 2 * K:
+        raise ValueError(f"ccgqa_prep_backward: qkv width {W} != L + 2K = {L + 2 * K}")
+    if qkv.stride(-1) != 1 or (B > 1 and qkv.stride(0) != S * qkv.stride(1)):
+        qkv = qkv.contiguous()
+    dt = qkv.dtype
+    dq, dk, dv = (t.to(dt).contiguous() for t in (dq, dk, dv))
+    convs = bool(flags & CCGQA_CONVS)
+    if convs:
+        y2q, y2k = y2q.to(dt).contiguous(), y2k.to(dt).contiguous()
+    dy = torch.empty((B, S, L + K), dtype=dt, device=qkv.device) if convs else None
+    dqkv = torch.empty((B, S, W), dtype=dt, device=qkv.device)
+    norm = bool(flags & CCGQA_QK_NORM)
+    dtemp = torch.empty(B * S, dtype=torch.float32, device=qkv.device) if norm else None
+    temp = None if temperature is None else temperature.detach().to(dt).contiguous()
+    if flags & CCGQA_ROPE:
+        if cos.dim() == 4:
+            cos, sin = cos[0, 0], sin[0, 0]
+        cos = cos[:S].float().contiguous()
+        sin = sin[:S].float().contiguous()
+    with torch.cuda.device(qkv.device):
+        _lib.call("hydra_ccgqa_prep_bwd", qkv.data_ptr(), qkv.stride(1), _lib.ptr(y2q), _lib.ptr(y2k),
+                  _lib.ptr(temp), _lib.ptr(cos), _lib.ptr(sin),
+                  head_dim // 2 if cos is None else cos.stride(0), dq.data_ptr(), dk.data_ptr(),
+                  dv.data_ptr(), _lib.ptr(dy), dqkv.data_ptr(), dqkv.stride(1), _lib.ptr(dtemp), B, S,
+                  n_heads, n_kv_heads, head_dim, flags & ~CCGQA_W_TILED, _lib.dtype_code(qkv),
+                  _lib.stream(qkv))
+    return dy, dqkv, dtemp

@@ -200,6 +200,42 @@ int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
  * host which conv-weight layout to pack. */
 int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype);
 
+/* Backward of hydra_ccgqa_prep_fwd's pointwise chain: what torch autograd
+ * computes through attention.py:211-266 (value shift, QK-mean, F.normalize
+ * with the key temperature, RoPE) given the gradients dq [B,Hq,S,hd] and
+ * dk, dv [B,Hkv,S,hd] (contiguous) of its outputs.  y2q/y2k: the conv
+ * outputs ([B,Hq,S,hd] / [B,Hkv,S,hd], i.e. hydra_ccgqa_prep_fwd with
+ * HYDRA_CCGQA_CONVS alone), required with HYDRA_CCGQA_CONVS.  Writes
+ *   dy [B,S,L+K]: gradient of the conv outputs (with CONVS),
+ *   dqkv [B,S,L+2K] (row stride dqkv_rs): [:L+K] the QK-mean part of the
+ *     q0/k0 gradient (plus the direct part without CONVS), [L+K:] the v
+ *     part (value shift undone),
+ *   dtemp_tok [B*S] (may be NULL): per-token partial of the temperature
+ *     gradient (their sum is the gradient).
+ * The flags are the forward's; V_TRANSPOSED is rejected.  L+K <= 4096. */
+int hydra_ccgqa_prep_bwd(const void* qkv, int64_t qkv_rs, const void* y2q,
+                         const void* y2k, const void* temp, const float* cos,
+                         const float* sin, int64_t cs_rs, const void* dq,
+                         const void* dk, const void* dv, void* dy, void* dqkv,
+                         int64_t dqkv_rs, float* dtemp_tok, int64_t B, int64_t S,
+                         int64_t Hq, int64_t Hkv, int64_t hd, int flags, int dtype,
+                         void* stream);
+
+/* The k = 3 causal conv of OptimizedConvSequence (kernels/fused_conv.py:52-57,
+ * left padding 2 per batch row) as a GEMM operand: x [B,S,G*cg] (row stride
+ * x_rs) -> out [G][B*S][3*cg] contiguous, out[g][b*S+s][t*cg+c] =
+ * x[b, s+t-2, g*cg+c] (0 before the row start).  A conv with weight
+ * W[o, c, t] (groups G) is then out[g] @ Wr[g]^T with Wr[g][o][t*cg+c]. */
+int hydra_causal_im2col(const void* x, int64_t x_rs, void* out, int64_t B, int64_t S,
+                        int64_t G, int64_t cg, int dtype, void* stream);
+
+/* The transpose of hydra_causal_im2col: out[b,s,g*cg+c] (row stride out_rs)
+ * = sum over taps t of in[g][b*S+s-t+2][t*cg+c] for s-t+2 < S, added to
+ * out's contents when accumulate != 0 (the conv's input gradient from the
+ * GEMM dY @ Wr). */
+int hydra_causal_col2im(const void* in, void* out, int64_t out_rs, int64_t B, int64_t S,
+                        int64_t G, int64_t cg, int accumulate, int dtype, void* stream);
+
 /* Key-mask modes of hydra_attn_fwd (key_mask: uint8 [B,S], nonzero = keep).
  * KEY_PADDING: key t is visible to query s iff key_mask[b,t] != 0 (and t <= s
  *   when causal).

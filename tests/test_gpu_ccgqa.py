@@ -150,14 +150,6 @@ def test_standalone_conv_sequence(cuda):
     assert max_rel_err(got, want) < 1e-5
 
 
-def test_backward_raises(cuda):
-    cfg, params, x = _bench_case(256, 4, 1, 1, 16, torch.float32, None, 44)
-    m = _module(cfg, params, cuda, torch.float32).train()
-    y = m(x.to(cuda).requires_grad_())
-    with pytest.raises(NotImplementedError):
-        y.sum().backward()
-
-
 def test_prep_generic_kernel_fallback(cuda, monkeypatch):
     """The one-thread-per-output VALU prep kernel (forced; otherwise taken
     only by layouts the other kernels reject) against the oracle, fp32."""
