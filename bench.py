@@ -95,7 +95,8 @@ class C3Step:
         self.cos = mm.cos_cached[0, 0, :S].float().contiguous()
         self.sin = mm.sin_cached[0, 0, :S].float().contiguous()
         self.out = torch.empty(B, S, mm.latent_dim, dtype=torch.bfloat16, device=dev)
-        self.bound = mm._score_bound()  # |q.k| bound from QK-norm (temperature 1.0)
+        # |q.k| bound from QK-norm, taken by the kernel from the temperature
+        self.temp = mm.key_temperature.detach()
 
     @torch.no_grad()
     def __call__(self, ev=None, x=None):
@@ -113,7 +114,7 @@ class C3Step:
         if ev:
             ev[2].record()
         o_view = self.out.view(self.B, self.S, m.n_heads, m.head_dim).transpose(1, 2)
-        attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view, score_bound=self.bound)
+        attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view, bound_temperature=self.temp)
         if ev:
             ev[3].record()
         y = F.linear(self.out, m.o_proj.weight)
@@ -214,7 +215,7 @@ def bench_c3(dev, steps, warmup):
                              temperature=m.key_temperature, cos=step.cos, sin=step.sin, packed=True)
     o_view = step.out.view(step.B, step.S, m.n_heads, m.head_dim).transpose(1, 2)
     attn_ms = _time_rotating(lambda: attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view,
-                                                       score_bound=step.bound),
+                                                       bound_temperature=step.temp),
                              [()], 8 * max(1, steps // 2))
     return step, graph_ms, eager_ms, stages, attn_ms
 

@@ -49,7 +49,7 @@ SIGNATURES = {
     "hydra_ccgqa_prep_fwd": [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P,
                              _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_attn_fwd": [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64,
-                       _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _I, _P],
+                       _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _P, _I, _I, _P],
     "hydra_attn_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                        _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
     "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],

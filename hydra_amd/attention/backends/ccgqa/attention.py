@@ -35,8 +35,7 @@ from ...._lib import CCGQA_V_TRANSPOSED, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_R
 from .autograd import ccgqa_prep_train
 from .kernels.fused_attention import CCGQAAttentionFused
 from .kernels.fused_conv import OptimizedConvSequence
-from .ops import (attention_forward, ccgqa_prep, pack_conv_weight, prep_flags,
-                  qk_norm_score_bound, tiled_weights_ok)
+from .ops import attention_forward, ccgqa_prep, pack_conv_weight, prep_flags, tiled_weights_ok
 
 # Kept for callers that probe these names (attention.py:13-28).
 FUSED_KERNELS_AVAILABLE = True
@@ -140,7 +139,8 @@ class CCGQAAttention(nn.Module):
             o_view = out.view(B, S, self.n_heads, self.head_dim).transpose(1, 2)
             attention_forward(q, k, v, causal=True, scale=self.scale,
                               key_mask=mask, mask_mode=_mask_mode() if mask is not None else 0,
-                              out=o_view, score_bound=self._score_bound())
+                              out=o_view,
+                              bound_temperature=self.key_temperature if self.use_qk_norm else None)
         # A padding mask has no backward here (the attention backward takes
         # none): a recorded graph through it raises instead of going silent.
         out = track(out, x, self.qkv_proj.weight, self.key_temperature, *convw)
@@ -167,22 +167,6 @@ class CCGQAAttention(nn.Module):
         if self.output_scale != 1.0:
             out = out * self.output_scale
         return out
-
-    def _score_bound(self):
-        """The bound on |q.k| that QK-norm implies (qk_norm_score_bound of the
-        key temperature), or None without QK-norm.  The temperature is read
-        from the device once per value: cached on the parameter's version
-        counter, like the packed conv weights (so a captured HIP graph keeps
-        the value it was captured with)."""
-        if not self.use_qk_norm:
-            return None
-        t = self.key_temperature
-        key = (t.data_ptr(), t._version, t.device)
-        cache = getattr(self, "_bound_cache", None)
-        if cache is None or cache[0] != key:
-            cache = (key, qk_norm_score_bound(t.detach().abs().max().item()))
-            self._bound_cache = cache
-        return cache[1]
 
     def _packed_conv_weights(self, convw, dtype, tiled=False):
         """Packed copies (tap-major, or MFMA-tiled) of the four conv weights in

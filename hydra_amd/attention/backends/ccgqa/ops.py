@@ -99,12 +99,16 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
 def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool,
                       scale: Optional[float] = None, key_mask: Optional[torch.Tensor] = None,
                       mask_mode: int = MASK_NONE, out: Optional[torch.Tensor] = None,
-                      want_lse: bool = False, score_bound: Optional[float] = None):
+                      want_lse: bool = False, score_bound: Optional[float] = None,
+                      bound_temperature: Optional[torch.Tensor] = None):
     """Softmax attention over [B,H,S,hd] q and [B,Hkv,S,hd] k/v.  `out` may be
     any [B,Hq,S,hd]-indexed view (e.g. a [B,S,Hq,hd] buffer transposed).
     score_bound: optional beta >= max |q.k| (before the scale); with one the
     bf16 kernel takes a fixed reference max instead of a running row max
-    (see qk_norm_score_bound).  Returns (out, lse or None)."""
+    (see qk_norm_score_bound).  bound_temperature: a one-element bf16/fp32
+    tensor on the device whose qk_norm_score_bound the kernel takes itself
+    at launch (no host sync; graph replays follow later values).  Returns
+    (out, lse or None)."""
     _lib.require_gpu("attention_forward", q, k, v, key_mask, out)
     B, Hq, S, hd = q.shape
     Hkv = k.shape[1]
@@ -129,12 +133,19 @@ def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
             raise ValueError(f"attention_forward: key mask must be [B,S] = [{B},{S}]")
         km = (key_mask != 0).to(torch.uint8).contiguous()
     sc = float(hd ** -0.5) if scale is None else float(scale)
+    bt = None
+    if bound_temperature is not None:
+        bt = bound_temperature.detach()
+        if bt.dtype not in (torch.bfloat16, torch.float32):
+            bt = bt.float()
+        bt = bt.reshape(-1)[:1].contiguous()
+        _lib.require_gpu("attention_forward", bt)
     with torch.cuda.device(q.device):
         _lib.call("hydra_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                   _lib.ptr(lse), _lib.ptr(km), mask_mode, B, Hq, Hkv, S, hd,
                   _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
-                  1 if causal else 0, sc, float(score_bound or 0.0), _lib.dtype_code(q),
-                  _lib.stream(q))
+                  1 if causal else 0, sc, float(score_bound or 0.0), _lib.ptr(bt),
+                  0 if bt is None else _lib.dtype_code(bt), _lib.dtype_code(q), _lib.stream(q))
     return out, lse
 
 

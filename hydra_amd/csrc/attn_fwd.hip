@@ -272,9 +272,38 @@ __device__ __forceinline__ void attn_tile(const uint16_t* kt, const uint16_t* vt
   }
 }
 
+// LDS tile sizes of attn_fwd_mfma_body / attn_fwd_kp_body (elements).
+template <int HD, bool VT>
+struct AttnLds {
+  static constexpr int DT = (HD + 31) / 32;
+  static constexpr int KSL = HD / 8 + 1;
+  static constexpr int KBUF = kAttnBN * 8 * KSL;
+  static constexpr int VSL = kAttnBN / 8 + 1;
+  static constexpr int VROW = VT ? 8 * VSL : kAttnBN + 4;
+  static constexpr int VINS = (HD * VSL + 63) / 64;
+  static constexpr int VBUF = (VT && VINS * 512 > DT * 32 * VROW) ? VINS * 512 : DT * 32 * VROW;
+};
+
+// Whether the fixed-reference path applies, from the QK-norm temperature on
+// the device: |q.k| <= 1.03 |temperature| (q unit norm, k of norm
+// |temperature|, with room for the bf16 roundings), and the path needs that
+// bound times scale * log2(e) to be <= 48 (log2 units).  Read by every lane
+// from one address and made wave-uniform.
+__device__ __forceinline__ bool attn_fixed_from_temperature(const void* tau, int tau_bf16,
+                                                            float scale_log2) {
+  float t;
+  if (tau_bf16) {
+    t = __uint_as_float(static_cast<uint32_t>(*static_cast<const uint16_t*>(tau)) << 16);
+  } else {
+    t = *static_cast<const float*>(tau);
+  }
+  t = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(t)));
+  return 1.03f * fabsf(t) * scale_log2 <= 48.f;
+}
+
 template <int HD, bool CAUSAL, int MASK, bool VT, int NW, bool FIXED>
-__global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+__device__ __forceinline__ void attn_fwd_mfma_body(
+    uint16_t* __restrict__ Ks, uint16_t* __restrict__ Vt, const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
     int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int T, int per_item,
     float* __restrict__ ws, int4* __restrict__ desc,
@@ -312,9 +341,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   // scaled Q is rounded to bf16 once (2^-9 relative per element, the size of
   // Q's own bf16 rounding).
   constexpr bool fixed_max = FIXED;
-
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * KBUF];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2 * VBUF];
+  static_assert(KBUF == AttnLds<HD, VT>::KBUF && VBUF == AttnLds<HD, VT>::VBUF,
+                "LDS sizes agree with the kernel's arrays");
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -621,6 +649,36 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
   if (!started && tid == 0) desc[blockIdx.x] = make_int4(0, 0, 0, 0);
 }
 
+// FXM: 0 running row max, 1 fixed reference (the host has bounded |q.k|),
+// 2 either, chosen per launch from the temperature on the device (no host
+// read of it, and a captured graph follows later temperatures).
+template <int HD, bool CAUSAL, int MASK, bool VT, int NW, int FXM>
+__global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int T, int per_item,
+    float* __restrict__ ws, int4* __restrict__ desc,
+    int64_t qs0, int64_t qs1, int64_t qs2,
+    int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2,
+    int64_t os0, int64_t os1, int64_t os2, float scale_log2, const void* tau, int tau_bf16) {
+  using Lds = AttnLds<HD, VT>;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * Lds::KBUF];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2 * Lds::VBUF];
+#define HYDRA_MFMA_BODY(FX)                                                                  \
+  attn_fwd_mfma_body<HD, CAUSAL, MASK, VT, NW, FX>(Ks, Vt, q, k, v, o, lse, kmask, S, Hq, Hkv, \
+                                                   G, ntasks, nwg, BH, T, per_item, ws, desc, \
+                                                   qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1,    \
+                                                   vs2, os0, os1, os2, scale_log2)
+  if constexpr (FXM == 2) {
+    if (attn_fixed_from_temperature(tau, tau_bf16, scale_log2)) HYDRA_MFMA_BODY(true);
+    else HYDRA_MFMA_BODY(false);
+  } else {
+    HYDRA_MFMA_BODY(FXM == 1);
+  }
+#undef HYDRA_MFMA_BODY
+}
+
 // Key-split workgroups (V^T rows only).  A workgroup of KP x NW waves takes
 // one item whole -- NW tasks, as in attn_fwd_mfma_kernel -- and its KP groups
 // of NW waves walk the item's key tiles in turn (group g: tiles g, g + KP,
@@ -631,8 +689,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
 // KP-fold fewer steps, which is what balances the causal triangle when
 // there are few items.
 template <int HD, bool CAUSAL, int MASK, int NW, int KP, bool FIXED>
-__global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+__device__ __forceinline__ void attn_fwd_kp_body(
+    uint16_t* __restrict__ smem, const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
     int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH,
     int64_t qs0, int64_t qs1, int64_t qs2,
@@ -657,8 +715,9 @@ __global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
   constexpr int NT = 64 * NW * KP;
   constexpr int XF = DT * 16 + 2;          // exchanged floats per lane: O, m, l
   static_assert((KP - 1) * NW * 64 * XF * 4 <= KP * GBUF * 2, "the exchange fits in the tile buffers");
+  static_assert(KBUF == AttnLds<HD, true>::KBUF && VBUF == AttnLds<HD, true>::VBUF,
+                "LDS sizes agree with the kernel's array");
   constexpr uint32_t kOob = 0x80000000u;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[KP * GBUF];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -847,6 +906,30 @@ __global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
   }
 }
 
+template <int HD, bool CAUSAL, int MASK, int NW, int KP, int FXM>
+__global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH,
+    int64_t qs0, int64_t qs1, int64_t qs2,
+    int64_t ks0, int64_t ks1, int64_t ks2,
+    int64_t vs0, int64_t vs1, int64_t vs2,
+    int64_t os0, int64_t os1, int64_t os2, float scale_log2, const void* tau, int tau_bf16) {
+  using Lds = AttnLds<HD, true>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[KP * 2 * (Lds::KBUF + Lds::VBUF)];
+#define HYDRA_KP_BODY(FX)                                                                     \
+  attn_fwd_kp_body<HD, CAUSAL, MASK, NW, KP, FX>(smem, q, k, v, o, lse, kmask, S, Hq, Hkv, G,  \
+                                                 ntasks, nwg, BH, qs0, qs1, qs2, ks0, ks1, ks2, \
+                                                 vs0, vs1, vs2, os0, os1, os2, scale_log2)
+  if constexpr (FXM == 2) {
+    if (attn_fixed_from_temperature(tau, tau_bf16, scale_log2)) HYDRA_KP_BODY(true);
+    else HYDRA_KP_BODY(false);
+  } else {
+    HYDRA_KP_BODY(FXM == 1);
+  }
+#undef HYDRA_KP_BODY
+}
+
 // Combines the chunks of split items.  One thread per (w, wave, lane),
 // where w is the workgroup whose range holds the item's tile 0: lane l of a
 // wave holds query l%32 and, for f = 0..DT*4-1, d = 32(f/4) + 8(f%4) +
@@ -992,7 +1075,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t S, const int64_t* qs, const int64_t* ks,
                        const int64_t* vs, const int64_t* os, bool causal, float scale,
-                       float score_bound, hipStream_t st) {
+                       float score_bound, const void* tau, int tau_bf16, hipStream_t st) {
   constexpr int NW = 4;  // waves per workgroup; GQA heads share each staged K/V tile
   constexpr int DT = (HD + 31) / 32;
   // V with unit stride along the keys is read as V^T rows (vs[3] apart).
@@ -1024,7 +1107,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   auto go = [&](auto c_tag, auto m_tag, auto f_tag) -> int {
     constexpr bool C = decltype(c_tag)::value;
     constexpr int M = decltype(m_tag)::value;
-    constexpr bool FX = decltype(f_tag)::value;
+    constexpr int FX = decltype(f_tag)::value;
     // Schedule.  With at least two items per resident workgroup slot, one
     // workgroup per item (longest first) lets the dispatcher balance the
     // load.  With fewer: for V^T rows, key-split workgroups (one item per
@@ -1048,7 +1131,7 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
       constexpr int KP = HD == 128 ? 2 : 3;  // key groups (LDS: KP double-buffered K/V^T tiles)
       attn_fwd_kp_kernel<HD, C, M, NW, KP, FX><<<dim3(static_cast<unsigned>(nwg * BH)), 64 * NW * KP, 0, st>>>(
           Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, qs[0], qs[1], qs[2], ks[0], ks[1],
-          ks[2], vs[0], vs[1], vs[3], os[0], os[1], os[2], sl2);
+          ks[2], vs[0], vs[1], vs[3], os[0], os[1], os[2], sl2, tau, tau_bf16);
       return check_launch("attn_fwd_kp_kernel");
     }
     auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX> : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>;
@@ -1084,7 +1167,8 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     desc = reinterpret_cast<int4*>(static_cast<char*>(w) + pb);
     kern<<<dim3(static_cast<unsigned>(P)), 64 * NW, 0, st>>>(
         Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, T, per_item ? 1 : 0, part, desc,
-        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2);
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2,
+        tau, tau_bf16);
     const int rc1 = check_launch("attn_fwd_mfma_kernel");
     if (rc1 != HYDRA_OK || !split) return rc1;
     const int64_t threads = static_cast<int64_t>(P) * NW * 64;
@@ -1097,11 +1181,17 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
   using M0 = std::integral_constant<int, 0>;
   using M1 = std::integral_constant<int, 1>;
   using M2 = std::integral_constant<int, 2>;
-  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) return go(F_(), M2(), F_());
-  if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) return go(T_(), M1(), F_());
-  if (mask_mode == HYDRA_MASK_KEY_PADDING) return go(F_(), M1(), F_());
-  if (causal) return use_fixed ? go(T_(), M0(), T_()) : go(T_(), M0(), F_());
-  return use_fixed ? go(F_(), M0(), T_()) : go(F_(), M0(), F_());
+  // fixed-reference mode: 0 none, 1 from the host's bound, 2 from the
+  // temperature on the device
+  using X0 = std::integral_constant<int, 0>;
+  using X1 = std::integral_constant<int, 1>;
+  using X2 = std::integral_constant<int, 2>;
+  if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) return go(F_(), M2(), X0());
+  if (causal && mask_mode == HYDRA_MASK_KEY_PADDING) return go(T_(), M1(), X0());
+  if (mask_mode == HYDRA_MASK_KEY_PADDING) return go(F_(), M1(), X0());
+  const bool dev = tau != nullptr;
+  if (causal) return dev ? go(T_(), M0(), X2()) : use_fixed ? go(T_(), M0(), X1()) : go(T_(), M0(), X0());
+  return dev ? go(F_(), M0(), X2()) : use_fixed ? go(F_(), M0(), X1()) : go(F_(), M0(), X0());
 }
 
 // ---------------------------------------------------------------------------
@@ -1292,8 +1382,12 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
                               int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
                               const int64_t* qs, const int64_t* ks, const int64_t* vs,
                               const int64_t* os, int causal, float scale,
-                              float score_bound, int dtype, void* stream) {
+                              float score_bound, const void* bound_temperature,
+                              int bound_temperature_dtype, int dtype, void* stream) {
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_fwd: bad size");
+  HYDRA_REQUIRE(bound_temperature == nullptr || bound_temperature_dtype == HYDRA_BF16 ||
+                    bound_temperature_dtype == HYDRA_F32,
+                "attn_fwd: the bound temperature must be bf16 or fp32");
   HYDRA_REQUIRE(Hq % Hkv == 0, "attn_fwd: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(qs && ks && vs && os, "attn_fwd: null stride array");
   HYDRA_REQUIRE(qs[3] == 1 && ks[3] == 1 && os[3] == 1,
@@ -1330,10 +1424,10 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   if (dtype == HYDRA_BF16 && mfma_shape && strides8 && aligned16(q) && aligned16(k) &&
       aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0) {
     switch (hd) {
-      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
-      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
-      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
-      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, st);
+      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
+      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
+      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
+      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
     }
   }
   HYDRA_REQUIRE(B * Hq * S / 256 < (int64_t(1) << 31), "attn_fwd: too many rows");

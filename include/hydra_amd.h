@@ -272,6 +272,13 @@ int hydra_causal_col2im(const void* in, void* out, int64_t out_rs, int64_t B, in
  *   RoPE a rotation) beta = 1.03 * |temperature| holds: the 3% covers the
  *   bf16 roundings of the norm, the normalised vector, the temperature
  *   product and RoPE.
+ * bound_temperature (device pointer to one bf16 or fp32 value, dtype code
+ *   bound_temperature_dtype; may be NULL): the same bound taken on the
+ *   device, beta = 1.03 * |*bound_temperature|, read by the kernel at each
+ *   launch -- no host read of the temperature, and a captured graph follows
+ *   its later values.  Takes precedence over score_bound; ignored with a
+ *   key mask.  (No counterpart in the reference: its Triton kernel always
+ *   keeps a running max.)
  * A query row with no visible key gets o = 0 (as CPU SDPA) and lse = -inf.
  * bf16 with hd in {16,32,64,128} runs on MFMA; other cases on the VALU. */
 int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
@@ -279,7 +286,8 @@ int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
                    const int64_t* qs, const int64_t* ks, const int64_t* vs,
                    const int64_t* os, int causal, float scale,
-                   float score_bound, int dtype, void* stream);
+                   float score_bound, const void* bound_temperature,
+                   int bound_temperature_dtype, int dtype, void* stream);
 
 /* Causal / full GQA attention backward: given the forward's q, k, v, its
  * output o and lse (hydra_attn_fwd's fp32 [B,Hq,S] natural-log sum-exp of

@@ -440,3 +440,55 @@ def test_attention_fixed_vt_rows(cuda, monkeypatch, case, sched):
     ref_lse = torch.logsumexp(logits, -1)
     assert (lse_f.cpu() - ref_lse).abs().max().item() < 2e-2
     assert (lse_f - lse_o).abs().max().item() < 2 ** -7
+
+
+@pytest.mark.parametrize("vt", [False, True])
+@pytest.mark.parametrize("tdtype", [torch.bfloat16, torch.float32])
+def test_attention_bound_from_device_temperature(cuda, vt, tdtype):
+    """bound_temperature: the kernel takes qk_norm_score_bound of the
+    temperature on the device.  Inside the fixed range it gives exactly the
+    host-bound result; outside (|q.k| up to 300) exactly the running-max
+    result."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward, qk_norm_score_bound
+
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    vv = (lambda t: _vt_rows(dev(t))) if vt else dev
+    for temp in (2.0, 300.0):
+        q, k, v = _normed_qkv(1, 4, 1, 512, 64, temp, seed=7)
+        t = torch.full((1,), temp, dtype=tdtype, device=cuda)
+        out_d, lse_d = attention_forward(dev(q), dev(k), vv(v), causal=True, want_lse=True,
+                                         bound_temperature=t)
+        out_h, lse_h = attention_forward(dev(q), dev(k), vv(v), causal=True, want_lse=True,
+                                         score_bound=qk_norm_score_bound(temp))
+        assert torch.equal(out_d, out_h) and torch.equal(lse_d, lse_h)
+        assert max_rel_err(out_d.cpu(), occ.attention(q, k, v, causal=True)) < 2e-2
+
+
+def test_attention_device_bound_follows_temperature_in_graph(cuda):
+    """A HIP graph captured with bound_temperature reads the temperature at
+    every replay: raising it past the fixed range afterwards switches the
+    replays to the running-max path (whose result differs in the last bits)."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    q, k, v = (dev(x) for x in _normed_qkv(1, 4, 1, 512, 64, 2.0, seed=8))
+    t = torch.full((1,), 2.0, dtype=torch.float32, device=cuda)
+    out = torch.empty_like(q)
+    want_fixed, _ = attention_forward(q, k, v, causal=True, score_bound=2.06)
+    want_online, _ = attention_forward(q, k, v, causal=True)
+    assert not torch.equal(want_fixed, want_online)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        attention_forward(q, k, v, causal=True, out=out, bound_temperature=t)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        attention_forward(q, k, v, causal=True, out=out, bound_temperature=t)
+    for temp, want in ((2.0, want_fixed), (1000.0, want_online), (2.0, want_fixed)):
+        t.fill_(temp)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), temp
