@@ -652,8 +652,11 @@ __device__ __forceinline__ void attn_fwd_mfma_body(
 // FXM: 0 running row max, 1 fixed reference (the host has bounded |q.k|),
 // 2 either, chosen per launch from the temperature on the device (no host
 // read of it, and a captured graph follows later temperatures).
+// With both paths in one kernel (FXM 2) the register budget is held to
+// three waves per SIMD at HD <= 64, the occupancy each path has alone.
 template <int HD, bool CAUSAL, int MASK, bool VT, int NW, int FXM>
-__global__ __launch_bounds__(64 * NW) void attn_fwd_mfma_kernel(
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu((FXM == 2 && HD <= 64) ? 3 : 1))) void attn_fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
     int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int T, int per_item,
