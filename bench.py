@@ -424,8 +424,8 @@ def bench_mod(dev, iters=50):
 
 # ------------------------------------------------------------- CPU baseline
 def host_cpu() -> dict:
-    """This host's CPU as the baseline reports it: model name, physical and
-    logical cores, the CPUs this process may run on, ISA extensions that
+    """This host's CPU as the baseline reports it: model name, family / model
+    / stepping, physical and logical cores, the CPUs this process may run on, ISA extensions that
     matter for torch's CPU kernels, and the threads the baselines use.
     Threads: the CPUs this process may use, capped by OMP_NUM_THREADS when
     the environment sets it (a GPU box shares its host between GPUs) and by
@@ -440,6 +440,9 @@ def host_cpu() -> dict:
             key, val = key.strip(), val.strip()
             if key == "model name" and info["model"] == "unknown":
                 info["model"] = val
+            elif key in ("cpu family", "model", "stepping"):
+                name = {"cpu family": "cpu_family", "model": "cpu_model", "stepping": "stepping"}[key]
+                info.setdefault(name, int(val) if val.isdigit() else val)
             elif key == "physical id":
                 phys = val
             elif key == "core id":
@@ -451,6 +454,8 @@ def host_cpu() -> dict:
         pass
     info["physical_cores"] = len(cores) or None
     info["isa"] = {f: f in flags for f in ("avx2", "avx512f", "avx512_bf16", "amx_bf16", "amx_tile")}
+    # family 26 (0x1A) is AMD Zen 5 (EPYC 9005); a guest names only "AMD EPYC"
+    info["virtualised"] = "hypervisor" in flags
     threads = info["usable_cpus"] or info["logical_cores"] or 1
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
         threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
