@@ -29,10 +29,17 @@ __device__ __forceinline__ uint32_t score_key_asc(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off)));
-  return v;
+// Inclusive prefix sum over the 64 lanes of a wave with DPP: row shifts
+// within each 16-lane row, then the broadcasts of lane 15 to rows 1 and 3 and
+// of lane 31 to rows 2 and 3.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
 }
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
@@ -116,7 +123,7 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_kernel(
     int64_t* __restrict__ idx_desc, int64_t* __restrict__ idx_sorted,
     void* __restrict__ mask, int mask_dtype) {
   constexpr int P = EPT * kTopkThreads;
-  extern __shared__ unsigned char smem[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
   uint32_t* bits = reinterpret_cast<uint32_t*>(smem + sizeof(uint64_t) * P);
   __shared__ int wave_tot[kTopkThreads / 64];
@@ -169,12 +176,7 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_kernel(
   int cnt = 0;
   for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(bits[w]);
   const int lane = tid & 63, wave = tid >> 6;
-  int incl = cnt;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int n = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += n;
-  }
+  const int incl = wave_incl_sum(cnt);
   if (lane == 63) wave_tot[wave] = incl;
   __syncthreads();
   int base = 0;
@@ -198,20 +200,22 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_kernel(
 //     descending, NaN first, -0.0 == +0.0); histogram of its top kBinBits
 //     bits in LDS (atomic adds; each key keeps its slot within its bin);
 //  2. exclusive scan of the histogram -> the first position of every bin in
-//     the value-descending order; the largest bin, and the bin holding
-//     position k-1 (the threshold bin);
+//     the value-descending order; whether any bin is over kBucketMaxBin, and
+//     the bin holding position k-1 (the threshold bin);
 //  3. every key written to its bin's segment as the 64-bit composite
-//     (desc << 32) | index;
-//  4. the rank of a key = first position of its bin + the keys of its bin
+//     (desc << 32) | index, so keys[] is in bin order;
+//  4. the selection bitmap of the keys below the threshold bin, and of the
+//     threshold bin's keys of rank < k (see 5);
+//  5. the rank of a key = first position of its bin + the keys of its bin
 //     with a smaller composite (a larger score, or an equal score at a lower
 //     index) -- exact, the order of a stable descending sort.  Keys below the
 //     threshold bin are selected, keys above are not, keys in it are
-//     selected when their rank is < k; the workgroup ranks the selected keys
-//     of its 1024-key part and writes idx_desc[rank] = index;
-//  5. the selection bitmap of the whole row (only the threshold bin needs
-//     ranks), prefix counts over its words, then the mask and the ascending
-//     list entries of the workgroup's part.
-// Steps 1-3 are repeated by each of a row's workgroups (cheap); the ranks,
+//     selected when their rank is < k; the workgroup ranks the keys of the
+//     bins up to the threshold bin that start at positions [1024 part,
+//     1024 part + 1024) of keys[] and writes idx_desc[rank] = index;
+//  6. prefix counts over the bitmap's words give the mask and the ascending
+//     list entries of the workgroup's part of the row.
+// Steps 1-4 are repeated by each of a row's workgroups (cheap); the ranks,
 // the expensive part, are split between them.  Bins are small for real
 // score distributions (tens of keys for N(0, 1) scores at L = 4096); when the
 // largest bin exceeds kBucketMaxBin keys (e.g. many equal scores) the row's
@@ -226,18 +230,30 @@ constexpr int kBinWords = kBins + kBins / 4;
 __device__ __forceinline__ uint32_t bin_slot(uint32_t b) { return b + 4 * (b >> 4); }
 constexpr int kBucketMaxL = 8192;
 constexpr int kBucketMaxBin = 512;
+constexpr int kKeyPad = 8;  // all-ones keys after the row, read by seg_rank
 
-// Rank of composite `me` within the bin segment keys[b0, b1): b0 + the keys
-// smaller than it (8 independent LDS reads in flight per step; the tail
-// reads clamp to the segment's last key and count 0).
-__device__ __forceinline__ int bin_rank(const uint64_t* keys, int b0, int b1, uint64_t me) {
-  int r = b0;
-  for (int j = b0; j < b1; j += 8) {
-    uint64_t kv[8];
+// Rank of composite `me` among the row's keys, given its bin's segment
+// [b0, b1) of the bin-ordered keys[]: b0 + the segment's keys below `me`.
+// The reads start at b0 rounded down to an even position (16-byte aligned;
+// the lanes of a wave that rank different bins then spread over the LDS
+// banks) and run in rounds of 8 keys past b1: the key before b0 belongs to
+// a lower bin (below `me`, so it counts b0 - s) and those at or after b1 to
+// higher bins or the all-ones padding after the row (never below `me`), so
+// the rank is s + the count.
+__device__ __forceinline__ int seg_rank(const uint64_t* keys, int b0, int b1, uint64_t me) {
+  const int s = b0 & ~1;
+  int r = s;
+  for (int j = s; j < b1; j += 8) {
+    const uint4* q = reinterpret_cast<const uint4*>(keys + j);
+    uint4 w[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) kv[u] = keys[min(j + u, b1 - 1)];
+    for (int u = 0; u < 4; ++u) w[u] = q[u];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) r += (j + u < b1 && kv[u] < me) ? 1 : 0;
+    for (int u = 0; u < 4; ++u) {
+      const uint64_t a = (static_cast<uint64_t>(w[u].y) << 32) | w[u].x;
+      const uint64_t c = (static_cast<uint64_t>(w[u].w) << 32) | w[u].z;
+      r += (a < me ? 1 : 0) + (c < me ? 1 : 0);
+    }
   }
   return r;
 }
@@ -248,34 +264,41 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
     int64_t* __restrict__ idx_desc, int64_t* __restrict__ idx_sorted,
     void* __restrict__ mask, int mask_dtype) {
   constexpr int P = EPT * kTopkThreads;
-  extern __shared__ unsigned char smem[];
-  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);                         // [P] composites
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + sizeof(uint64_t) * P);  // [kBinWords]
-  uint32_t* bits = hist + kBinWords;                                          // [L/32] selection
-  uint32_t* wpre = bits + P / 32;                                             // [L/32] word prefixes
-  __shared__ int wave_tot[kTopkThreads / 64];
-  __shared__ int wave_max[kTopkThreads / 64];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);                                      // [P + 8]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + sizeof(uint64_t) * (P + kKeyPad));  // [kBinWords]
+  uint32_t* bits = hist + kBinWords;                                                       // [L/32] selection
+  uint32_t* wpre = bits + P / 32;                                                          // [L/32] word prefixes
+  // per wave: bin count | (any bin > kBucketMaxBin) << 16; then popcounts
+  __shared__ __align__(16) int wave_tot[kTopkThreads / 64];
+  __shared__ __align__(16) int wave_pc[kTopkThreads / 64];
   __shared__ int thr[2];  // threshold bin, its first position
 
   const int row = blockIdx.x / R, part = blockIdx.x - row * R;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const S* sr = scores + static_cast<int64_t>(row) * s_rs;
-  for (int i = tid; i < kBinWords; i += kTopkThreads) hist[i] = 0u;
+  // the row's scores load while the bins clear; element e of this thread
+  // is i = tid + 1024 e
+  S raw[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = tid + kTopkThreads * e;
+    raw[e] = i < L ? sr[i] : S();
+  }
+  static_assert(kBinWords % (4 * kTopkThreads) == 0, "bins clear in whole 16-byte rounds");
+#pragma unroll
+  for (int i = tid; i < kBinWords / 4; i += kTopkThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0u, 0u, 0u, 0u);
   const int nwords = (L + 31) / 32;
   for (int i = tid; i < nwords; i += kTopkThreads) bits[i] = 0u;
   __syncthreads();
 
-  // 1. keys and histogram; element e of this thread is i = tid + 1024 e
+  // 1. histogram of the keys (each key keeps its slot within its bin)
   uint32_t dk[EPT], slot[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int i = tid + kTopkThreads * e;
-    dk[e] = 0u;
-    slot[e] = 0u;
-    if (i < L) {
-      dk[e] = ~score_key_asc(to_f32(sr[i]));
-      slot[e] = atomicAdd(&hist[bin_slot(dk[e] >> (32 - kBinBits))], 1u);
-    }
+    dk[e] = i < L ? ~score_key_asc(to_f32(raw[e])) : 0u;
+    slot[e] = i < L ? atomicAdd(&hist[bin_slot(dk[e] >> (32 - kBinBits))], 1u) : 0u;
   }
   __syncthreads();
 
@@ -289,28 +312,29 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
     const uint4 w = hrun[q];
     hv[4 * q] = w.x; hv[4 * q + 1] = w.y; hv[4 * q + 2] = w.z; hv[4 * q + 3] = w.w;
   }
-  int cnt = 0, mx = 0;
+  int cnt = 0;
+  bool big = false;
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
     cnt += static_cast<int>(hv[j]);
-    mx = max(mx, static_cast<int>(hv[j]));
+    big |= hv[j] > static_cast<uint32_t>(kBucketMaxBin);
   }
-  int incl = cnt;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int n = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += n;
-  }
-  mx = static_cast<int>(wave_max_u(static_cast<uint32_t>(mx)));
-  if (lane == 63) wave_tot[wave] = incl;
-  if (lane == 0) wave_max[wave] = mx;
+  const int incl = wave_incl_sum(cnt);
+  const bool wbig = __ballot(big) != 0;
+  if (lane == 63) wave_tot[wave] = incl | (wbig ? 1 << 16 : 0);
   __syncthreads();
-  int base = 0, gmx = 0;
-  for (int w = 0; w < kTopkThreads / 64; ++w) {
-    if (w < wave) base += wave_tot[w];
-    gmx = max(gmx, wave_max[w]);
+  int base = 0, nbig = 0;
+#pragma unroll
+  for (int q = 0; q < kTopkThreads / 256; ++q) {
+    const int4 t = reinterpret_cast<const int4*>(wave_tot)[q];
+    const int tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      base += 4 * q + u < wave ? (tv[u] & 0xffff) : 0;
+      nbig += tv[u] >> 16;
+    }
   }
-  if (gmx > kBucketMaxBin) {
+  if (nbig) {
     // Degenerate bins: the row's first workgroup sorts the whole row (ties
     // by index, as above) and writes every output; the others leave.
     if (part != 0) return;
@@ -329,18 +353,28 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
     }
   } else {
     int pos = base + incl - cnt;
+    if (pos <= k - 1 && k - 1 < pos + cnt) {  // exactly one thread's bins hold position k-1
+      // the threshold bin is the first whose end passes k-1
+      int q = pos, jt = 0, pt = pos;
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) {
+        q += static_cast<int>(hv[j]);
+        const bool before = q <= k - 1;
+        jt += before ? 1 : 0;
+        pt = before ? q : pt;
+      }
+      thr[0] = tid * BPT + jt;
+      thr[1] = pt;
+    }
 #pragma unroll
     for (int j = 0; j < BPT; ++j) {
       const int c = static_cast<int>(hv[j]);
-      if (pos <= k - 1 && k - 1 < pos + c) {  // exactly one bin holds position k-1
-        thr[0] = tid * BPT + j;
-        thr[1] = pos;
-      }
       hv[j] = static_cast<uint32_t>(pos);  // first position of the bin
       pos += c;
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) hrun[q] = make_uint4(hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]);
+    if (tid < kKeyPad) keys[L + tid] = ~uint64_t(0);  // padding read by seg_rank
     __syncthreads();
     // 3. composites into their bins' segments
 #pragma unroll
@@ -354,39 +388,48 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
     const uint32_t tb = static_cast<uint32_t>(thr[0]);
     const int tb0 = thr[1];
     const int tb1 = tb + 1 < kBins ? static_cast<int>(hist[bin_slot(tb + 1)]) : L;
-    // 4. ranks of this part's selected keys (element tid + 1024 * part)
-    {
-      const int e = part;
-      const int i = tid + kTopkThreads * e;
-      uint32_t d = 0u;
-#pragma unroll
-      for (int x = 0; x < EPT; ++x)
-        if (x == e) d = dk[x];
-      const uint32_t b = d >> (32 - kBinBits);
-      if (i < L && b <= tb) {
-        const int b0 = static_cast<int>(hist[bin_slot(b)]);
-        const int b1 = b == tb ? tb1 : static_cast<int>(hist[bin_slot(b + 1)]);
-        const int r = bin_rank(keys, b0, b1, (static_cast<uint64_t>(d) << 32) | static_cast<uint32_t>(i));
-        if (r < k && idx_desc) idx_desc[static_cast<int64_t>(row) * k + r] = static_cast<int64_t>(i);
-      }
-    }
-    // 5. the whole row's selection: every key below the threshold bin (a
-    // wave's 64 consecutive keys -> two bitmap words by ballot, one plain
-    // store each), then the threshold bin's keys of rank < k
+    // 4. the selection bitmap below the threshold bin: a wave's 64
+    // consecutive keys -> two bitmap words by ballot, OR-ed in by one lane
+    // (the threshold bin's bits below may share the words)
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const int i = tid + kTopkThreads * e;
       const uint64_t sel = __ballot(i < L && (dk[e] >> (32 - kBinBits)) < tb);
       const int w0 = (kTopkThreads * e + 64 * wave) >> 5;
-      if (lane == 0 && w0 < nwords) bits[w0] = static_cast<uint32_t>(sel);
-      if (lane == 0 && w0 + 1 < nwords) bits[w0 + 1] = static_cast<uint32_t>(sel >> 32);
+      if (lane == 0 && w0 < nwords && static_cast<uint32_t>(sel)) atomicOr(&bits[w0], static_cast<uint32_t>(sel));
+      if (lane == 0 && w0 + 1 < nwords && static_cast<uint32_t>(sel >> 32))
+        atomicOr(&bits[w0 + 1], static_cast<uint32_t>(sel >> 32));
     }
-    __syncthreads();
+    // 5. the threshold bin's keys of rank < k complete the bitmap
     for (int p = tb0 + tid; p < tb1; p += kTopkThreads) {
       const uint64_t me = keys[p];
-      if (bin_rank(keys, tb0, tb1, me) < k) {
+      if (seg_rank(keys, tb0, tb1, me) < k) {
         const uint32_t i = static_cast<uint32_t>(me & 0xffffffffu);
         atomicOr(&bits[i >> 5], 1u << (i & 31));
+      }
+    }
+    // 6. ranks in bin order.  The slot order inside a bin differs between
+    // the row's workgroups, so the split between them follows bins: this
+    // part ranks the bins that start among its positions [1024 part,
+    // 1024 part + 1024), up to the end of the last of them (a bin holds at
+    // most kBucketMaxBin keys) or of the threshold bin.  A wave's 64
+    // positions share a few bins, so the segment reads are mostly broadcasts.
+    if (idx_desc) {
+      const int plo = kTopkThreads * part;
+      int phi = plo + kTopkThreads;
+      if (phi < tb1) {
+        const uint32_t bl = static_cast<uint32_t>(keys[phi - 1] >> (64 - kBinBits));
+        phi = bl == tb ? tb1 : static_cast<int>(hist[bin_slot(bl + 1)]);
+      }
+      phi = min(phi, tb1);
+      for (int p = plo + tid; p < phi; p += kTopkThreads) {
+        const uint64_t me = keys[p];
+        const uint32_t b = static_cast<uint32_t>(me >> (64 - kBinBits));
+        const int b0 = static_cast<int>(hist[bin_slot(b)]);
+        if (b0 < plo) continue;  // the previous part's bin
+        const int b1 = b == tb ? tb1 : static_cast<int>(hist[bin_slot(b + 1)]);
+        const int r = seg_rank(keys, b0, b1, me);
+        if (r < k) idx_desc[static_cast<int64_t>(row) * k + r] = static_cast<int64_t>(me & 0xffffffffu);
       }
     }
   }
@@ -396,8 +439,8 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
   const int i0 = kTopkThreads * part;
   if (mask) {
     const int64_t mrow = static_cast<int64_t>(row) * L;
-    const int hi = gmx > kBucketMaxBin ? L : min(L, i0 + kTopkThreads);
-    for (int i = (gmx > kBucketMaxBin ? 0 : i0) + tid; i < hi; i += kTopkThreads) {
+    const int hi = nbig ? L : min(L, i0 + kTopkThreads);
+    for (int i = (nbig ? 0 : i0) + tid; i < hi; i += kTopkThreads) {
       const float v = (bits[i >> 5] >> (i & 31)) & 1u ? 1.f : 0.f;
       switch (mask_dtype) {
         case HYDRA_F32: static_cast<float*>(mask)[mrow + i] = v; break;
@@ -410,22 +453,21 @@ __global__ __launch_bounds__(kTopkThreads) void mod_topk_bucket_kernel(
   // word prefixes: exclusive scan of the popcounts of the row's words
   // (nwords <= 256 < 1024: thread t owns word t)
   const int pc = tid < nwords ? __popc(bits[tid]) : 0;
-  int pincl = pc;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int n = __shfl_up(pincl, off, 64);
-    if (lane >= off) pincl += n;
-  }
-  __syncthreads();  // wave_tot reuse
-  if (lane == 63) wave_tot[wave] = pincl;
+  const int pincl = wave_incl_sum(pc);
+  if (lane == 63) wave_pc[wave] = pincl;
   __syncthreads();
   int pbase = 0;
-  for (int w = 0; w < wave; ++w) pbase += wave_tot[w];
+#pragma unroll
+  for (int q = 0; q < kTopkThreads / 256; ++q) {
+    const int4 t = reinterpret_cast<const int4*>(wave_pc)[q];
+    pbase += (4 * q < wave ? t.x : 0) + (4 * q + 1 < wave ? t.y : 0) + (4 * q + 2 < wave ? t.z : 0) +
+             (4 * q + 3 < wave ? t.w : 0);
+  }
   if (tid < nwords) wpre[tid] = static_cast<uint32_t>(pbase + pincl - pc);
   __syncthreads();
   int64_t* orow = idx_sorted + static_cast<int64_t>(row) * k;
-  const int hi = gmx > kBucketMaxBin ? L : min(L, i0 + kTopkThreads);
-  for (int i = (gmx > kBucketMaxBin ? 0 : i0) + tid; i < hi; i += kTopkThreads) {
+  const int hi = nbig ? L : min(L, i0 + kTopkThreads);
+  for (int i = (nbig ? 0 : i0) + tid; i < hi; i += kTopkThreads) {
     const uint32_t wbits = bits[i >> 5];
     if ((wbits >> (i & 31)) & 1u) {
       const int o = static_cast<int>(wpre[i >> 5]) + __popc(wbits & ((1u << (i & 31)) - 1u));
@@ -598,7 +640,8 @@ extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t 
   while (ept * kTopkThreads < L) ept <<= 1;
   const int P = ept * kTopkThreads;
   const bool bucket = L <= kBucketMaxL && getenv("HYDRA_TOPK_BITONIC") == nullptr;
-  const size_t lds = bucket ? sizeof(uint64_t) * P + sizeof(uint32_t) * kBinWords + 2 * sizeof(uint32_t) * (P / 32)
+  const size_t lds = bucket ? sizeof(uint64_t) * (P + kKeyPad) + sizeof(uint32_t) * kBinWords +
+                                2 * sizeof(uint32_t) * (P / 32)
                             : sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);
   const int R = static_cast<int>((L + kTopkThreads - 1) / kTopkThreads);  // bucket kernel: parts per row
   if (lds + 1024 > static_cast<size_t>(max_lds_per_block()))
