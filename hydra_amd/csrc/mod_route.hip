@@ -3,15 +3,17 @@
 // scatter (hydra/routing/mixture_of_depths.py:159-216,
 // hydra/model/framework/blocks.py:243-269).
 //
-// Top-k: one workgroup per row.  Each score becomes a 64-bit composite key
+// Top-k: each score becomes a 64-bit composite key
 //   (~order_preserving_u32(score) << 32) | index
 // so that an ascending sort gives value-descending order with ties resolved
-// by ascending index, i.e. the order of a stable descending sort.  The keys
-// are bitonic-sorted in LDS; the first k are the selection.  The ascending
+// by ascending index, i.e. the order of a stable descending sort.  Rows of
+// up to 8192 keys take the bucket kernel (a counting sort over the keys' top
+// bits in LDS, several workgroups per row; rows whose bins degenerate fall
+// back to a bitonic sort in LDS by one workgroup); longer rows a device-wide
+// radix sort in global memory (mod_topk_large.hip).  The ascending
 // index list comes from a bitmap of the selection and a block prefix count.
-// The sort keeps each thread's keys in registers and only crosses waves
-// through LDS, so a 4096-key row needs 10 barriers instead of 78.
 #include "common.h"
+#include "mod_keys.h"
 
 #include <cstdlib>
 #include <type_traits>
@@ -19,28 +21,6 @@
 namespace hydra {
 
 constexpr int kTopkThreads = 1024;
-
-// Order-preserving map of a float to u32 (ascending), with -0.0 folded into
-// +0.0 and every NaN mapped above +inf (torch.topk treats NaN as largest).
-__device__ __forceinline__ uint32_t score_key_asc(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN
-  if (u == 0x80000000u) u = 0u;                               // -0.0 -> +0.0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave with DPP: row shifts
-// within each 16-lane row, then the broadcasts of lane 15 to rows 1 and 3 and
-// of lane 31 to rows 2 and 3.
-__device__ __forceinline__ int wave_incl_sum(int x) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
-  return x;
-}
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m);
@@ -229,6 +209,7 @@ constexpr int kBins = 1 << kBinBits;
 constexpr int kBinWords = kBins + kBins / 4;
 __device__ __forceinline__ uint32_t bin_slot(uint32_t b) { return b + 4 * (b >> 4); }
 constexpr int kBucketMaxL = 8192;
+constexpr int kLdsMaxL = 16384;  // longest row the bitonic kernel sorts in LDS
 constexpr int kBucketMaxBin = 512;
 constexpr int kKeyPad = 8;  // all-ones keys after the row, read by seg_rank
 
@@ -628,18 +609,26 @@ extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t 
                               void* mask, int score_dtype, int mask_dtype,
                               void* stream) {
   HYDRA_REQUIRE(B >= 0, "mod_topk: negative batch");
-  HYDRA_REQUIRE(L >= 1 && L <= 16384, "mod_topk: need 1 <= L <= 16384");
+  HYDRA_REQUIRE(L >= 1 && L < (int64_t(1) << 31), "mod_topk: need 1 <= L < 2^31");
   HYDRA_REQUIRE(k >= 1 && k <= L, "mod_topk: need 1 <= k <= L");
   HYDRA_REQUIRE(s_rs >= L, "mod_topk: row stride smaller than L");
+  HYDRA_REQUIRE(score_dtype == HYDRA_F32 || score_dtype == HYDRA_BF16 || score_dtype == HYDRA_F16,
+                "mod_topk: unknown score dtype code");
   HYDRA_REQUIRE(mask_dtype == HYDRA_F32 || mask_dtype == HYDRA_BF16 || mask_dtype == HYDRA_F16,
                 "mod_topk: unknown mask dtype code");
   HYDRA_REQUIRE(B <= 65535, "mod_topk: B must be <= 65535");
   if (B == 0) return HYDRA_OK;
   HYDRA_REQUIRE(scores != nullptr, "mod_topk: null scores");
+  // rows beyond the bucket kernel: the device-wide radix sort (the
+  // bitonic kernel stays reachable up to kLdsMaxL as a test switch)
+  const bool force_bitonic = getenv("HYDRA_TOPK_BITONIC") != nullptr;
+  if (L > kLdsMaxL || (L > kBucketMaxL && !force_bitonic))
+    return mod_topk_large(scores, B, L, s_rs, k, idx_desc, idx_sorted, mask, score_dtype, mask_dtype,
+                          static_cast<hipStream_t>(stream));
   int ept = 1;
   while (ept * kTopkThreads < L) ept <<= 1;
   const int P = ept * kTopkThreads;
-  const bool bucket = L <= kBucketMaxL && getenv("HYDRA_TOPK_BITONIC") == nullptr;
+  const bool bucket = L <= kBucketMaxL && !force_bitonic;
   const size_t lds = bucket ? sizeof(uint64_t) * (P + kKeyPad) + sizeof(uint32_t) * kBinWords +
                                 2 * sizeof(uint32_t) * (P / 32)
                             : sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);

@@ -402,7 +402,10 @@ int hydra_mor_route(const void* logits, int64_t n, void* probs, void* logits_out
  * idx_desc: int64 [B, k] in value-descending order (may be NULL);
  * idx_sorted: int64 [B, k] ascending (may be NULL);
  * mask: [B, L] of mask_dtype, 1 for selected tokens else 0 (may be NULL).
- * Limits: 1 <= k <= L <= 16384. */
+ * Limits: 1 <= k <= L < 2^31, B <= 65535; rows longer than 8192 also need
+ * B * L < 2^31 and take a global-memory radix sort whose workspace is
+ * allocated and freed stream-ordered (hipMallocAsync / hipFreeAsync) on
+ * `stream`. */
 int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t s_rs,
                    int64_t k, int64_t* idx_desc, int64_t* idx_sorted,
                    void* mask, int score_dtype, int mask_dtype, void* stream);

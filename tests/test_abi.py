@@ -53,8 +53,10 @@ def test_abi_version_and_error_path():
                   (ctypes.c_int64 * 4)(3, 3, 3, 1), 1, 1, 0, None)
     with pytest.raises(ValueError, match="1 <= k <= L"):
         _lib.call("hydra_mod_topk", None, 1, 10, 10, 11, None, None, None, 0, 0, None)
-    with pytest.raises(ValueError, match="L <= 16384"):
-        _lib.call("hydra_mod_topk", None, 1, 16385, 16385, 5, None, None, None, 0, 0, None)
+    with pytest.raises(ValueError, match="1 <= L"):
+        _lib.call("hydra_mod_topk", None, 1, 0, 16385, 1, None, None, None, 0, 0, None)
+    with pytest.raises(ValueError, match="unknown score dtype"):
+        _lib.call("hydra_mod_topk", None, 1, 16385, 16385, 5, None, None, None, 7, 0, None)
     with pytest.raises(ValueError, match="multiple of n_kv_heads"):
         st = (ctypes.c_int64 * 4)(0, 0, 0, 1)
         _lib.call("hydra_attn_fwd", None, None, None, None, None, None, 0, 1, 3, 2, 8, 16,

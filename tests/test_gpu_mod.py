@@ -39,8 +39,9 @@ def test_topk_c4(cuda):
                                    (2, 16384, 12288), (5, 333, 100), (70, 128, 96),
                                    (3, 8192, 6144), (2, 8193, 7000), (4, 4096, 1)])
 def test_topk_sizes(cuda, monkeypatch, B, L, k, bitonic):
-    """Rows up to 8192 take the bucketed rank kernel (forced bitonic sort as
-    well); longer rows the bitonic kernel."""
+    """Rows up to 8192 take the bucketed rank kernel, longer rows the
+    device-wide radix sort; forced, the bitonic kernel takes rows up to
+    16384."""
     if bitonic:
         monkeypatch.setenv("HYDRA_TOPK_BITONIC", "1")
     g = torch.Generator().manual_seed(L + k)
@@ -64,6 +65,31 @@ def test_topk_degenerate_bins(cuda, pattern):
         s = torch.linspace(-5, 5, L).repeat(3, 1)
     for k in (1, 1000, 3072, L):
         _check_topk(s, k, cuda)
+
+
+@pytest.mark.parametrize("B,L,k", [(3, 16385, 12000), (2, 65536, 49152), (1, 100003, 1),
+                                   (2, 40000, 40000), (4, 20000, 5000)])
+def test_topk_long_rows(cuda, B, L, k):
+    """Rows longer than 8192 take the radix sort in global memory."""
+    g = torch.Generator().manual_seed(L + k)
+    _check_topk(omod.make_tied_logits(B, L, 0.05, g), k, cuda)
+
+
+def test_topk_long_rows_ties_specials_bf16(cuda):
+    """Long rows: all-equal scores (ties resolved by index alone), NaN /
+    +-inf / signed zeros sprinkled into random scores, and bf16 scores with
+    a bf16 mask."""
+    L = 30000
+    g = torch.Generator().manual_seed(5)
+    for k in (1, 7777, L):
+        _check_topk(torch.full((2, L), -0.5), k, cuda)
+    s = torch.randn(2, L, generator=g)
+    pos = torch.randperm(L, generator=g)[:64]
+    specials = torch.tensor([float("nan"), float("inf"), float("-inf"), 0.0, -0.0, 3.0, 3.0, -3.0])
+    s[:, pos] = specials.repeat(8)
+    for k in (1, 5, 12000):
+        _check_topk(s, k, cuda)
+    _check_topk(torch.randn(3, L, generator=g).to(torch.bfloat16), 20000, cuda, mask_dtype=torch.bfloat16)
 
 
 def test_topk_special_values(cuda):
