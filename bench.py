@@ -97,10 +97,12 @@ class C3Step:
         self.out = torch.empty(B, S, mm.latent_dim, dtype=torch.bfloat16, device=dev)
         # |q.k| bound from QK-norm, taken by the kernel from the temperature
         self.temp = mm.key_temperature.detach()
+        # o_proj weight in the output-projection kernel's fragment order
+        self.w_o = mm._packed_o_proj()
 
     @torch.no_grad()
     def __call__(self, ev=None, x=None):
-        from hydra_amd.attention.backends.ccgqa.ops import attention_forward, ccgqa_prep
+        from hydra_amd.attention.backends.ccgqa.ops import attention_forward, ccgqa_prep, output_projection
 
         m = self.m
         if ev:
@@ -117,7 +119,7 @@ class C3Step:
         attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view, bound_temperature=self.temp)
         if ev:
             ev[3].record()
-        y = F.linear(self.out, m.o_proj.weight)
+        y = output_projection(self.out, m.o_proj.weight, self.w_o)
         if ev:
             ev[4].record()
         return y

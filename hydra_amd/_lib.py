@@ -26,6 +26,7 @@ CCGQA_W_TILED = 64
 MASK_NONE, MASK_KEY_PADDING, MASK_REFERENCE_SDPA = 0, 1, 2
 SCATTER_ADD, SCATTER_REPLACE, SCATTER_ADD_SEQ = 0, 1, 2
 NORM_NONE, NORM_RMS, NORM_ADA = 0, 1, 2
+LINEAR_W_TILED = 1
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -52,6 +53,7 @@ SIGNATURES = {
                        _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _P, _I, _I, _P],
     "hydra_attn_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                        _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
+    "hydra_linear_fwd": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],
     "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
     "hydra_ccgqa_prep_bwd": [_P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P,
@@ -112,6 +114,20 @@ def call(name: str, *args) -> None:
     rc = getattr(lib, name)(*args)
     if rc != OK:
         msg = lib.hydra_last_error().decode(errors="replace")
+        if rc == ERR_ARG:
+            raise ValueError(f"{name}: {msg}")
+        raise HydraError(f"{name} failed ({rc}): {msg}")
+
+
+def call_status(name: str, *args) -> int:
+    """Call an entry point and return its status (for callers that handle
+    HYDRA_ERR_UNSUPPORTED themselves); check() raises for the others."""
+    return int(getattr(load(), name)(*args))
+
+
+def check(rc: int, name: str) -> None:
+    if rc != OK:
+        msg = load().hydra_last_error().decode(errors="replace")
         if rc == ERR_ARG:
             raise ValueError(f"{name}: {msg}")
         raise HydraError(f"{name} failed ({rc}): {msg}")

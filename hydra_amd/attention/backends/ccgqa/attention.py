@@ -35,7 +35,8 @@ from ...._lib import CCGQA_V_TRANSPOSED, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_R
 from .autograd import ccgqa_prep_train
 from .kernels.fused_attention import CCGQAAttentionFused
 from .kernels.fused_conv import OptimizedConvSequence
-from .ops import attention_forward, ccgqa_prep, pack_conv_weight, prep_flags, tiled_weights_ok
+from .ops import (attention_forward, ccgqa_prep, linear_weight_ok, output_projection, pack_conv_weight,
+                  pack_linear_weight, prep_flags, tiled_weights_ok)
 
 # Kept for callers that probe these names (attention.py:13-28).
 FUSED_KERNELS_AVAILABLE = True
@@ -144,7 +145,8 @@ class CCGQAAttention(nn.Module):
         # A padding mask has no backward here (the attention backward takes
         # none): a recorded graph through it raises instead of going silent.
         out = track(out, x, self.qkv_proj.weight, self.key_temperature, *convw)
-        out = F.linear(out, self.o_proj.weight)
+        w_o = self.o_proj.weight
+        out = output_projection(out, w_o, self._packed_o_proj() if linear_weight_ok(w_o) else None)
         if self.output_scale != 1.0:
             out = out * self.output_scale
         return out
@@ -177,6 +179,17 @@ class CCGQAAttention(nn.Module):
         if cache is None or cache[0] != key:
             cache = (key, tuple(pack_conv_weight(w, dtype, tiled) for w in convw))
             self._packed_cache = cache
+        return cache[1]
+
+    def _packed_o_proj(self):
+        """o_proj's weight in hydra_linear_fwd's fragment order, rebuilt only
+        when the weight changes (tensor version counter) or moves."""
+        w = self.o_proj.weight
+        key = (w.data_ptr(), w._version, w.device, w.dtype)
+        cache = getattr(self, "_packed_o_cache", None)
+        if cache is None or cache[0] != key:
+            cache = (key, pack_linear_weight(w))
+            self._packed_o_cache = cache
         return cache[1]
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,

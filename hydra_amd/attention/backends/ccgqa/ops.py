@@ -1,11 +1,12 @@
 """Thin tensor-level wrappers over the CCGQA entry points of the C ABI
-(hydra_ccgqa_prep_fwd, hydra_attn_fwd).  Shapes and dtypes are checked
+(hydra_ccgqa_prep_fwd, hydra_attn_fwd, hydra_linear_fwd).  Shapes and dtypes are checked
 here; strides, pointers and the current stream go to the library."""
 from __future__ import annotations
 
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from ...._lib import (CCGQA_CONVS, CCGQA_QK_MEAN, CCGQA_QK_NORM, CCGQA_ROPE,
                       CCGQA_V_TRANSPOSED, CCGQA_VALUE_SHIFT, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_NONE,
@@ -185,6 +186,48 @@ def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: t
                   _lib.strides(out), _lib.strides(grad_out), _lib.strides(dq), _lib.strides(dk),
                   _lib.strides(dv), 1 if causal else 0, sc, _lib.dtype_code(q), _lib.stream(q))
     return dq, dk, dv
+
+
+def linear_weight_ok(weight: torch.Tensor) -> bool:
+    """Whether hydra_linear_fwd takes this [N, K] weight (bf16, K in
+    {64, 128, 256}, N % 64 == 0)."""
+    N, K = weight.shape
+    return weight.dtype == torch.bfloat16 and K in (64, 128, 256) and N % 64 == 0
+
+
+def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
+    """[N, K] -> the MFMA-fragment order hydra_linear_fwd reads with
+    HYDRA_LINEAR_W_TILED: [N/32, K/16, 2, 32, 8], element [j, s, h, n, e] =
+    weight[32 j + n, 16 s + 8 h + e]."""
+    N, K = weight.shape
+    return (weight.detach().reshape(N // 32, 32, K // 16, 2, 8).permute(0, 2, 3, 1, 4)
+            .contiguous())
+
+
+def output_projection(x: torch.Tensor, weight: torch.Tensor,
+                      packed: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """F.linear(x, weight) without bias: CCGQAAttention's o_proj
+    (attention.py:329-331).  bf16 rows of width 64, 128 or 256 with
+    weight.shape[0] % 64 == 0 go to hydra_linear_fwd (with `packed`, the
+    weight already in pack_linear_weight's order; else it is packed here);
+    other shapes (and a recorded autograd graph, which the kernel has no
+    backward for) stay on the library GEMM, as in the reference."""
+    N, K = weight.shape
+    if (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad)) or \
+            x.dtype != torch.bfloat16 or not linear_weight_ok(weight) or x.shape[-1] != K:
+        return F.linear(x, weight)
+    _lib.require_gpu("output_projection", x, weight, packed)
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w = pack_linear_weight(weight) if packed is None else packed
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
+    rc = _lib.call_status("hydra_linear_fwd", x2.data_ptr(), x2.stride(0), w.data_ptr(), K, y.data_ptr(), N,
+                          x2.shape[0], N, K, _lib.LINEAR_W_TILED, _lib.BF16, _lib.stream(x))
+    if rc == _lib.ERR_UNSUPPORTED:  # unaligned rows
+        return F.linear(x, weight)
+    _lib.check(rc, "hydra_linear_fwd")
+    return y
 
 
 def qk_norm_score_bound(temperature: float) -> float:

@@ -132,4 +132,4 @@ extern "C" const char* hydra_last_error(void) {
   return hydra::g_last_error.c_str();
 }
 
-extern "C" int hydra_abi_version(void) { return 107; }
+extern "C" int hydra_abi_version(void) { return 108; }

@@ -312,6 +312,21 @@ int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                    const int64_t* gos, const int64_t* gqs, const int64_t* gks,
                    const int64_t* gvs, int causal, float scale, int dtype, void* stream);
 
+#define HYDRA_LINEAR_W_TILED 1 /* W in MFMA-fragment order (below)             */
+
+/* Output projection y = x W^T (F.linear without bias), the CCGQA o_proj
+ * (attention.py:329-331: out.reshape(B, S, L) @ o_proj.weight^T).  x: [M, K]
+ * (row stride x_rs), y: [M, N] (row stride y_rs), W: [N, K] (row stride
+ * w_rs), or with HYDRA_LINEAR_W_TILED packed as [N/32][K/16][2][32][8]
+ * (element [j][s][h][n][e] = W[32 j + n][16 s + 8 h + e]; w_rs unused), the
+ * layout the kernel loads with one coalesced 16-byte read per lane and
+ * fragment.  Takes bf16 with K in {64, 128, 256}, N % 64 == 0 and 16-byte
+ * aligned rows; returns HYDRA_ERR_UNSUPPORTED for anything else (the caller
+ * then uses a library GEMM).  fp32 accumulation, one rounding. */
+int hydra_linear_fwd(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y,
+                     int64_t y_rs, int64_t M, int64_t N, int64_t K, int flags, int dtype,
+                     void* stream);
+
 /* ---- LM-head loss (hydra/kernels/fused_ops.py) ------------------------- */
 
 /* Token-row softmax cross-entropy of a logits block x [rows, vocab] (unit
