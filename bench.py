@@ -19,8 +19,10 @@ Also reported on the same line:
   stages        per-stage average durations of the eager step;
   fused_ops     config 2 RMSNorm / RoPE / SwiGLU in HBM GB/s and % of peak
                 (buffers rotated over > 512 MB so the 256 MB MALL cannot
-                serve repeats);
-  mod           config 4 top-k / gather / residual scatter;
+                serve repeats), each beside the same-device time of a plain
+                non-temporal copy of its bytes (copy_ms, pct_of_copy);
+  mod           config 4 top-k / gather / residual scatter (with the same
+                copy figures);
   c1_block      config 1: embedding + HydraBlock (CCGQA dim 512, 8/2 heads
                 of 16, SwiGLU hidden 1365) forward in fp32, B2 x S512,
                 tokens/s (a HIP graph of the steps), with the oracle's CPU
@@ -290,7 +292,41 @@ def bench_fused_ops(dev, iters=60):
     res.update(_bench_fused_backward(dev, g, iters))
     for v in res.values():
         v["pct_peak"] = 100.0 * v["GBs"] / HBM_PEAK_GBS
+    _annotate_copy_ceiling(dev, res, iters)
     return res
+
+
+def _copy_ceiling_ms(dev, nbytes, iters):
+    """Time of hydra_stream_copy moving nbytes in total (half read, half
+    written) on this device, with rotating buffers (>= ~600 MB, past the
+    L2 and the 256 MB Infinity Cache), graph-replayed like the kernels."""
+    from hydra_amd import _lib
+
+    half = (nbytes // 2 + 15) // 16 * 16
+    nsets = max(4, -(-600_000_000 // (2 * half)))
+    sets = [(torch.empty(half, dtype=torch.uint8, device=dev), torch.empty(half, dtype=torch.uint8, device=dev))
+            for _ in range(nsets)]
+    ms = _time_rotating(lambda a, b: _lib.call("hydra_stream_copy", a.data_ptr(), b.data_ptr(), half,
+                                               _lib.stream(a)), sets, iters)
+    del sets
+    return ms
+
+
+def _annotate_copy_ceiling(dev, res, iters):
+    """Per HBM-bound kernel: the same-device copy time of its algorithmic
+    bytes (half each way) and the kernel's rate as a percentage of that
+    copy's -- the practical ceiling of a one-pass kernel, which varies from
+    box to box (62-73% of 8 TB/s measured at ~50 MB)."""
+    cache = {}
+    for v in res.values():
+        if "GBs" not in v:
+            continue
+        nb = v["bytes"]
+        if nb not in cache:
+            cache[nb] = _copy_ceiling_ms(dev, nb, iters)
+        v["copy_ms"] = cache[nb]
+        v["copy_pct_peak"] = 100.0 * nb / cache[nb] / 1e6 / HBM_PEAK_GBS
+        v["pct_of_copy"] = 100.0 * cache[nb] / v["ms"]
 
 
 def bench_attention_backward(dev, iters=20):
@@ -421,6 +457,7 @@ def bench_mod(dev, iters=50):
     ms = _time_rotating(lambda h, y: weighted_residual_scatter(h, y, idx), list(zip(xs, ys)), iters)
     nb = 3 * B * k * D * 2
     res["scatter"] = {"ms": ms, "bytes": nb, "GBs": nb / ms / 1e6, "pct_peak": 100 * nb / ms / 1e6 / HBM_PEAK_GBS}
+    _annotate_copy_ceiling(dev, res, iters)
     return res
 
 

@@ -68,6 +68,7 @@ SIGNATURES = {
     "hydra_mod_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P],
     "hydra_mod_gather": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_mod_scatter": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
+    "hydra_stream_copy": [_P, _P, _I64, _P],
 }
 
 _lib = None

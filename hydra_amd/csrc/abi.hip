@@ -132,4 +132,31 @@ extern "C" const char* hydra_last_error(void) {
   return hydra::g_last_error.c_str();
 }
 
-extern "C" int hydra_abi_version(void) { return 108; }
+extern "C" int hydra_abi_version(void) { return 109; }
+
+// ---- same-device HBM copy (measurement aid) ---------------------------------
+// One 16-byte chunk per thread, non-temporal load and store, 256-thread
+// blocks: the fastest plain copy form measured for tens of MB on gfx950
+// (non-temporal 10.0 us against 11.4 us cached for 25 MB each way).
+namespace hydra {
+namespace {
+__global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* __restrict__ src,
+                                                          uint4* __restrict__ dst, int64_t n) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t < n) st16raw<true>(dst + t, ld16raw<true>(src + t));
+}
+}  // namespace
+}  // namespace hydra
+
+extern "C" int hydra_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  using namespace hydra;
+  HYDRA_REQUIRE(bytes >= 0 && bytes % 16 == 0, "stream_copy: bytes must be a non-negative multiple of 16");
+  if (bytes == 0) return HYDRA_OK;
+  HYDRA_REQUIRE(src && dst, "stream_copy: null pointer");
+  HYDRA_REQUIRE(aligned16(src) && aligned16(dst), "stream_copy: pointers must be 16-byte aligned");
+  const int64_t n = bytes / 16;
+  HYDRA_REQUIRE((n + 255) / 256 < (int64_t(1) << 31), "stream_copy: too large");
+  stream_copy_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint4*>(src), static_cast<uint4*>(dst), n);
+  return check_launch("stream_copy_kernel");
+}

@@ -550,38 +550,39 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_kernel(
   }
 }
 
-// Weight gradient from the n partial rows, in one launch: a block of 16
-// waves per 64-column strip, wave w adding partial rows w, w+16, .. (loads
-// unrolled so several are in flight), then the 16 waves' sums in order;
-// clamped.  Deterministic.
-constexpr int kRmsBwdWaves = 16;
+// Weight gradient from the n partial rows, in one launch: a block of 1024
+// threads per 32-column strip (each row segment one 128-byte line), thread
+// (c, g) adding partial rows g, g + 32, .. of column c in order (8 loads in
+// flight), then the 32 sums of each column in order through LDS; clamped.
+// Deterministic.  After the main kernel: 19.9 us for both launches at
+// [16384, 768] against 22.5 with 64-column strips of 16 waves (12 blocks).
+constexpr int kRmsBwdCols = 32;
+constexpr int kRmsBwdGroups = 1024 / kRmsBwdCols;
 template <typename GT>
-__global__ __launch_bounds__(64 * kRmsBwdWaves) void rms_norm_bwd_w_kernel(const float* __restrict__ part,
-                                                                          GT* __restrict__ gw, int n, int dim) {
-  __shared__ float red[kRmsBwdWaves][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + lane;
+__global__ __launch_bounds__(1024) void rms_norm_bwd_w_kernel(const float* __restrict__ part,
+                                                             GT* __restrict__ gw, int n, int dim) {
+  constexpr int U = 8;
+  __shared__ float red[kRmsBwdGroups][kRmsBwdCols];
+  const int c = threadIdx.x % kRmsBwdCols, grp = threadIdx.x / kRmsBwdCols;
+  const int col = blockIdx.x * kRmsBwdCols + c;
   float s = 0.f;
   if (col < dim) {
-    int r = wave;
-    for (; r + 3 * kRmsBwdWaves < n; r += 4 * kRmsBwdWaves) {
-      const float a = part[static_cast<int64_t>(r) * dim + col];
-      const float b = part[static_cast<int64_t>(r + kRmsBwdWaves) * dim + col];
-      const float c = part[static_cast<int64_t>(r + 2 * kRmsBwdWaves) * dim + col];
-      const float d = part[static_cast<int64_t>(r + 3 * kRmsBwdWaves) * dim + col];
-      s += a;
-      s += b;
-      s += c;
-      s += d;
-    }
-    for (; r < n; r += kRmsBwdWaves) s += part[static_cast<int64_t>(r) * dim + col];
-  }
-  red[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0 && col < dim) {
-    float t = 0.f;
+    int r = grp;
+    for (; r + kRmsBwdGroups * (U - 1) < n; r += kRmsBwdGroups * U) {
+      float a[U];
 #pragma unroll
-    for (int w = 0; w < kRmsBwdWaves; ++w) t += red[w][lane];
+      for (int u = 0; u < U; ++u) a[u] = part[static_cast<int64_t>(r + kRmsBwdGroups * u) * dim + col];
+#pragma unroll
+      for (int u = 0; u < U; ++u) s += a[u];
+    }
+    for (; r < n; r += kRmsBwdGroups) s += part[static_cast<int64_t>(r) * dim + col];
+  }
+  red[grp][c] = s;
+  __syncthreads();
+  if (threadIdx.x < kRmsBwdCols && col < dim) {
+    float t = 0.f;
+#pragma unroll 8
+    for (int g = 0; g < kRmsBwdGroups; ++g) t += red[g][c];
     gw[col] = from_f32<GT>(fminf(fmaxf(t, -100.f), 100.f));
   }
 }
@@ -625,19 +626,22 @@ template <typename GT>
 static int rms_bwd_reduce_w(const float* part, GT* gw, int n, int dim, hipStream_t st) {
   const int rc0 = check_launch("rms_norm_bwd_kernel");
   if (rc0 != HYDRA_OK) return rc0;
-  rms_norm_bwd_w_kernel<GT><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(part, gw, n, dim);
+  rms_norm_bwd_w_kernel<GT><<<dim3((dim + kRmsBwdCols - 1) / kRmsBwdCols), 1024, 0, st>>>(part, gw, n, dim);
   return check_launch("rms_norm_bwd_w_kernel");
 }
 
 // Partial rows of the weight gradient (fp32 [n][dim]) the two backward
-// paths write: at most kRmsBwdParts rows for any shape.
-constexpr int kRmsBwdParts = 512;
+// paths write: at most kRmsBwdParts rows for any shape.  768 = 3 resident
+// 4-wave blocks on each of 256 CUs at 144 VGPRs (dim 768 bf16): one full
+// wave of blocks, no tail (512 blocks of two row groups: 18.1 us, 768 of
+// one: 16.7 us; 896 and 1024 blocks, which do not all fit at once: 20 us).
+constexpr int kRmsBwdParts = 768;
 
 template <typename T, typename WT, int LPR, int CPL>
 static int launch_rms_bwd_vec(const T* X, const WT* W, const T* GY, T* GX, WT* GW, float* part,
                               int64_t rows, int nvec, int dim, int64_t x_rs, int64_t gy_rs,
                               int64_t gx_rs, float eps, hipStream_t st) {
-  constexpr int RI = CPL >= 4 ? 1 : (CPL >= 2 ? 2 : 4);  // row groups per wave per step
+  constexpr int RI = CPL >= 3 ? 1 : (CPL == 2 ? 2 : 4);  // row groups per wave per step
   constexpr int RPB = (kBlock / 64) * (64 / LPR) * RI;
   // A fixed number of blocks (from the shape only), so the summation order
   // of the weight gradient does not depend on the device.
@@ -954,7 +958,7 @@ static int rms_norm_bwd_body(const void* x, const void* w, const void* grad_y, v
     // no rows: the weight gradient is zero (a fill kernel, not a memset, so
     // the call can sit in a captured graph)
     return HYDRA_DISPATCH_DTYPE(w_dtype, GT, [&] {
-      rms_norm_bwd_w_kernel<GT><<<dim3((dim + 63) / 64), 64 * kRmsBwdWaves, 0, st>>>(
+      rms_norm_bwd_w_kernel<GT><<<dim3(static_cast<unsigned>((dim + kRmsBwdCols - 1) / kRmsBwdCols)), 1024, 0, st>>>(
           nullptr, static_cast<GT*>(grad_w), 0, static_cast<int>(dim));
       return check_launch("rms_norm_bwd_w_kernel");
     });
@@ -984,7 +988,7 @@ static int rms_norm_bwd_check(const void* x, const void* w, const void* grad_y, 
 // ---- allocation-free variant ----------------------------------------------
 // hydra_rms_norm_bwd_noalloc keeps the weight-gradient partial rows in this
 // file-scope device array instead of the library's growable workspace, so
-// the call allocates nothing.  8 MiB per device (kRmsBwdParts rows of up to
+// the call allocates nothing.  12 MiB per device (kRmsBwdParts rows of up to
 // kNoAllocMaxDim fp32), held until the process ends.  Every partial row the
 // reduction reads is written earlier in the same call, so nothing has to be
 // cleared between calls; calls that overlap on one device share the array and

@@ -106,7 +106,7 @@ int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* g
                        int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream);
 
 /* hydra_rms_norm_bwd without any allocation: the same kernels and results
- * (bit for bit), with the weight-gradient partials in a fixed 8 MiB device
+ * (bit for bit), with the weight-gradient partials in a fixed 12 MiB device
  * array of the library (one per device, held until the process ends) instead
  * of the growable workspace.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
@@ -454,6 +454,16 @@ int hydra_mod_scatter(void* out, const void* y, const int64_t* idx,
                       const float* w, int64_t B, int64_t L, int64_t k,
                       int64_t D, int64_t o_bs, int64_t o_ls, int mode,
                       int dtype, void* stream);
+
+/* ---- measurement aid ----------------------------------------------------- */
+
+/* dst[0, bytes) = src[0, bytes): a plain device-to-device copy with
+ * non-temporal 16-byte loads and stores, one chunk per thread.  No
+ * counterpart in the reference: it gives callers (bench.py) the copy rate
+ * of the same bytes on the same device, the practical ceiling of a
+ * one-pass HBM-bound kernel.  bytes % 16 == 0, both pointers 16-byte
+ * aligned, the ranges must not overlap. */
+int hydra_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 #ifdef __cplusplus
 }

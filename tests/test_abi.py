@@ -43,7 +43,7 @@ def test_abi_version_and_error_path():
     from hydra_amd import _lib
 
     lib = _lib.load()
-    assert lib.hydra_abi_version() == 108
+    assert lib.hydra_abi_version() == 109
     # dim = 0 is rejected before any HIP call
     rc = lib.hydra_rms_norm_fwd(None, None, None, 4, 0, 0, 0, ctypes.c_float(1e-6), 1, None)
     assert rc == _lib.ERR_ARG
@@ -76,3 +76,8 @@ def test_abi_version_and_error_path():
     assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 3, 64, _lib.BF16) == 0
     # empty work is a no-op success
     _lib.call("hydra_swiglu_fwd", None, None, None, 0, 8, 8, 8, 8, 1, None)
+    _lib.call("hydra_stream_copy", None, None, 0, None)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        _lib.call("hydra_stream_copy", 16, 32, 24, None)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _lib.call("hydra_stream_copy", 8, 32, 32, None)
