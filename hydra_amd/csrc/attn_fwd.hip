@@ -728,12 +728,6 @@ __device__ __forceinline__ void attn_fwd_kp_body(
   const int n = lane & 31, hf = lane >> 5;
   const bool walk = CAUSAL && MASK != 2;
   const int p = blockIdx.x / BH, bk = blockIdx.x - p * BH;
-  // Issue priority rises with the group: a SIMD's arbiter otherwise favours
-  // the oldest wave, so group 0 finishes its tile ~500 cycles before group 2
-  // and waits at the step's barrier (shader-clock stamps per wave at config
-  // 3: 2050 / 2300 / 2560 cycles of tile work in a 3350-cycle step).  Worth
-  // ~1% (46.1 against 46.5 us, five alternating runs on one box).
-  if (grp > 0) __builtin_amdgcn_s_setprio(grp > 3 ? 3 : grp);
   const int wg = attn_pos_item(p, nwg, false);
   const int nkb = attn_tiles<NW>(wg, S, G, ntasks, walk);
   const int b = bk / Hkv, kvh = bk - b * Hkv;
