@@ -52,3 +52,45 @@ def test_ccgqa_forward_graph_replays_match_eager(cuda):
     torch.cuda.synchronize()
     assert torch.equal(y, want2)
     del graph
+
+
+def test_hydra_model_forward_graph_replays_match_eager(cuda):
+    """The config-5 model path (MoR blocks, MoD middle blocks, tied LM head)
+    captured in a HIP graph: routing is capacity-based, so every shape is
+    fixed and the forward has no host synchronisation.  Replays with eager
+    work in between equal the eager logits bit for bit, and a replay on new
+    token ids equals the eager forward of those ids.  bench.py times config
+    5 this way."""
+    from test_gpu_blocks import _model_from_checkpoint
+
+    m, z, meta = _model_from_checkpoint(cuda, torch.bfloat16)
+    g = torch.Generator(device=cuda).manual_seed(5)
+    ids = torch.from_numpy(z["ids"]).to(cuda)
+    with torch.no_grad():
+        m(ids)
+        want = m(ids).clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            m(ids)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y = m(ids)
+    for r in range(3):
+        noise = torch.randn(4096, 4096, device=cuda, generator=g).sum()
+        torch.cuda.synchronize()
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), f"replay {r} differs from the eager forward"
+        del noise
+    ids2 = torch.randint(0, meta["vocab_size"], ids.shape, device=cuda, generator=g)
+    with torch.no_grad():
+        want2 = m(ids2).clone()
+    ids.copy_(ids2)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, want2)
+    del graph
