@@ -208,14 +208,13 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
 
 // ===========================================================================
 // VALU variant for the shapes the MFMA kernel does not take (fp32, fp16,
-// odd head layouts): TT = 8 tokens per workgroup, fp32 LDS rows.  A thread
+// odd head layouts): TT = 8 (or 4) tokens per workgroup, fp32 LDS rows.  A thread
 // owns one output channel at a time and keeps the tile's TT (conv2) or
 // TT + 2 (conv1) token accumulators in registers, so each weight element it
 // reads (tap-major rows, 4 consecutive input channels per step) feeds TT
 // FMAs, and the token rows come from LDS as 16-byte broadcast reads.
 // Rounding points as in ccgqa_prep_generic_kernel.
 // ===========================================================================
-constexpr int kPrepVecTT = 8;
 
 template <typename T>
 __device__ __forceinline__ void ld4(const T* p, float* out) {
@@ -230,14 +229,13 @@ __device__ __forceinline__ void ld4(const T* p, float* out) {
   }
 }
 
-template <typename T>
+template <typename T, int TT>
 __global__ __launch_bounds__(256) void ccgqa_prep_vec_kernel(
     const T* __restrict__ qkv, int64_t qkv_rs, const T* __restrict__ wq1,
     const T* __restrict__ wq2, const T* __restrict__ wk1, const T* __restrict__ wk2,
     const T* __restrict__ temp, const float* __restrict__ cs, const float* __restrict__ sn,
     int64_t cs_rs, T* __restrict__ qo, T* __restrict__ ko, T* __restrict__ vo, int S,
     int Hq, int Hkv, int hd, int flags) {
-  constexpr int TT = kPrepVecTT;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   float* sm = reinterpret_cast<float*>(smem_raw);
   const int L = Hq * hd, K = Hkv * hd, CW = L + K;
@@ -1145,23 +1143,33 @@ static int launch_prep_vec(const void* qkv, int64_t qkv_rs, const void* wq1, con
                            const float* sn, int64_t cs_rs, void* qo, void* ko, void* vo, int64_t B,
                            int64_t S, int64_t Hq, int64_t Hkv, int64_t hd, int flags,
                            size_t max_lds, hipStream_t st) {
-  constexpr int TT = kPrepVecTT;
+  // 8-token tiles, or 4 when 8 would leave CUs without a workgroup (each
+  // workgroup's time is mostly its weight reads, the same for both).
   const int64_t CW = (Hq + Hkv) * hd;
-  const size_t lds = static_cast<size_t>(3 * TT + 6) * CW * sizeof(float);
-  if (lds > max_lds) return -1;
-  auto kern = ccgqa_prep_vec_kernel<T>;
-  if (lds > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(lds)) != hipSuccess)
-    return -1;
-  const int threads = static_cast<int>(std::min<int64_t>(256, (CW + 63) / 64 * 64));
-  const dim3 grid(static_cast<unsigned>((S + TT - 1) / TT), static_cast<unsigned>(B));
-  kern<<<grid, threads, lds, st>>>(
-      static_cast<const T*>(qkv), qkv_rs, static_cast<const T*>(wq1), static_cast<const T*>(wq2),
-      static_cast<const T*>(wk1), static_cast<const T*>(wk2), static_cast<const T*>(temp), cs, sn,
-      cs_rs, static_cast<T*>(qo), static_cast<T*>(ko), static_cast<T*>(vo), (int)S, (int)Hq,
-      (int)Hkv, (int)hd, flags);
-  return check_launch("ccgqa_prep_vec_kernel");
+  const int tt = B * ((S + 7) / 8) < device_cus() ? 4 : 8;
+  auto go = [&](auto tt_tag) -> int {
+    constexpr int TT = decltype(tt_tag)::value;
+    const size_t lds = static_cast<size_t>(3 * TT + 6) * CW * sizeof(float);
+    if (lds > max_lds) return -1;
+    auto kern = ccgqa_prep_vec_kernel<T, TT>;
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+      return -1;
+    const int threads = static_cast<int>(std::min<int64_t>(256, (CW + 63) / 64 * 64));
+    const dim3 grid(static_cast<unsigned>((S + TT - 1) / TT), static_cast<unsigned>(B));
+    kern<<<grid, threads, lds, st>>>(
+        static_cast<const T*>(qkv), qkv_rs, static_cast<const T*>(wq1), static_cast<const T*>(wq2),
+        static_cast<const T*>(wk1), static_cast<const T*>(wk2), static_cast<const T*>(temp), cs, sn,
+        cs_rs, static_cast<T*>(qo), static_cast<T*>(ko), static_cast<T*>(vo), (int)S, (int)Hq,
+        (int)Hkv, (int)hd, flags);
+    return check_launch("ccgqa_prep_vec_kernel");
+  };
+  if (tt == 4) {
+    const int rc = go(std::integral_constant<int, 4>());
+    if (rc != -1) return rc;
+  }
+  return go(std::integral_constant<int, 8>());
 }
 
 template <typename T>
