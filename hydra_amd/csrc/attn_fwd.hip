@@ -1248,20 +1248,52 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(
   const int kend = walk ? min(S, sb * RW + RW) : S;
   const T* kb = k + b * ks0 + j * ks1;
   const T* vb = v + b * vs0 + j * vs1;
-  for (int t0 = 0; t0 < kend; t0 += TK) {
-    __syncthreads();
-    for (int i = tid; i < TK * HD; i += 256) {
+  // Head dims up to 64: the next tile's K and V are loaded into registers
+  // before this tile's arithmetic, so the loads' latency hides behind it
+  // (one tile in flight; written to LDS after the next barrier).
+  constexpr bool PF = HD <= 64;
+  constexpr int PER = PF ? TK * HD / 256 : 1;  // elements per thread per tile
+  static_assert(!PF || TK * HD % 256 == 0, "whole tile per pass");
+  float kpre[PER], vpre[PER];
+  auto prefetch = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = tid + 256 * u;
       const int kk = i / HD, d = i - kk * HD;
       const int t = t0 + kk;
       const bool in = t < S;
-      Ks[kk * KP + d] = in ? to_f32(kb[static_cast<int64_t>(t) * ks2 + d]) : 0.f;
-      Vs[kk * KP + d] = in ? to_f32(vb[static_cast<int64_t>(t) * vs2 + d * vs3]) : 0.f;
+      kpre[u] = in ? to_f32(kb[static_cast<int64_t>(t) * ks2 + d]) : 0.f;
+      vpre[u] = in ? to_f32(vb[static_cast<int64_t>(t) * vs2 + d * vs3]) : 0.f;
+    }
+  };
+  if constexpr (PF) prefetch(0);
+  for (int t0 = 0; t0 < kend; t0 += TK) {
+    __syncthreads();
+    if constexpr (PF) {
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int i = tid + 256 * u;
+        const int kk = i / HD, d = i - kk * HD;
+        Ks[kk * KP + d] = kpre[u];
+        Vs[kk * KP + d] = vpre[u];
+      }
+    } else {
+      for (int i = tid; i < TK * HD; i += 256) {
+        const int kk = i / HD, d = i - kk * HD;
+        const int t = t0 + kk;
+        const bool in = t < S;
+        Ks[kk * KP + d] = in ? to_f32(kb[static_cast<int64_t>(t) * ks2 + d]) : 0.f;
+        Vs[kk * KP + d] = in ? to_f32(vb[static_cast<int64_t>(t) * vs2 + d * vs3]) : 0.f;
+      }
     }
     if (mask_mode != HYDRA_MASK_NONE && tid < TK) {
       const int t = t0 + tid;
       Vis[tid] = t < S ? (kmask[static_cast<int64_t>(b) * S + t] != 0) : 0;
     }
     __syncthreads();
+    if constexpr (PF) {
+      if (t0 + TK < kend) prefetch(t0 + TK);
+    }
     float x[KPT];
     float mt = m;
 #pragma unroll
