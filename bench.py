@@ -65,7 +65,8 @@ def _events(n):
 class C3Step:
     """One CCGQA attention forward at config 3, stage by stage."""
 
-    def __init__(self, dev, B=4, S=4096, dim=1024, n_heads=4, n_kv_heads=1, comp=4, seed=0):
+    def __init__(self, dev, B=4, S=4096, dim=1024, n_heads=4, n_kv_heads=1, comp=4, seed=0,
+                 temperature=1.0):
         from hydra_amd.attention import CCGQAAttention
 
         g = torch.Generator().manual_seed(seed)
@@ -76,7 +77,7 @@ class C3Step:
             x = torch.randn(B, S, dim, generator=g)
             for name, p in m.named_parameters():
                 if name == "key_temperature":
-                    p.fill_(1.0)
+                    p.fill_(temperature)
                 else:
                     p.copy_(torch.randn(p.shape, generator=g) * 0.02)
         self.m = m.to(dev, torch.bfloat16).eval()
@@ -149,6 +150,86 @@ def c3_flops(B=4, S=4096, dim=1024, Hq=4, Hkv=1, comp=4, ks=3):
 
 
 N_X_SETS = 16  # rotating input sets: 16 x 32 MiB, more than the 256 MiB MALL holds
+
+
+def time_prep_and_attention(step, iters):
+    """Average durations (ms) of the prep kernel and of the attention op of
+    a C3Step's module, each timed alone as back-to-back calls."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward, ccgqa_prep
+
+    m = step.m
+    with torch.no_grad():
+        qkv = F.linear(step.x, m.qkv_proj.weight)
+        prep = lambda: ccgqa_prep(qkv, m.n_heads, m.n_kv_heads, m.head_dim, step.flags, *step.convw,
+                                  temperature=m.key_temperature, cos=step.cos, sin=step.sin,
+                                  packed=True)
+        q, k, v = prep()
+        prep_ms = _time_rotating(prep, [()], iters)
+        o_view = step.out.view(step.B, step.S, m.n_heads, m.head_dim).transpose(1, 2)
+        attn_ms = _time_rotating(lambda: attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view,
+                                                           bound_temperature=step.temp),
+                                 [()], iters)
+    return prep_ms, attn_ms
+
+
+def shader_clock_mhz(dev, iters=200, reps=5):
+    """The shader clock under a synthetic matrix-core load
+    (hydra_clock_probe: two 8-wave workgroups per CU issuing bf16 MFMAs and
+    v_exp_f32), median over `reps` back-to-back probes: sum of s_memtime
+    ticks over sum of s_memrealtime ticks, times the wall clock's rate.
+    Returns (MHz, wall-clock rate in kHz)."""
+    import ctypes
+
+    from hydra_amd import _lib
+
+    nwg = 2 * torch.cuda.get_device_properties(dev).multi_processor_count
+    stamps = torch.zeros(nwg * 5, dtype=torch.int64, device=dev)
+    khz = ctypes.c_int64(0)
+    vals = []
+    for _ in range(reps):
+        _lib.call("hydra_clock_probe", stamps.data_ptr(), nwg, iters, ctypes.byref(khz), _lib.stream(stamps))
+        st = stamps.view(nwg, 5).cpu()
+        shader = (st[:, 1] - st[:, 0]).double().sum().item()
+        wall = (st[:, 3] - st[:, 2]).double().sum().item()
+        vals.append(shader / wall * khz.value / 1e3)
+    vals.sort()
+    return vals[len(vals) // 2], khz.value
+
+
+def attention_clock(step, wall_khz, reps=5):
+    """The shader clock the key-split attention kernel itself runs at: its
+    workgroups stamp s_memtime and s_memrealtime at start and end
+    (hydra_attn_clock_stamps), over `reps` back-to-back launches; returns
+    (MHz = sum of shader ticks / sum of wall ticks x wall rate, mean
+    first-start-to-last-end span of a launch in ms)."""
+    from hydra_amd import _lib
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward, ccgqa_prep
+
+    m = step.m
+    cap = 1 << 16
+    buf = torch.zeros(reps, cap * 4, dtype=torch.int64, device=step.x.device)
+    with torch.no_grad():
+        qkv = F.linear(step.x, m.qkv_proj.weight)
+        q, k, v = ccgqa_prep(qkv, m.n_heads, m.n_kv_heads, m.head_dim, step.flags, *step.convw,
+                             temperature=m.key_temperature, cos=step.cos, sin=step.sin, packed=True)
+        o_view = step.out.view(step.B, step.S, m.n_heads, m.head_dim).transpose(1, 2)
+        attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view, bound_temperature=step.temp)
+        try:
+            for r in range(reps):
+                _lib.call("hydra_attn_clock_stamps", buf[r].data_ptr(), cap)
+                attention_forward(q, k, v, causal=True, scale=m.scale, out=o_view,
+                                  bound_temperature=step.temp)
+        finally:
+            _lib.call("hydra_attn_clock_stamps", None, 0)
+    torch.cuda.synchronize()
+    st = buf.view(reps, cap, 4).cpu()
+    used = st[0, :, 3] != 0
+    st = st[:, used]
+    shader = (st[..., 1] - st[..., 0]).double().sum().item()
+    wall = (st[..., 3] - st[..., 2]).double().sum().item()
+    span = ((st[..., 3].max(1).values - st[..., 2].min(1).values).double().mean().item()
+            / wall_khz)
+    return shader / wall * wall_khz / 1e3, span
 
 
 def bench_c3(dev, steps, warmup):
@@ -701,11 +782,32 @@ def bench_c5(dev, steps=3, warmup=1):
     assert out.shape == (4, 4096, 32000) and torch.isfinite(out[0, :4].float()).all()
     del model, out
     torch.cuda.empty_cache()
+    # one block's CCGQA prep and attention core at this shape, timed alone
+    # (temperature sqrt(16) = 4, the module's initial value)
+    st = C3Step(dev, B=4, S=4096, dim=1792, n_heads=28, n_kv_heads=4, comp=4, temperature=4.0)
+    prep_ms, attn_ms = time_prep_and_attention(st, 40)
+    fl = c3_flops(B=4, S=4096, dim=1792, Hq=28, Hkv=4, comp=4)
+    prep_fl = fl["q_conv"] + fl["k_conv"]
+    del st
+    torch.cuda.empty_cache()
     return {"value": 4 * 4096 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "steps": steps,
             "warmup": warmup, "dtype": "bf16", "params": n_params,
             "workload": "config 5: HydraModel 1B shape (dim 1792, 20 MoR blocks x 4 recursions, "
-                        "28/4 heads x hd 16, mlp 3.6, MoD 0.75 middle blocks, vocab 32000), "
-                        "B4 x S4096, bf16, eager"}
+                        "28/4 heads x hd 16 (7:1, the reference's 1B preset; the config's 8:1 has no "
+                        "even head dim for latent 448 with 4 kv heads), mlp 3.6, MoD 0.75 middle "
+                        "blocks, MoR router target 0.2 -> 0.5 (the code's; the README's 40% -> 80% "
+                        "is not in the code), vocab 32000), B4 x S4096, bf16, eager",
+            "roofline": {
+                "attention": {"kernel": "attn_fwd_mfma_kernel<16,causal>", "bound": "mfma",
+                              "avg_ms": attn_ms, "flops_per_launch": fl["core"],
+                              "achieved": fl["core"] / (attn_ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS,
+                              "unit": "TFLOP/s",
+                              "frac": fl["core"] / (attn_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS},
+                "prep": {"kernel": "ccgqa_prep_mfma_kernel<16,64>", "bound": "mfma",
+                         "avg_ms": prep_ms, "flops_per_launch": prep_fl,
+                         "achieved": prep_fl / (prep_ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": prep_fl / (prep_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS},
+            }}
 
 
 def calibrate_copy(mib=512, reps=3):
@@ -804,8 +906,12 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     step, ms_step, eager_ms, stages, attn_ms = bench_c3(dev, args.steps, args.warmup)
+    probe_mhz, wall_khz = shader_clock_mhz(dev)
+    clock, span_ms = attention_clock(step, wall_khz)
     fl = c3_flops()
     achieved = fl["core"] / (attn_ms * 1e-3) / 1e12
+    # the nominal peak is 256 CUs x 4 SIMDs x 1024 FLOP/clk at 2400 MHz
+    peak_at_clock = BF16_PEAK_TFLOPS * clock / 2400.0
     line = {
         "metric": METRIC,
         "value": step.B * step.S / (ms_step * 1e-3),
@@ -826,7 +932,13 @@ def main():
                      "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS,
                      "traffic": measured_traffic("attention_op<64,causal>"),
-                     "flops_per_launch": fl["core"], "avg_ms": attn_ms},
+                     "flops_per_launch": fl["core"], "avg_ms": attn_ms,
+                     "clock_mhz": clock, "peak_at_clock": peak_at_clock,
+                     "frac_at_clock": achieved / peak_at_clock,
+                     "clock_source": "the attention kernel's own s_memtime / s_memrealtime stamps "
+                                     "per workgroup (5 launches after the timing)",
+                     "stamped_span_ms": span_ms,
+                     "probe_clock_mhz": probe_mhz},
         "launch": "HIP graph of the K steps (16 rotating 32 MiB input sets), one launch",
         "eager_ms_per_step": eager_ms,
         "stages_ms": {"eager_events": stages, "attention_graph": attn_ms},

@@ -56,6 +56,7 @@ SIGNATURES = {
     "hydra_linear_fwd": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],
     "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
+    "hydra_ccgqa_prep_faults": [_P],
     "hydra_ccgqa_prep_bwd": [_P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P,
                              _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_causal_im2col": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P],
@@ -69,6 +70,8 @@ SIGNATURES = {
     "hydra_mod_gather": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_mod_scatter": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_stream_copy": [_P, _P, _I64, _P],
+    "hydra_clock_probe": [_P, _I, _I, _I64P, _P],
+    "hydra_attn_clock_stamps": [_P, _I64],
 }
 
 _lib = None
@@ -132,6 +135,15 @@ def check(rc: int, name: str) -> None:
         if rc == ERR_ARG:
             raise ValueError(f"{name}: {msg}")
         raise HydraError(f"{name} failed ({rc}): {msg}")
+
+
+def prep_faults() -> int:
+    """hydra_ccgqa_prep_faults: prep tiles (on the current device, since
+    load) whose epilogue timed out waiting for the QK-mean terms; 0 on a
+    working device."""
+    n = ctypes.c_uint(0)
+    call("hydra_ccgqa_prep_faults", ctypes.byref(n))
+    return int(n.value)
 
 
 def query(name: str, *args) -> int:

@@ -54,6 +54,39 @@ def _mask_mode() -> int:
     return MASK_KEY_PADDING if v in {"key_padding", "padding"} else MASK_REFERENCE_SDPA
 
 
+class _EvalRecompute(torch.autograd.Function):
+    """CCGQAAttention in eval() mode with autograd recording (parameters
+    that require grad, an input that does not): the forward runs the
+    inference kernels and keeps only x; the backward runs the training path
+    (CCGQAPrepFunction, CCGQAAttentionFused, F.linear) on x again and
+    differentiates that.  Its gradients are those of the training path,
+    whose forward equals the inference forward within bf16 rounding."""
+
+    @staticmethod
+    def forward(ctx, module, x, *params):
+        ctx.module = module
+        ctx.save_for_backward(x)
+        qkv = F.linear(x, module.qkv_proj.weight)
+        flags, convw = module._prep_args()
+        return module._forward_infer(x, qkv, flags, convw, None)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (x,) = ctx.saved_tensors
+        m = ctx.module
+        params = tuple(m.parameters())
+        with torch.enable_grad():
+            xr = x.detach().requires_grad_(ctx.needs_input_grad[1])
+            qkv = F.linear(xr, m.qkv_proj.weight)
+            flags, convw = m._prep_args()
+            out = m._forward_train(qkv, flags, convw)
+            wrt = ([xr] if xr.requires_grad else []) + [p for p in params if p.requires_grad]
+            grads = list(torch.autograd.grad(out, wrt, grad_out, allow_unused=True))
+        dx = grads.pop(0) if xr.requires_grad else None
+        dparams = [grads.pop(0) if p.requires_grad else None for p in params]
+        return (None, dx, *dparams)
+
+
 class CCGQAAttention(nn.Module):
     """Compressed Convolutional Grouped Query Attention on gfx950."""
 
@@ -115,15 +148,35 @@ class CCGQAAttention(nn.Module):
         if self.use_rope and S > self.cos_cached.shape[2]:
             raise ValueError(f"CCGQAAttention: sequence length {S} exceeds the RoPE cache "
                              f"({self.cos_cached.shape[2]})")
+        recording = mask is None and torch.is_grad_enabled() and (
+            x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        if recording and not (self.training or x.requires_grad):
+            # eval() with parameters that require grad: the inference kernels
+            # give the output; a backward, if one comes, recomputes the
+            # forward through the training path (as activation checkpointing
+            # would) instead of keeping its activations now.
+            return _EvalRecompute.apply(self, x, *self.parameters())
         qkv = F.linear(x, self.qkv_proj.weight)
+        flags, convw = self._prep_args()
+        if recording:
+            return self._forward_train(qkv, flags, convw)
+        return self._forward_infer(x, qkv, flags, convw, mask)
+
+    def _prep_args(self):
+        """The prep kernel's feature flags and the four conv weights (Conv1d
+        layout; empty without convs)."""
         flags = prep_flags(self.use_convs, self.use_qk_mean, self.use_value_shift,
                            self.use_qk_norm, self.use_rope)
         convw = ((self.q_conv.conv1.weight, self.q_conv.conv2.weight,
                   self.k_conv.conv1.weight, self.k_conv.conv2.weight)
                  if self.use_convs else ())
-        if mask is None and torch.is_grad_enabled() and (
-                x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            return self._forward_train(qkv, flags, convw)
+        return flags, convw
+
+    def _forward_infer(self, x, qkv, flags, convw, mask):
+        """The inference kernels: prep with V^T rows and MFMA-tiled conv
+        weights, the attention kernel writing [B, S, L], o_proj in
+        hydra_linear_fwd."""
+        B, S, _ = x.shape
         if x.dtype == torch.bfloat16 and S % 8 == 0 and self.head_dim in (16, 32, 64, 128):
             flags |= CCGQA_V_TRANSPOSED  # V^T feeds the MFMA attention without a transpose
         tiled = self.use_convs and tiled_weights_ok(self.n_heads, self.n_kv_heads, self.head_dim, x.dtype)

@@ -132,7 +132,7 @@ extern "C" const char* hydra_last_error(void) {
   return hydra::g_last_error.c_str();
 }
 
-extern "C" int hydra_abi_version(void) { return 109; }
+extern "C" int hydra_abi_version(void) { return 110; }
 
 // ---- same-device HBM copy (measurement aid) ---------------------------------
 // One 16-byte chunk per thread, non-temporal load and store, 256-thread
@@ -159,4 +159,72 @@ extern "C" int hydra_stream_copy(const void* src, void* dst, int64_t bytes, void
   stream_copy_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint4*>(src), static_cast<uint4*>(dst), n);
   return check_launch("stream_copy_kernel");
+}
+
+// ---- shader clock under matrix-core load (measurement aid) -----------------
+// Each workgroup of 8 waves (two per SIMD) issues v_mfma_f32_32x32x16_bf16
+// into four independent accumulators and v_exp_f32 on 16 independent chains
+// per iteration, the attention tile's two instruction kinds, and stamps the
+// shader clock (s_memtime) and the constant-rate wall clock
+// (s_memrealtime) before and after, between workgroup barriers.
+namespace hydra {
+namespace {
+typedef __attribute__((ext_vector_type(8))) __bf16 probe_bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float probe_f32x16_t;
+
+__global__ __launch_bounds__(512) void clock_probe_kernel(unsigned long long* __restrict__ stamps, int iters) {
+  const int lane = threadIdx.x & 63;
+  const uint4 raw = make_uint4(0x3f803f80u ^ lane, 0x3f803f80u, 0x3c003c00u, 0x3f003f00u);
+  const probe_bf16x8_t a = __builtin_bit_cast(probe_bf16x8_t, raw);
+  probe_f32x16_t acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  float e[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) e[j] = 0.01f * (lane + j);
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, a, acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) e[j] = __builtin_amdgcn_exp2f(-0.5f * e[j]);
+  }
+  __syncthreads();
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  float sink = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sink += acc[j][lane & 15];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) sink += e[j];
+  if (threadIdx.x == 0) {
+    unsigned long long* o = stamps + 5 * static_cast<int64_t>(blockIdx.x);
+    o[0] = t0;
+    o[1] = t1;
+    o[2] = r0;
+    o[3] = r1;
+    o[4] = static_cast<unsigned long long>(__float_as_uint(sink));
+  }
+}
+}  // namespace
+}  // namespace hydra
+
+extern "C" int hydra_clock_probe(void* stamps, int nwg, int iters, int64_t* wall_khz, void* stream) {
+  using namespace hydra;
+  HYDRA_REQUIRE(stamps != nullptr && wall_khz != nullptr, "clock_probe: null pointer");
+  HYDRA_REQUIRE(nwg >= 1 && nwg <= 65535, "clock_probe: need 1 <= nwg <= 65535");
+  HYDRA_REQUIRE(iters >= 1, "clock_probe: need iters >= 1");
+  HYDRA_REQUIRE(reinterpret_cast<uintptr_t>(stamps) % 8 == 0, "clock_probe: stamps must be 8-byte aligned");
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+    return fail(HYDRA_ERR_LAUNCH, "clock_probe: no wall-clock rate for this device");
+  *wall_khz = khz;
+  clock_probe_kernel<<<dim3(static_cast<unsigned>(nwg)), 512, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<unsigned long long*>(stamps), iters);
+  return check_launch("clock_probe_kernel");
 }

@@ -683,23 +683,42 @@ __attribute__((amdgpu_waves_per_eu((FXM == 2 && HD <= 64) ? 3 : 1))) void attn_f
 }
 
 // Key-split workgroups (V^T rows only).  A workgroup of KP x NW waves takes
-// one item whole -- NW tasks, as in attn_fwd_mfma_kernel -- and its KP groups
-// of NW waves walk the item's key tiles in turn (group g: tiles g, g + KP,
-// ..), each group staging its own tiles in LDS, one barrier per step.  At
-// the end, groups 1.. KP-1 leave (O, m, l) in LDS and group 0 folds them in
-// group order and writes the rows.  Every item is one workgroup, longest
-// first: no chunk partials and no merge kernel, and the longest item takes
-// KP-fold fewer steps, which is what balances the causal triangle when
-// there are few items.
+// one or two items -- NW tasks each, as in attn_fwd_mfma_kernel -- one after
+// the other, and for each item its KP groups of NW waves walk the item's
+// key tiles in turn (group g: tiles g, g + KP, ..), each group staging its
+// own tiles in LDS, one barrier per step.  At the end of an item, groups
+// 1..KP-1 leave (O, m, l) in LDS and group 0 folds them in group order and
+// writes the rows.  Items are taken longest first in snake order over the
+// P workgroups (workgroup w: items w and 2P-1-w), so with P = items / 2
+// resident workgroups each gets a long and a short item and the causal
+// triangle balances without chunk partials or a merge kernel.  The second
+// item's first tiles and Q rows are fetched before the first item's fold,
+// so their latency hides behind it, and no CU waits for a second launch.
+// Strides are 32-bit here (the host checks they fit) to keep the two
+// items' state within the scalar registers.
+//
+// LDS: every group's buffer 0 (K, V^T) in the first third of the array,
+// buffer 1 in the second, and the fold's exchange over buffer 1 and the
+// rest: an item's first tiles always land in buffer 0, which the fold
+// leaves alone.
+template <int HD, int NW, int KP>
+struct KpLds {
+  using L = AttnLds<HD, true>;
+  static constexpr int DT = L::DT;
+  static constexpr int TILE = L::KBUF + L::VBUF;     // one group's K and V^T buffer (elements)
+  static constexpr int XF = DT * 16 + 2;             // exchanged floats per lane: O, m, l
+  static constexpr int XCH = (KP - 1) * NW * 64 * XF * 2;  // exchange size in elements
+  static constexpr int XOFF = KP * TILE;             // exchange start: the buffer-1 region
+  static constexpr int SIZE = XOFF + (XCH > KP * TILE ? XCH : KP * TILE);
+};
+
 template <int HD, bool CAUSAL, int MASK, int NW, int KP, bool FIXED>
 __device__ __forceinline__ void attn_fwd_kp_body(
     uint16_t* __restrict__ smem, const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
-    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH,
-    int64_t qs0, int64_t qs1, int64_t qs2,
-    int64_t ks0, int64_t ks1, int64_t ks2,
-    int64_t vs0, int64_t vs1, int64_t vs2,
-    int64_t os0, int64_t os1, int64_t os2, float scale_log2) {
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int P,
+    int qs0, int qs1, int qs2, int ks0, int ks1, int ks2,
+    int vs0, int vs1, int vs2, int os0, int os1, int os2, float scale_log2) {
   constexpr int BN = kAttnBN;
   constexpr int KSTEPS = HD / 16;
   constexpr int DT = (HD + 31) / 32;
@@ -714,10 +733,10 @@ __device__ __forceinline__ void attn_fwd_kp_body(
   constexpr int VBUF = VINS * 512 > DT * 32 * VROW ? VINS * 512 : DT * 32 * VROW;
   constexpr int KIPW = (KINS + NW - 1) / NW;
   constexpr int VIPW = (VINS + NW - 1) / NW;
-  constexpr int GBUF = 2 * (KBUF + VBUF);  // a group's double-buffered K and V^T (elements)
+  using Lay = KpLds<HD, NW, KP>;
+  constexpr int TILE = Lay::TILE;
   constexpr int NT = 64 * NW * KP;
-  constexpr int XF = DT * 16 + 2;          // exchanged floats per lane: O, m, l
-  static_assert((KP - 1) * NW * 64 * XF * 4 <= KP * GBUF * 2, "the exchange fits in the tile buffers");
+  constexpr int XF = Lay::XF;
   static_assert(KBUF == AttnLds<HD, true>::KBUF && VBUF == AttnLds<HD, true>::VBUF,
                 "LDS sizes agree with the kernel's array");
   constexpr uint32_t kOob = 0x80000000u;
@@ -727,25 +746,16 @@ __device__ __forceinline__ void attn_fwd_kp_body(
   const int grp = wv / NW, wq = wv - grp * NW;  // key group, task within the item
   const int n = lane & 31, hf = lane >> 5;
   const bool walk = CAUSAL && MASK != 2;
-  const int p = blockIdx.x / BH, bk = blockIdx.x - p * BH;
-  const int wg = attn_pos_item(p, nwg, false);
-  const int nkb = attn_tiles<NW>(wg, S, G, ntasks, walk);
-  const int b = bk / Hkv, kvh = bk - b * Hkv;
-  const int task = wg * NW + wq;
-  const bool active = task < ntasks;
-  const int qb = task / G;
-  const int h = kvh * G + (task - qb * G);
-  const int q0 = qb * 32, qi = q0 + n;
-  const bf16* kbase = k + b * ks0 + kvh * ks1;
-  const bf16* vbase = v + b * vs0 + kvh * vs1;
-  uint16_t* Ks = smem + grp * GBUF;
-  uint16_t* Vt = Ks + 2 * KBUF;
+  const int nitems = nwg * BH;
+  // group grp's buffer b: K at smem + (b * KP + grp) * TILE, V^T after it
+  auto kbuf = [&](int b) { return smem + (b * KP + grp) * TILE; };
+  auto vbuf = [&](int b) { return smem + (b * KP + grp) * TILE + KBUF; };
 
   if constexpr (DT * 32 > HD) {  // zero the padding rows of every V^T buffer once
     constexpr int PADE = (DT * 32 - HD) * VROW;
     for (int i = tid; i < KP * 2 * PADE; i += NT) {
-      const int bu = i / PADE, r = i - bu * PADE;
-      smem[(bu >> 1) * GBUF + 2 * KBUF + (bu & 1) * VBUF + HD * VROW + r] = 0;
+      const int bu = i / PADE, r = i - bu * PADE;  // bu = buffer * KP + group
+      smem[bu * TILE + KBUF + HD * VROW + r] = 0;
     }
   }
   // Per-lane byte offsets within a tile (fixed for the kernel): K slot
@@ -755,69 +765,77 @@ __device__ __forceinline__ void attn_fwd_kp_body(
   uint32_t koffs[KIPW];
 #pragma unroll
   for (int i = 0; i < KIPW; ++i) {
-    const int j = wq + NW * i, P = 64 * j + lane;
-    const int r = P / KSL, c = P - r * KSL;
+    const int j = wq + NW * i, Pp = 64 * j + lane;
+    const int r = Pp / KSL, c = Pp - r * KSL;
     koffs[i] = (j < KINS && c < DC) ? static_cast<uint32_t>((r * ks2 + c * 8) * 2) : kOob;
   }
   uint32_t vtoffs[VIPW];
   int vtkey[VIPW];  // first key of the slot's chunk (BN for pad slots)
 #pragma unroll
   for (int i = 0; i < VIPW; ++i) {
-    const int j = wq + NW * i, P = 64 * j + lane;
-    const int d = P / VSL, c = P - d * VSL;
+    const int j = wq + NW * i, Pp = 64 * j + lane;
+    const int d = Pp / VSL, c = Pp - d * VSL;
     const bool ok = j < VINS && d < HD && c < BN / 8;
     vtoffs[i] = ok ? static_cast<uint32_t>((d * vs2 + 8 * c) * 2) : kOob;
     vtkey[i] = ok ? 8 * c : BN;
   }
-  const uint32_t ks_lds = lds_addr(Ks), vt_lds = lds_addr(Vt);
 
-  // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7];
-  // FIXED: scaled by scale * log2(e) and rounded to bf16 once.
-  bf16x8_t qf[KSTEPS];
-  {
-    const bf16* qrow = q + b * qs0 + h * qs1 + static_cast<int64_t>(qi) * qs2;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (active && qi < S) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
-      if constexpr (FIXED) {
-        uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = pack2<bf16>(__uint_as_float(w[e] << 16) * scale_log2,
-                             __uint_as_float(w[e] & 0xffff0000u) * scale_log2);
-        raw = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-      qf[s] = as_bf16x8(raw);
-    }
-  }
+  // One item: position pos in the longest-first order.
+  struct Item {
+    int wg, nkb, b, kvh, h, q0, qi;
+    bool active;
+    const bf16* kbase;
+    const bf16* vbase;
+  };
+  auto locate = [&](int pos) {
+    Item it;
+    const int p = pos / BH, bk = pos - p * BH;
+    it.wg = attn_pos_item(p, nwg, false);
+    it.nkb = attn_tiles<NW>(it.wg, S, G, ntasks, walk);
+    it.b = bk / Hkv;
+    it.kvh = bk - it.b * Hkv;
+    const int task = it.wg * NW + wq;
+    it.active = task < ntasks;
+    const int qb = task / G;
+    it.h = it.kvh * G + (task - qb * G);
+    it.q0 = qb * 32;
+    it.qi = it.q0 + n;
+    it.kbase = k + static_cast<int64_t>(it.b) * ks0 + static_cast<int64_t>(it.kvh) * ks1;
+    it.vbase = v + static_cast<int64_t>(it.b) * vs0 + static_cast<int64_t>(it.kvh) * vs1;
+    return it;
+  };
+  // snake order: round r takes position r*P + w (r even) or r*P + P-1-w
+  auto pos_of = [&](int r) {
+    return r * P + ((r & 1) ? P - 1 - static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x));
+  };
 
-  // The group's loads of tile kb into its buffer buf.  Keys at or past S
-  // (last tile only; S % 8 == 0 on this path) load as zeros: K rows through
-  // num_records, V^T chunks through the lane's offset.
-  auto fetch = [&](int kb, int buf) {
+  // The group's loads of tile kb of item `it` into its buffer buf.  Keys at
+  // or past S (last tile only; S % 8 == 0 on this path) load as zeros: K
+  // rows through num_records, V^T chunks through the lane's offset.
+  auto fetch = [&](const Item& it, int kb, int buf) {
     const int key0 = kb * BN;
     const int rows = min(BN, S - key0);
-    const i32x4_t kr = raw_rsrc(kbase + static_cast<int64_t>(key0) * ks2,
+    const i32x4_t kr = raw_rsrc(it.kbase + static_cast<int64_t>(key0) * ks2,
                                 static_cast<int>((rows - 1) * ks2 * 2 + HD * 2));
+    const uint32_t ks_lds = lds_addr(kbuf(buf));
+    const uint32_t vt_lds = lds_addr(vbuf(buf));
 #pragma unroll
     for (int i = 0; i < KIPW; ++i) {
       const int j = wq + NW * i;
-      if (j < KINS) load16_to_lds(kr, ks_lds + (buf * KBUF + 512 * j) * 2, koffs[i]);
+      if (j < KINS) load16_to_lds(kr, ks_lds + 1024 * j, koffs[i]);
     }
-    const i32x4_t vr = raw_rsrc(vbase + key0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2));
+    const i32x4_t vr = raw_rsrc(it.vbase + key0, static_cast<int>((HD - 1) * vs2 * 2 + rows * 2));
     if (key0 + BN <= S) {
 #pragma unroll
       for (int i = 0; i < VIPW; ++i) {
         const int j = wq + NW * i;
-        if (j < VINS) load16_to_lds(vr, vt_lds + (buf * VBUF + 512 * j) * 2, vtoffs[i]);
+        if (j < VINS) load16_to_lds(vr, vt_lds + 1024 * j, vtoffs[i]);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < VIPW; ++i) {
         const int j = wq + NW * i;
-        if (j < VINS)
-          load16_to_lds(vr, vt_lds + (buf * VBUF + 512 * j) * 2, key0 + vtkey[i] < S ? vtoffs[i] : kOob);
+        if (j < VINS) load16_to_lds(vr, vt_lds + 1024 * j, key0 + vtkey[i] < S ? vtoffs[i] : kOob);
       }
     }
   };
@@ -825,104 +843,193 @@ __device__ __forceinline__ void attn_fwd_kp_body(
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's loads, LDS writes included
     __syncthreads();
   };
-
-  float m_i = FIXED ? 0.f : -INFINITY, l_i = 0.f;
-  f32x16_t acc[DT];
+  // Q fragments (B operand of S^T = K Q^T): lane holds q[qi, 16s+8hf .. +7],
+  // loaded raw (no wait) and, once landed, FIXED: scaled by scale * log2(e)
+  // and rounded to bf16 once.
+  auto load_q = [&](const Item& it, uint4* raw) {
+    const bf16* qrow = q + static_cast<int64_t>(it.b) * qs0 + static_cast<int64_t>(it.h) * qs1 +
+                       static_cast<int64_t>(it.qi) * qs2;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+    for (int s = 0; s < KSTEPS; ++s) {
+      raw[s] = make_uint4(0, 0, 0, 0);
+      if (it.active && it.qi < S) raw[s] = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hf);
+    }
+  };
+  auto make_qf = [&](const uint4* raw, bf16x8_t* qf) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+    for (int s = 0; s < KSTEPS; ++s) {
+      uint4 r = raw[s];
+      if constexpr (FIXED) {
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack2<bf16>(__uint_as_float(w[e] << 16) * scale_log2,
+                             __uint_as_float(w[e] & 0xffff0000u) * scale_log2);
+        r = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      qf[s] = as_bf16x8(r);
+    }
+  };
 
-  // Tiles [0, nfull) are in bounds and at or below the diagonal of every
-  // wave; the rest need the mask.
-  const int wg_qmin = ((wg * NW) / G) * 32;
-  int nfull = 0;
-  if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
-  nfull = min(nfull, nkb);
-  const uint8_t* kmrow = MASK != 0 ? kmask + static_cast<int64_t>(b) * S : nullptr;
-  const int nsteps = (nkb + KP - 1) / KP;
-  // Steps [0, st_full) have every group's tile unmasked; the rest (at most
-  // a few at the end of a causal item) run the masked code for all tiles.
-  // Two loops rather than a per-tile choice: a join of the two tile codes
-  // costs a copy of the accumulators every step.
-  const int st_full = nfull / KP;
-  if (grp < nkb) fetch(grp, 0);
-  land();
-  int st = 0;
-  for (; st < st_full; ++st) {
-    const int kb = st * KP + grp, buf = st & 1;
-    // The group's next tile goes into its other buffer, which the group
-    // finished reading before the barrier that ended the previous step.
-    if (kb + KP < nkb) fetch(kb + KP, buf ^ 1);
-    if (active)
-      attn_tile<HD, CAUSAL, MASK, FIXED, false, KROW, VROW>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i, l_i,
-                                                           kb * BN, qi, S, n, hf, kmrow, scale_log2);
-    land();
-  }
-  for (; st < nsteps; ++st) {
-    const int kb = st * KP + grp, buf = st & 1;
-    if (kb + KP < nkb) fetch(kb + KP, buf ^ 1);
-    if (active && kb < nkb && !(walk && kb * BN > q0 + 31))
-      attn_tile<HD, CAUSAL, MASK, FIXED, true, KROW, VROW>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i, l_i,
-                                                          kb * BN, qi, S, n, hf, kmrow, scale_log2);
-    land();
-  }
-
-  // Fold the groups: the last barrier ended every read of the tile buffers.
-  l_i = halves_sum(l_i);
-  float* xch = reinterpret_cast<float*>(smem);
-  if (grp > 0) {
-    float* xw = xch + static_cast<int64_t>((grp - 1) * NW + wq) * 64 * XF;
+  float* xch = reinterpret_cast<float*>(smem + Lay::XOFF);
+  uint4 qraw[KSTEPS];
+  // One item: its steps, then (when `nxt` is valid) the next item's first
+  // tiles and Q rows, then the fold and the rows' stores.
+  auto run_item = [&](const Item& cur, int nxt_pos) {
+    bf16x8_t qf[KSTEPS];
+    make_qf(qraw, qf);
+    float m_i = FIXED ? 0.f : -INFINITY, l_i = 0.f;
+    f32x16_t acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) xw[(dt * 16 + r) * 64 + lane] = acc[dt][r];
-    xw[(DT * 16) * 64 + lane] = m_i;
-    xw[(DT * 16 + 1) * 64 + lane] = l_i;
-  }
-  __syncthreads();
-  if (grp == 0 && active && qi < S) {
+      for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+
+    // Tiles [0, nfull) are in bounds and at or below the diagonal of every
+    // wave; the rest need the mask.
+    const int nkb = cur.nkb;
+    const int wg_qmin = ((cur.wg * NW) / G) * 32;
+    int nfull = 0;
+    if (MASK == 0) nfull = min(CAUSAL ? (wg_qmin + 1) / BN : nkb, S / BN);
+    nfull = min(nfull, nkb);
+    const uint8_t* kmrow = MASK != 0 ? kmask + static_cast<int64_t>(cur.b) * S : nullptr;
+    const int nsteps = (nkb + KP - 1) / KP;
+    // Steps [0, st_full) have every group's tile unmasked; the rest (at most
+    // a few at the end of a causal item) run the masked code for all tiles.
+    // Two loops rather than a per-tile choice: a join of the two tile codes
+    // costs a copy of the accumulators every step.
+    const int st_full = nfull / KP;
+    int st = 0;
+    for (; st < st_full; ++st) {
+      const int kb = st * KP + grp, buf = st & 1;
+      // The group's next tile goes into its other buffer, which the group
+      // finished reading before the barrier that ended the previous step.
+      if (kb + KP < nkb) fetch(cur, kb + KP, buf ^ 1);
+      if (cur.active)
+        attn_tile<HD, CAUSAL, MASK, FIXED, false, KROW, VROW>(kbuf(buf), vbuf(buf), qf, acc, m_i, l_i,
+                                                             kb * BN, cur.qi, S, n, hf, kmrow, scale_log2);
+      land();
+    }
+    for (; st < nsteps; ++st) {
+      const int kb = st * KP + grp, buf = st & 1;
+      if (kb + KP < nkb) fetch(cur, kb + KP, buf ^ 1);
+      if (cur.active && kb < nkb && !(walk && kb * BN > cur.q0 + 31))
+        attn_tile<HD, CAUSAL, MASK, FIXED, true, KROW, VROW>(kbuf(buf), vbuf(buf), qf, acc, m_i, l_i,
+                                                            kb * BN, cur.qi, S, n, hf, kmrow, scale_log2);
+      land();
+    }
+    // Every read of this item's tiles ended at the last barrier: the next
+    // item's first tiles go into buffer 0 and its Q rows into registers
+    // while this item folds (the exchange lies outside buffer 0).
+    if (nxt_pos < nitems) {
+      const Item nxt = locate(nxt_pos);
+      if (grp < nxt.nkb) fetch(nxt, grp, 0);
+      load_q(nxt, qraw);
+    }
+    // Fold the groups.  The exchange holds, per (group, wave), 4*DT rows
+    // of 64 lanes x 16 bytes (O) and one of 64 x 8 bytes (m, l): every LDS
+    // instruction moves one contiguous 1 KB (or 512 B) row.
+    l_i = halves_sum(l_i);
+    if (grp > 0) {
+      float* xw = xch + static_cast<int64_t>((grp - 1) * NW + wq) * 64 * XF;
 #pragma unroll
-    for (int g = 1; g < KP; ++g) {
-      const float* xw = xch + static_cast<int64_t>((g - 1) * NW + wq) * 64 * XF;
-      const float m2 = xw[(DT * 16) * 64 + lane], l2 = xw[(DT * 16 + 1) * 64 + lane];
-      if constexpr (FIXED) {
-        l_i += l2;
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<float4*>(xw + ((dt * 4 + r4) * 64 + lane) * 4) =
+              make_float4(acc[dt][4 * r4], acc[dt][4 * r4 + 1], acc[dt][4 * r4 + 2], acc[dt][4 * r4 + 3]);
+      *reinterpret_cast<float2*>(xw + DT * 16 * 64 + 2 * lane) = make_float2(m_i, l_i);
+    }
+    __syncthreads();
+    const bool store = grp == 0 && cur.active && cur.qi < S;
+    if (store) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] += xw[(dt * 16 + r) * 64 + lane];
-      } else if (m2 != -INFINITY) {  // a group that saw no key of this row adds nothing
-        const float mn = fmaxf(m_i, m2);
-        const float s1 = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - mn);
-        const float s2 = __builtin_amdgcn_exp2f(m2 - mn);
-        l_i = fmaf(l2, s2, l_i * s1);
+      for (int g = 1; g < KP; ++g) {
+        const float* xw = xch + static_cast<int64_t>((g - 1) * NW + wq) * 64 * XF;
+        const float2 ml = *reinterpret_cast<const float2*>(xw + DT * 16 * 64 + 2 * lane);
+        const float m2 = ml.x, l2 = ml.y;
+        float4 part[DT * 4];
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int j = 0; j < DT * 4; ++j) part[j] = *reinterpret_cast<const float4*>(xw + (j * 64 + lane) * 4);
+        if constexpr (FIXED) {
+          l_i += l2;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(xw[(dt * 16 + r) * 64 + lane], s2, acc[dt][r] * s1);
-        m_i = mn;
+          for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const float4 x = part[dt * 4 + r4];
+              acc[dt][4 * r4] += x.x;
+              acc[dt][4 * r4 + 1] += x.y;
+              acc[dt][4 * r4 + 2] += x.z;
+              acc[dt][4 * r4 + 3] += x.w;
+            }
+        } else if (m2 != -INFINITY) {  // a group that saw no key of this row adds nothing
+          const float mn = fmaxf(m_i, m2);
+          const float s1 = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - mn);
+          const float s2 = __builtin_amdgcn_exp2f(m2 - mn);
+          l_i = fmaf(l2, s2, l_i * s1);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const float4 x = part[dt * 4 + r4];
+              acc[dt][4 * r4] = fmaf(x.x, s2, acc[dt][4 * r4] * s1);
+              acc[dt][4 * r4 + 1] = fmaf(x.y, s2, acc[dt][4 * r4 + 1] * s1);
+              acc[dt][4 * r4 + 2] = fmaf(x.z, s2, acc[dt][4 * r4 + 2] * s1);
+              acc[dt][4 * r4 + 3] = fmaf(x.w, s2, acc[dt][4 * r4 + 3] * s1);
+            }
+          m_i = mn;
+        }
       }
     }
-    attn_store_row<HD>(o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2, acc, m_i, l_i, hf,
-                       lse ? lse + (static_cast<int64_t>(b) * Hq + h) * S + qi : nullptr);
+    // Before the next item: its tiles and Q rows have landed, and group 0
+    // has read the exchange before any group writes buffer 1 again.  The
+    // rows are stored after that barrier, so the stores overlap the next
+    // item's first step instead of holding the barrier.
+    if (nxt_pos < nitems) land();
+    if (store)
+      attn_store_row<HD>(o + static_cast<int64_t>(cur.b) * os0 + static_cast<int64_t>(cur.h) * os1 +
+                             static_cast<int64_t>(cur.qi) * os2, acc, m_i, l_i, hf,
+                         lse ? lse + (static_cast<int64_t>(cur.b) * Hq + cur.h) * S + cur.qi : nullptr);
+  };
+
+  // At most two items per workgroup (the launch makes P >= items / 2): the
+  // body is written out twice rather than looped, which keeps the step
+  // loop's register pressure at one item's.
+  const int pos0 = pos_of(0);
+  if (pos0 >= nitems) return;
+  const int pos1 = pos_of(1);
+  {
+    const Item first = locate(pos0);
+    if (grp < first.nkb) fetch(first, grp, 0);
+    load_q(first, qraw);
+    land();
+    run_item(first, pos1);
   }
+  if (pos1 >= nitems) return;
+  run_item(locate(pos1), nitems);
 }
 
 template <int HD, bool CAUSAL, int MASK, int NW, int KP, int FXM>
 __global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
-    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH,
-    int64_t qs0, int64_t qs1, int64_t qs2,
-    int64_t ks0, int64_t ks1, int64_t ks2,
-    int64_t vs0, int64_t vs1, int64_t vs2,
-    int64_t os0, int64_t os1, int64_t os2, float scale_log2, const void* tau, int tau_bf16) {
-  using Lds = AttnLds<HD, true>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[KP * 2 * (Lds::KBUF + Lds::VBUF)];
-#define HYDRA_KP_BODY(FX)                                                                     \
-  attn_fwd_kp_body<HD, CAUSAL, MASK, NW, KP, FX>(smem, q, k, v, o, lse, kmask, S, Hq, Hkv, G,  \
-                                                 ntasks, nwg, BH, qs0, qs1, qs2, ks0, ks1, ks2, \
+    int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int P,
+    int qs0, int qs1, int qs2, int ks0, int ks1, int ks2,
+    int vs0, int vs1, int vs2, int os0, int os1, int os2, float scale_log2, const void* tau, int tau_bf16,
+    unsigned long long* __restrict__ clk) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[KpLds<HD, NW, KP>::SIZE];
+  // Clock stamps (measurement aid, off unless the host installed a buffer):
+  // thread 0 records the shader-clock and wall-clock counters when the
+  // workgroup starts and after its last rows are stored.
+  unsigned long long t0 = 0, r0 = 0;
+  if (clk) {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+#define HYDRA_KP_BODY(FX)                                                                       \
+  attn_fwd_kp_body<HD, CAUSAL, MASK, NW, KP, FX>(smem, q, k, v, o, lse, kmask, S, Hq, Hkv, G,    \
+                                                 ntasks, nwg, BH, P, qs0, qs1, qs2, ks0, ks1, ks2, \
                                                  vs0, vs1, vs2, os0, os1, os2, scale_log2)
   if constexpr (FXM == 2) {
     if (attn_fixed_from_temperature(tau, tau_bf16, scale_log2)) HYDRA_KP_BODY(true);
@@ -931,6 +1038,15 @@ __global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
     HYDRA_KP_BODY(FXM == 1);
   }
 #undef HYDRA_KP_BODY
+  if (clk && threadIdx.x == 0) {
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long* c = clk + 4 * static_cast<int64_t>(blockIdx.x);
+    c[0] = t0;
+    c[1] = t1;
+    c[2] = r0;
+    c[3] = r1;
+  }
 }
 
 // Combines the chunks of split items.  One thread per (w, wave, lane),
@@ -1073,6 +1189,12 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
   if (lse) lse[gid] = l > 0.f ? m + logf(l) : -INFINITY;
 }
 
+// Clock-stamp buffer of the key-split kernel (hydra_attn_clock_stamps):
+// 4 counters per workgroup, used by launches of at most g_clock_stamp_cap
+// workgroups.  Host-side, process-wide; a measurement aid.
+static unsigned long long* g_clock_stamps = nullptr;
+static int64_t g_clock_stamp_cap = 0;
+
 template <int HD>
 static int launch_mfma(const void* q, const void* k, const void* v, void* o, float* lse,
                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
@@ -1126,15 +1248,33 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
                                         64 * NW);
     const int64_t items = static_cast<int64_t>(nwg) * BH;
     const char* sched = getenv("HYDRA_ATTN_SCHED");
-    bool kp = vt && items < 2 * slots;
+    // the key-split kernel takes 32-bit strides
+    auto fits32 = [](const int64_t* x, int n) {
+      for (int i = 0; i < n; ++i)
+        if (x[i] < 0 || x[i] > INT32_MAX) return false;
+      return true;
+    };
+    const bool s32 = fits32(qs, 3) && fits32(ks, 3) && fits32(vs, 4) && fits32(os, 3);
+    bool kp = vt && s32 && items < 2 * slots;
     if (sched && strcmp(sched, "streamk") == 0) kp = false;
-    if (sched && strcmp(sched, "kp") == 0) kp = vt;
+    if (sched && strcmp(sched, "kp") == 0) kp = vt && s32;
     if (getenv("HYDRA_ATTN_WGS")) kp = false;
     if (kp) {
       constexpr int KP = HD == 128 ? 2 : 3;  // key groups (LDS: KP double-buffered K/V^T tiles)
-      attn_fwd_kp_kernel<HD, C, M, NW, KP, FX><<<dim3(static_cast<unsigned>(nwg * BH)), 64 * NW * KP, 0, st>>>(
-          Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, qs[0], qs[1], qs[2], ks[0], ks[1],
-          ks[2], vs[0], vs[1], vs[3], os[0], os[1], os[2], sl2, tau, tau_bf16);
+      auto kkern = attn_fwd_kp_kernel<HD, C, M, NW, KP, FX>;
+      // one resident wave of workgroups, each taking two items (more
+      // workgroups when there are more than two items per resident slot)
+      const int64_t kslots = static_cast<int64_t>(device_cus()) *
+                             std::max(1, blocks_per_cu(reinterpret_cast<const void*>(kkern), 64 * NW * KP));
+      const int Pk = static_cast<int>(std::min<int64_t>(items, std::max<int64_t>(kslots, (items + 1) / 2)));
+      const int32_t qs32[3] = {(int32_t)qs[0], (int32_t)qs[1], (int32_t)qs[2]};
+      const int32_t ks32[3] = {(int32_t)ks[0], (int32_t)ks[1], (int32_t)ks[2]};
+      const int32_t vs32[3] = {(int32_t)vs[0], (int32_t)vs[1], (int32_t)vs[3]};
+      const int32_t os32[3] = {(int32_t)os[0], (int32_t)os[1], (int32_t)os[2]};
+      kkern<<<dim3(static_cast<unsigned>(Pk)), 64 * NW * KP, 0, st>>>(
+          Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, Pk, qs32[0], qs32[1], qs32[2],
+          ks32[0], ks32[1], ks32[2], vs32[0], vs32[1], vs32[2], os32[0], os32[1], os32[2], sl2, tau, tau_bf16,
+          Pk <= g_clock_stamp_cap ? g_clock_stamps : nullptr);
       return check_launch("attn_fwd_kp_kernel");
     }
     auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX> : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>;
@@ -1411,6 +1551,15 @@ static int launch_generic(const void* q, const void* k, const void* v, void* o, 
 }  // namespace hydra
 
 using namespace hydra;
+
+extern "C" int hydra_attn_clock_stamps(void* stamps, int64_t max_workgroups) {
+  HYDRA_REQUIRE(max_workgroups >= 0, "attn_clock_stamps: negative capacity");
+  HYDRA_REQUIRE(stamps != nullptr || max_workgroups == 0, "attn_clock_stamps: null buffer");
+  HYDRA_REQUIRE(reinterpret_cast<uintptr_t>(stamps) % 8 == 0, "attn_clock_stamps: buffer must be 8-byte aligned");
+  hydra::g_clock_stamps = static_cast<unsigned long long*>(stamps);
+  hydra::g_clock_stamp_cap = stamps ? max_workgroups : 0;
+  return HYDRA_OK;
+}
 
 extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
                               float* lse, const uint8_t* key_mask, int mask_mode,

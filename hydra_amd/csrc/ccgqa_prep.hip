@@ -34,6 +34,12 @@
 
 namespace hydra {
 
+// Tiles whose epilogue gave up waiting for the QK-mean terms (see
+// ccgqa_prep_mfma_kernel); read by hydra_ccgqa_prep_faults.  Stays 0 unless
+// the hardware or the compiler breaks the kernel's forward-progress
+// assumptions.
+__device__ unsigned int g_prep_wait_faults = 0;
+
 template <typename T>
 __device__ __forceinline__ float rnd(float v) {
   return to_f32(from_f32<T>(v));
@@ -1071,18 +1077,34 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
       if (wave < ntask) {
         mfma(wave, acc);
         if (qk_mean) {
-          for (int spin = 0; spin < (1 << 22); ++spin) {
-            if (__hip_atomic_load(qa_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW - ntask)
-              break;
-            __builtin_amdgcn_s_sleep(2);
+          // Every lane of every term wave adds 1 with release order after
+          // its own term writes; the acquire load that reads the final
+          // count synchronises with all of those adds (one release
+          // sequence), so the terms are visible to the epilogue's reads.
+          const int want = 64 * (NW - ntask);
+          bool ready = false;
+          for (int spin = 0; spin < (1 << 22) && !ready; ++spin) {
+            ready = __hip_atomic_load(qa_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= want;
+            if (!ready) __builtin_amdgcn_s_sleep(2);
+          }
+          if (!ready) {
+            // Cannot happen while the term waves run (they wait for
+            // nothing); if it ever does, the tile's outputs become NaN and
+            // the fault is counted for hydra_ccgqa_prep_faults, rather than
+            // an epilogue over incomplete terms.
+            if (lane == 0) atomicAdd(&g_prep_wait_faults, 1u);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+              for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[m][j][i] = __builtin_nanf("");
           }
         }
         epilogue(wave, acc);
       } else {
         qa_work(ntask);
-        // LDS operations of one wave complete in order: the QA writes land
-        // before the count does
-        if (lane == 0) atomicAdd(qa_done, 1);
+        __hip_atomic_fetch_add(qa_done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         v_work(ntask);
       }
     } else {
@@ -1197,6 +1219,13 @@ static int launch_prep_generic(const void* qkv, int64_t qkv_rs, const void* wq1,
 }  // namespace hydra
 
 using namespace hydra;
+
+extern "C" int hydra_ccgqa_prep_faults(unsigned int* count) {
+  if (!count) return hydra::fail(HYDRA_ERR_ARG, "hydra_ccgqa_prep_faults: null count");
+  const hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(hydra::g_prep_wait_faults), sizeof(unsigned int));
+  if (e != hipSuccess) return hydra::fail(HYDRA_ERR_LAUNCH, std::string("hydra_ccgqa_prep_faults: ") + hipGetErrorString(e));
+  return HYDRA_OK;
+}
 
 extern "C" int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype) {
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;

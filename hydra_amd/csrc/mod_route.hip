@@ -628,13 +628,19 @@ extern "C" int hydra_mod_topk(const void* scores, int64_t B, int64_t L, int64_t 
   int ept = 1;
   while (ept * kTopkThreads < L) ept <<= 1;
   const int P = ept * kTopkThreads;
-  const bool bucket = L <= kBucketMaxL && !force_bitonic;
-  const size_t lds = bucket ? sizeof(uint64_t) * (P + kKeyPad) + sizeof(uint32_t) * kBinWords +
-                                2 * sizeof(uint32_t) * (P / 32)
-                            : sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);
+  // The bucket kernel's 16K-bin histogram needs ~90-146 KiB of LDS; on a
+  // device with less per workgroup the row takes the bitonic kernel, and a
+  // row that fits neither takes the device-wide sort.
+  const size_t lds_bucket = sizeof(uint64_t) * (P + kKeyPad) + sizeof(uint32_t) * kBinWords +
+                            2 * sizeof(uint32_t) * (P / 32);
+  const size_t lds_bitonic = sizeof(uint64_t) * P + sizeof(uint32_t) * ((L + 31) / 32);
+  const size_t lds_cap = static_cast<size_t>(max_lds_per_block());
+  const bool bucket = L <= kBucketMaxL && !force_bitonic && lds_bucket + 1024 <= lds_cap;
+  const size_t lds = bucket ? lds_bucket : lds_bitonic;
   const int R = static_cast<int>((L + kTopkThreads - 1) / kTopkThreads);  // bucket kernel: parts per row
-  if (lds + 1024 > static_cast<size_t>(max_lds_per_block()))
-    return fail(HYDRA_ERR_UNSUPPORTED, "mod_topk: row does not fit in LDS on this device");
+  if (lds + 1024 > lds_cap)
+    return mod_topk_large(scores, B, L, s_rs, k, idx_desc, idx_sorted, mask, score_dtype, mask_dtype,
+                          static_cast<hipStream_t>(stream));
   auto st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(B));
   auto go = [&](auto s_tag, auto e_tag) {

@@ -144,7 +144,9 @@ class _ScatterRows(torch.autograd.Function):
             g_sel = _gather(grad, idx)
         g_vals = g_w = None
         if ctx.needs_input_grad[1]:
-            g_vals = g_sel if weights is None else g_sel * weights.to(g_sel.dtype)[..., None]
+            # the forward adds fmaf(w, v, out) with the fp32 weight: the
+            # product takes the fp32 weight and rounds once
+            g_vals = g_sel if weights is None else g_sel.float() * weights.float()[..., None]
             g_vals = g_vals.to(values.dtype)
         if weights is not None and ctx.needs_input_grad[3]:
             g_w = (g_sel.float() * values.float()).sum(-1).to(weights.dtype)

@@ -200,6 +200,13 @@ int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
  * host which conv-weight layout to pack. */
 int hydra_ccgqa_prep_tiled_ok(int64_t Hq, int64_t Hkv, int64_t hd, int dtype);
 
+/* Number of hydra_ccgqa_prep_fwd tiles on the current device, since the
+ * library was loaded, whose epilogue timed out waiting for the QK-mean
+ * terms of its own workgroup (their outputs are written as NaN).  Always 0
+ * on a working device; a health check for tests.  Synchronous (reads a
+ * device counter).  No counterpart in the reference. */
+int hydra_ccgqa_prep_faults(unsigned int* count);
+
 /* Backward of hydra_ccgqa_prep_fwd's pointwise chain: what torch autograd
  * computes through attention.py:211-266 (value shift, QK-mean, F.normalize
  * with the key temperature, RoPE) given the gradients dq [B,Hq,S,hd] and
@@ -464,6 +471,27 @@ int hydra_mod_scatter(void* out, const void* y, const int64_t* idx,
  * one-pass HBM-bound kernel.  bytes % 16 == 0, both pointers 16-byte
  * aligned, the ranges must not overlap. */
 int hydra_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/* The shader clock under matrix-core load: nwg workgroups of 8 waves each
+ * run `iters` iterations of four bf16 32x32x16 MFMAs and 16 v_exp_f32 (the
+ * attention tile's instruction kinds) and write, per workgroup, 5 uint64
+ * to stamps (device memory): shader-clock counter (s_memtime) before and
+ * after, wall-clock counter (s_memrealtime) before and after, and a sink
+ * value.  *wall_khz receives the wall clock's constant rate.  The clock is
+ * sum(shader ticks) / sum(wall ticks) * wall_khz.  No counterpart in the
+ * reference: bench.py reports the clock the matrix-core fraction was
+ * reached at. */
+int hydra_clock_probe(void* stamps, int nwg, int iters, int64_t* wall_khz, void* stream);
+
+/* Installs (stamps != NULL) or removes (NULL) a device buffer of
+ * 4 * max_workgroups uint64 into which every later launch of
+ * hydra_attn_fwd's key-split kernel with at most max_workgroups
+ * workgroups writes, per workgroup: the shader-clock counter (s_memtime)
+ * at its start and after its last store, and the wall-clock counter
+ * (s_memrealtime) at the same two points.  Process-wide; the caller keeps
+ * the buffer alive while installed.  No counterpart in the reference:
+ * bench.py reads the clock the attention kernel itself ran at. */
+int hydra_attn_clock_stamps(void* stamps, int64_t max_workgroups);
 
 #ifdef __cplusplus
 }

@@ -43,7 +43,7 @@ def test_abi_version_and_error_path():
     from hydra_amd import _lib
 
     lib = _lib.load()
-    assert lib.hydra_abi_version() == 109
+    assert lib.hydra_abi_version() == 110
     # dim = 0 is rejected before any HIP call
     rc = lib.hydra_rms_norm_fwd(None, None, None, 4, 0, 0, 0, ctypes.c_float(1e-6), 1, None)
     assert rc == _lib.ERR_ARG

@@ -31,6 +31,7 @@ CASES = [
     (1, 2, 2, 1, 64),
     (1, 4, 2, 31, 64),
     (3, 6, 3, 65, 16),
+    (2, 28, 4, 520, 16),  # config 5's heads: groups of 7, head_dim 16
 ]
 
 
@@ -289,6 +290,7 @@ FIXED_CASES = [
     (2, 8, 1, 100, 128, 11.3, True),
     (1, 2, 1, 64, 64, -8.0, False),
     (1, 4, 1, 2048, 64, 40.0, True),
+    (2, 28, 4, 300, 16, 4.0, True),  # config 5's heads, temperature sqrt(16)
 ]
 
 
@@ -358,6 +360,7 @@ VT_CASES = [
     (1, 4, 2, 8, 64),
     (3, 6, 3, 72, 16),
     (1, 8, 1, 1000, 64),
+    (2, 28, 4, 264, 16),  # config 5's heads: groups of 7, head_dim 16
 ]
 VT_MODES = [(True, "none"), (False, "none"), (True, "key_padding"), (False, "key_padding"),
             (True, "reference")]
@@ -413,6 +416,7 @@ FIXED_VT_CASES = [
     (2, 8, 1, 104, 128, 11.3, True),
     (1, 2, 1, 64, 64, -8.0, False),
     (1, 4, 1, 2048, 64, 40.0, True),
+    (2, 28, 4, 304, 16, 4.0, True),  # config 5's heads, temperature sqrt(16)
 ]
 
 

@@ -259,3 +259,61 @@ def test_hydra_model_bf16_decisions(cuda):
             for b in range(own.shape[0]):
                 inter = len(set(own[b].tolist()) & set(rec[i][key][b].tolist()))
                 assert inter >= 0.95 * k
+
+
+def _capture_decisions(m):
+    """Forward hooks that record each layer's MoD selections (per call) and,
+    after the forward, its MoR depths: the forcing input of
+    oracle.blocks.hydra_model."""
+    rec = [dict() for _ in m.layers]
+    calls = [0] * len(m.layers)
+
+    def hook(li):
+        def fn(mod, inp, out):
+            rec[li][f"mod_idx{calls[li]}"] = mod._last_indices.cpu()
+            calls[li] += 1
+        return fn
+
+    hs = [l.mod_mlp_wrapper.register_forward_hook(hook(i)) for i, l in enumerate(m.layers)
+          if l.mod_mlp_wrapper is not None]
+
+    def finish():
+        for h in hs:
+            h.remove()
+        for i, l in enumerate(m.layers):
+            rec[i]["depths"] = l._last_depths.cpu()
+        return rec
+    return finish
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_hydra_model_c5_layout(cuda, dtype):
+    """Config 5's layer widths at reduced depth and length: dim 1792, 28 q /
+    4 kv heads of 16 (groups of 7), latent 448, mlp_ratio 3.6 (hidden
+    6656), 3 MoR blocks x 2 recursions with MoD (capacity 0.75) on the
+    middle block, tied LM head (vocab 1000).  The device's routing
+    decisions are handed to the oracle (oracle/blocks.py:hydra_model,
+    restating model.py:408-502 and blocks.py:431-756), which runs the same
+    weights on the CPU in the same dtype; logits within 1e-5 (fp32) /
+    2e-2 (bf16)."""
+    from hydra_amd.model.framework import HydraModel
+
+    torch.manual_seed(5)
+    kw = dict(vocab_size=1000, dim=1792, n_mor_blocks=3, recursions_per_block=2, n_heads=28,
+              n_kv_heads=4, compression_factor=4, max_seq_len=128, mod_capacity=0.75)
+    m = HydraModel(mlp_ratio=3.6, adaptive=True, tie_weights=True, **kw)
+    m.set_global_step(10000)
+    params = {k: v.detach().clone() for k, v in m.state_dict().items()}
+    if dtype != torch.float32:
+        params = {k: v.to(dtype) if v.is_floating_point() else v for k, v in params.items()}
+    m = m.to(device=cuda, dtype=dtype).eval()
+    g = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, 1000, (2, 64), generator=g)
+    finish = _capture_decisions(m)
+    with torch.no_grad():
+        logits = m(ids.to(cuda)).float().cpu()
+    rec = finish()
+    assert any(k.startswith("mod_idx") for k in rec[1]), "MoD ran on the middle block"
+    cfg = ob.ModelConfig(**kw)
+    want = ob.hydra_model(params, ids, cfg, forces=rec).float()
+    assert max_rel_err(logits, want) < TOL[dtype]

@@ -105,6 +105,10 @@ def test_prep_kernel(cuda, case, dtype):
                                 cos=cos.to(cuda), sin=sin.to(cuda))
         assert torch.equal(q3.cpu(), q.cpu()) and torch.equal(k3.cpu(), k.cpu())
         assert torch.equal(v3.cpu(), v.cpu())
+    # no tile's epilogue gave up waiting for its QK-mean terms
+    from hydra_amd import _lib
+
+    assert _lib.prep_faults() == 0
 
 
 def _bench_case(dim, n_heads, n_kv_heads, B, S, dtype, temperature, seed):

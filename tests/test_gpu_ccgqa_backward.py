@@ -159,3 +159,33 @@ def test_module_backward_with_mask_raises(cuda):
     out = m(x, mask=torch.ones(1, 16, dtype=torch.long, device=cuda))
     with pytest.raises(NotImplementedError):
         out.sum().backward()
+
+
+def test_module_eval_under_grad_uses_inference_kernels(cuda):
+    """model.eval() with parameters that require grad, outside no_grad:
+    the forward runs the inference kernels (the same bits as under
+    no_grad), and a backward recomputes the training path, giving the
+    gradients train() mode gives for the same input."""
+    from hydra_amd.attention import CCGQAAttention
+
+    torch.manual_seed(7)
+    m = CCGQAAttention(dim=1024, n_heads=4, n_kv_heads=1, compression_factor=4,
+                       max_seq_len=256).to(cuda, torch.bfloat16)
+    with torch.no_grad():
+        m.key_temperature.fill_(1.0)
+    x = torch.randn(2, 256, 1024, device=cuda, dtype=torch.bfloat16)
+    gout = torch.randn(2, 256, 1024, device=cuda, dtype=torch.bfloat16)
+    m.eval()
+    with torch.no_grad():
+        want = m(x)
+    got = m(x)
+    assert got.requires_grad and torch.equal(got.detach(), want)
+    got.backward(gout)
+    eval_grads = {n: p.grad.clone() for n, p in m.named_parameters()}
+    m.zero_grad(set_to_none=True)
+    m.train()
+    out = m(x)
+    assert max_rel_err(out.detach().float().cpu(), want.float().cpu()) < 2e-2
+    out.backward(gout)
+    for n, p in m.named_parameters():
+        assert torch.equal(p.grad, eval_grads[n]), n
