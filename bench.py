@@ -482,9 +482,11 @@ def _bench_fused_backward(dev, g, iters):
     gw = torch.empty(D, device=dev, dtype=bf)
     sets = [(torch.randn(N, D, device=dev, generator=g).to(bf), torch.randn(N, D, device=dev, generator=g).to(bf),
              torch.empty(N, D, device=dev, dtype=bf)) for _ in range(6)]
+    need = _lib.query("hydra_rms_norm_bwd_workspace", N, D)
+    ws = _lib.scratch(need, w)
     ms = _time_rotating(lambda x, gy, gx: _lib.call(
         "hydra_rms_norm_bwd", x.data_ptr(), w.data_ptr(), gy.data_ptr(), gx.data_ptr(), gw.data_ptr(),
-        N, D, D, D, D, 1e-6, _lib.dtype_code(x), _lib.dtype_code(w), st(x)), sets, iters)
+        N, D, D, D, D, 1e-6, _lib.dtype_code(x), _lib.dtype_code(w), ws.data_ptr(), need, st(x)), sets, iters)
     nbytes = 3 * N * D * 2 + 2 * D * 2
     res["rms_norm_bwd"] = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6}
     del sets

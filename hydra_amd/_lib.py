@@ -42,7 +42,8 @@ SIGNATURES = {
     "hydra_rope_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _I64, _I, _I, _P],
     "hydra_swiglu_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_qk_norm_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _P],
-    "hydra_rms_norm_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
+    "hydra_rms_norm_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P, _I64, _P],
+    "hydra_rms_norm_bwd_workspace": [_I64, _I64],
     "hydra_rms_norm_bwd_noalloc": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
     "hydra_rope_bwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _I64, _I, _I, _P],
     "hydra_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
@@ -50,9 +51,14 @@ SIGNATURES = {
     "hydra_ccgqa_prep_fwd": [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P,
                              _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_attn_fwd": [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64,
-                       _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _P, _I, _I, _P],
+                       _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _P, _I, _I, _P, _I64, _P],
+    "hydra_attn_fwd_workspace": [_I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _I64P, _I, _I, _I,
+                                 _I64P],
     "hydra_attn_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
-                       _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I, _F, _I, _P],
+                       _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _P, _I, _I, _F, _I, _P,
+                       _I64, _P],
+    "hydra_attn_bwd_workspace": [_I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
+                                 _I64P, _I64P, _I, _I, _I, _I64P],
     "hydra_linear_fwd": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_ce_rows": [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I, _P],
     "hydra_ccgqa_prep_tiled_ok": [_I64, _I64, _I64, _I],
@@ -73,6 +79,9 @@ SIGNATURES = {
     "hydra_clock_probe": [_P, _I, _I, _I64P, _P],
     "hydra_attn_clock_stamps": [_P, _I64],
 }
+
+# entry points that return a value (not a status) of type int64_t
+_RETURNS_INT64 = {"hydra_rms_norm_bwd_workspace"}
 
 _lib = None
 
@@ -97,7 +106,7 @@ def load() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = ctypes.c_int64 if name in _RETURNS_INT64 else ctypes.c_int
         _lib = lib
     return _lib
 
@@ -144,6 +153,12 @@ def prep_faults() -> int:
     n = ctypes.c_uint(0)
     call("hydra_ccgqa_prep_faults", ctypes.byref(n))
     return int(n.value)
+
+
+def scratch(nbytes: int, like: torch.Tensor) -> torch.Tensor:
+    """Device scratch of nbytes from torch's caching allocator on like's
+    device (the library owns no memory between calls)."""
+    return torch.empty(max(int(nbytes), 0), dtype=torch.uint8, device=like.device)
 
 
 def query(name: str, *args) -> int:

@@ -14,9 +14,11 @@ non-persistent RoPE buffers (cos_cached, sin_cached).  The forward is
                                                     written as [B, S, L]
     out  = o @ W_o^T * output_scale                 torch GEMM
 
-With autograd recording (and no padding mask) the forward goes through
-CCGQAPrepFunction and CCGQAAttentionFused instead, whose backwards are the
-HIP prep backward (plus the convs' GEMMs) and the HIP attention backward.
+With autograd recording the forward goes through CCGQAPrepFunction and
+CCGQAAttentionFused (MaskedAttentionFunction with a padding mask) instead,
+whose backwards are the HIP prep backward (plus the convs' GEMMs) and the
+HIP attention backward; in eval() mode with grad-enabled parameters the
+inference kernels run and a backward recomputes the training path.
 
 The reference's precomputed [max_seq_len, max_seq_len] causal mask buffer is
 not kept: the kernel derives causality from indices.
@@ -30,10 +32,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ...._autograd import track
 from ...._lib import CCGQA_V_TRANSPOSED, CCGQA_W_TILED, MASK_KEY_PADDING, MASK_REFERENCE_SDPA
 from .autograd import ccgqa_prep_train
-from .kernels.fused_attention import CCGQAAttentionFused
+from .kernels.fused_attention import CCGQAAttentionFused, MaskedAttentionFunction
 from .kernels.fused_conv import OptimizedConvSequence
 from .ops import (attention_forward, ccgqa_prep, linear_weight_ok, output_projection, pack_conv_weight,
                   pack_linear_weight, prep_flags, tiled_weights_ok)
@@ -63,12 +64,13 @@ class _EvalRecompute(torch.autograd.Function):
     whose forward equals the inference forward within bf16 rounding."""
 
     @staticmethod
-    def forward(ctx, module, x, *params):
+    def forward(ctx, module, x, mask, *params):
         ctx.module = module
+        ctx.mask = mask
         ctx.save_for_backward(x)
         qkv = F.linear(x, module.qkv_proj.weight)
         flags, convw = module._prep_args()
-        return module._forward_infer(x, qkv, flags, convw, None)
+        return module._forward_infer(x, qkv, flags, convw, mask)
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -79,12 +81,12 @@ class _EvalRecompute(torch.autograd.Function):
             xr = x.detach().requires_grad_(ctx.needs_input_grad[1])
             qkv = F.linear(xr, m.qkv_proj.weight)
             flags, convw = m._prep_args()
-            out = m._forward_train(qkv, flags, convw)
+            out = m._forward_train(qkv, flags, convw, ctx.mask)
             wrt = ([xr] if xr.requires_grad else []) + [p for p in params if p.requires_grad]
             grads = list(torch.autograd.grad(out, wrt, grad_out, allow_unused=True))
         dx = grads.pop(0) if xr.requires_grad else None
         dparams = [grads.pop(0) if p.requires_grad else None for p in params]
-        return (None, dx, *dparams)
+        return (None, dx, None, *dparams)
 
 
 class CCGQAAttention(nn.Module):
@@ -148,18 +150,18 @@ class CCGQAAttention(nn.Module):
         if self.use_rope and S > self.cos_cached.shape[2]:
             raise ValueError(f"CCGQAAttention: sequence length {S} exceeds the RoPE cache "
                              f"({self.cos_cached.shape[2]})")
-        recording = mask is None and torch.is_grad_enabled() and (
+        recording = torch.is_grad_enabled() and (
             x.requires_grad or any(p.requires_grad for p in self.parameters()))
         if recording and not (self.training or x.requires_grad):
             # eval() with parameters that require grad: the inference kernels
             # give the output; a backward, if one comes, recomputes the
             # forward through the training path (as activation checkpointing
             # would) instead of keeping its activations now.
-            return _EvalRecompute.apply(self, x, *self.parameters())
+            return _EvalRecompute.apply(self, x, mask, *self.parameters())
         qkv = F.linear(x, self.qkv_proj.weight)
         flags, convw = self._prep_args()
         if recording:
-            return self._forward_train(qkv, flags, convw)
+            return self._forward_train(qkv, flags, convw, mask)
         return self._forward_infer(x, qkv, flags, convw, mask)
 
     def _prep_args(self):
@@ -195,21 +197,19 @@ class CCGQAAttention(nn.Module):
                               key_mask=mask, mask_mode=_mask_mode() if mask is not None else 0,
                               out=o_view,
                               bound_temperature=self.key_temperature if self.use_qk_norm else None)
-        # A padding mask has no backward here (the attention backward takes
-        # none): a recorded graph through it raises instead of going silent.
-        out = track(out, x, self.qkv_proj.weight, self.key_temperature, *convw)
         w_o = self.o_proj.weight
         out = output_projection(out, w_o, self._packed_o_proj() if linear_weight_ok(w_o) else None)
         if self.output_scale != 1.0:
             out = out * self.output_scale
         return out
 
-    def _forward_train(self, qkv: torch.Tensor, flags: int, convw) -> torch.Tensor:
-        """The forward with autograd (no padding mask): CCGQAPrepFunction
-        (prep kernel forward; pointwise backward kernel plus the convs'
-        backward as GEMMs), then CCGQAAttentionFused (the HIP attention
-        forward and backward), as the reference trains attention.py:201-331
-        through autograd."""
+    def _forward_train(self, qkv: torch.Tensor, flags: int, convw, mask=None) -> torch.Tensor:
+        """The forward with autograd: CCGQAPrepFunction (prep kernel forward;
+        pointwise backward kernel plus the convs' backward as GEMMs), then
+        CCGQAAttentionFused (the HIP attention forward and backward) or, with
+        a padding mask, MaskedAttentionFunction (the same kernels with the
+        key mask), as the reference trains attention.py:201-331 through
+        autograd."""
         B, S, _ = qkv.shape
         w = tuple(convw) if self.use_convs else (None,) * 4
         q, k, v = ccgqa_prep_train(
@@ -217,7 +217,10 @@ class CCGQAAttention(nn.Module):
             temperature=self.key_temperature if self.use_qk_norm else None,
             cos=self.cos_cached if self.use_rope else None,
             sin=self.sin_cached if self.use_rope else None)
-        o = CCGQAAttentionFused.apply(q, k, v, True, True)
+        if mask is None:
+            o = CCGQAAttentionFused.apply(q, k, v, True, True)
+        else:
+            o = MaskedAttentionFunction.apply(q, k, v, mask.to(q.device), _mask_mode(), True)
         out = F.linear(o.transpose(1, 2).reshape(B, S, self.latent_dim), self.o_proj.weight)
         if self.output_scale != 1.0:
             out = out * self.output_scale

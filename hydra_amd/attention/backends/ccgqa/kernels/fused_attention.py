@@ -33,6 +33,31 @@ class CCGQAAttentionFused(torch.autograd.Function):
         return dq, dk, dv, None, None
 
 
+class MaskedAttentionFunction(torch.autograd.Function):
+    """Attention with a padding mask: the SDPA call of CCGQAAttention.forward
+    with its combined causal / padding attn_mask (attention.py:268-299),
+    which the reference trains through autograd.  (q, k, v, key_mask [B,S],
+    mask_mode, causal) -> out; the backward runs hydra_attn_bwd with the
+    same mask."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, key_mask, mask_mode, causal):
+        want = any(ctx.needs_input_grad[:3])
+        out, lse = attention_forward(q, k, v, causal=bool(causal), key_mask=key_mask,
+                                     mask_mode=int(mask_mode), want_lse=want)
+        if want:
+            ctx.save_for_backward(q, k, v, out, lse, key_mask)
+        ctx.causal, ctx.mask_mode = bool(causal), int(mask_mode)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, out, lse, key_mask = ctx.saved_tensors
+        dq, dk, dv = attention_backward(q, k, v, out, lse, grad_out, causal=ctx.causal,
+                                        key_mask=key_mask, mask_mode=ctx.mask_mode)
+        return dq, dk, dv, None, None, None
+
+
 def ccgqa_attention_fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           is_causal: bool = False, use_fused_backward: bool = True) -> torch.Tensor:
     """Public API of the fused CCGQA attention (fused_attention.py:826-840)."""

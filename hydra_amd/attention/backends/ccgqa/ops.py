@@ -3,6 +3,8 @@
 here; strides, pointers and the current stream go to the library."""
 from __future__ import annotations
 
+import ctypes
+
 from typing import Optional
 
 import torch
@@ -142,22 +144,29 @@ def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
         bt = bt.reshape(-1)[:1].contiguous()
         _lib.require_gpu("attention_forward", bt)
     with torch.cuda.device(q.device):
+        st = (_lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out))
+        need = ctypes.c_int64(0)
+        _lib.call("hydra_attn_fwd_workspace", B, Hq, Hkv, S, hd, *st, 1 if causal else 0, mask_mode,
+                  _lib.dtype_code(q), ctypes.byref(need))
+        ws = _lib.scratch(need.value, q) if need.value else None
         _lib.call("hydra_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                  _lib.ptr(lse), _lib.ptr(km), mask_mode, B, Hq, Hkv, S, hd,
-                  _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
+                  _lib.ptr(lse), _lib.ptr(km), mask_mode, B, Hq, Hkv, S, hd, *st,
                   1 if causal else 0, sc, float(score_bound or 0.0), _lib.ptr(bt),
-                  0 if bt is None else _lib.dtype_code(bt), _lib.dtype_code(q), _lib.stream(q))
+                  0 if bt is None else _lib.dtype_code(bt), _lib.dtype_code(q), _lib.ptr(ws),
+                  need.value, _lib.stream(q))
     return out, lse
 
 
 def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                        lse: torch.Tensor, grad_out: torch.Tensor, *, causal: bool,
-                       scale: Optional[float] = None):
+                       scale: Optional[float] = None, key_mask: Optional[torch.Tensor] = None,
+                       mask_mode: int = MASK_NONE):
     """Gradients (dq, dk, dv) of attention_forward's output, from the forward's
     inputs, its output and its fp32 log-sum-exp (want_lse=True): the split-K
     backward of CCGQAAttentionFused (fused_attention.py:706-823, kernels
     :113-338 and :432-635).  dk and dv sum the Hq/Hkv query heads that share
-    a K/V head.  No key mask (the reference's fused backward has none)."""
+    a K/V head.  key_mask / mask_mode: those of the forward call (the
+    backward of the padding-mask SDPA call, attention.py:268-299)."""
     _lib.require_gpu("attention_backward", q, k, v, out, lse, grad_out)
     B, Hq, S, hd = q.shape
     Hkv = k.shape[1]
@@ -179,12 +188,23 @@ def attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: t
         torch.empty_like(k, memory_format=torch.contiguous_format), \
         torch.empty_like(v, memory_format=torch.contiguous_format)
     sc = float(hd ** -0.5) if scale is None else float(scale)
+    km = None
+    if mask_mode != MASK_NONE:
+        if key_mask is None or key_mask.shape != (B, S):
+            raise ValueError(f"attention_backward: key mask must be [B,S] = [{B},{S}]")
+        _lib.require_gpu("attention_backward", key_mask)
+        km = (key_mask != 0).to(torch.uint8).contiguous()
     with torch.cuda.device(q.device):
+        st = (_lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(out),
+              _lib.strides(grad_out), _lib.strides(dq), _lib.strides(dk), _lib.strides(dv))
+        need = ctypes.c_int64(0)
+        _lib.call("hydra_attn_bwd_workspace", B, Hq, Hkv, S, hd, *st, mask_mode, 1 if causal else 0,
+                  _lib.dtype_code(q), ctypes.byref(need))
+        ws = _lib.scratch(need.value, q)
         _lib.call("hydra_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                   grad_out.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                  B, Hq, Hkv, S, hd, _lib.strides(q), _lib.strides(k), _lib.strides(v),
-                  _lib.strides(out), _lib.strides(grad_out), _lib.strides(dq), _lib.strides(dk),
-                  _lib.strides(dv), 1 if causal else 0, sc, _lib.dtype_code(q), _lib.stream(q))
+                  B, Hq, Hkv, S, hd, *st, _lib.ptr(km), mask_mode, 1 if causal else 0, sc,
+                  _lib.dtype_code(q), _lib.ptr(ws), need.value, _lib.stream(q))
     return dq, dk, dv
 
 

@@ -80,51 +80,6 @@ int blocks_per_cu(const void* kernel, int threads) {
   return nb;
 }
 
-// Library-owned scratch: one buffer per (device, stream, slot), grown on
-// demand and never freed (a buffer it outgrows is kept too), so a HIP graph
-// captured with a pointer from here stays valid.  Calls on one stream are
-// ordered by the stream, and eager calls on different streams get different
-// buffers, so concurrent streams do not share scratch.  A buffer cannot be
-// allocated under stream capture: a capturing stream without a large enough
-// buffer of its own takes one that an eager call on another stream of the
-// device already grew (the usual warm-up-then-capture pattern), and fails
-// when there is none.  Replays of such a graph share that buffer with the
-// stream that grew it; they must not overlap calls on that stream.
-int device_workspace(int slot, size_t bytes, hipStream_t st, void** out) {
-  struct Buf {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-  };
-  static std::mutex mu;
-  static std::map<std::tuple<int, hipStream_t, int>, Buf> bufs;
-  int dev = 0;
-  if (slot < 0 || slot >= kWorkspaceSlots) return fail(HYDRA_ERR_ARG, "workspace: bad slot");
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
-    return fail(HYDRA_ERR_LAUNCH, "workspace: no current device");
-  std::lock_guard<std::mutex> lock(mu);
-  Buf& w = bufs[std::make_tuple(dev, st, slot)];
-  if (w.bytes < bytes) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
-      for (const auto& kv : bufs) {
-        if (std::get<0>(kv.first) == dev && std::get<2>(kv.first) == slot && kv.second.bytes >= bytes) {
-          *out = kv.second.ptr;
-          return HYDRA_OK;
-        }
-      }
-      return fail(HYDRA_ERR_UNSUPPORTED,
-                  "workspace: the library's scratch buffer must grow, which cannot happen under "
-                  "graph capture; run the same shape once before capturing");
-    }
-    const size_t nb = std::max(bytes, 2 * w.bytes);
-    void* p = nullptr;
-    if (hipMalloc(&p, nb) != hipSuccess) return fail(HYDRA_ERR_LAUNCH, "workspace: allocation failed");
-    w.ptr = p;
-    w.bytes = nb;
-  }
-  *out = w.ptr;
-  return HYDRA_OK;
-}
 
 }  // namespace hydra
 
@@ -132,7 +87,7 @@ extern "C" const char* hydra_last_error(void) {
   return hydra::g_last_error.c_str();
 }
 
-extern "C" int hydra_abi_version(void) { return 110; }
+extern "C" int hydra_abi_version(void) { return 111; }
 
 // ---- same-device HBM copy (measurement aid) ---------------------------------
 // One 16-byte chunk per thread, non-temporal load and store, 256-thread

@@ -719,10 +719,22 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_kernel(
 // ---------------------------------------------------------------------------
 // Generic path: fp32 math, one thread per query row (dQ) or key row (dK, dV).
 // Rows of up to MAXD elements are accumulated in registers.
-template <typename T, int MAXD, bool CAUSAL>
+// Whether query s sees key t (t < S): causality, then the key mask
+// (MASK 1: key padding on top of causality; MASK 2: the forward's
+// reference-SDPA mode, key t > s or t padded, whatever `CAUSAL`).
+template <bool CAUSAL, int MASK>
+__device__ __forceinline__ bool bwd_visible(int s, int t, const uint8_t* kmrow) {
+  if constexpr (MASK == 2) return t > s || kmrow[t] == 0;
+  const bool c = !CAUSAL || t <= s;
+  if constexpr (MASK == 1) return c && kmrow[t] != 0;
+  return c;
+}
+
+template <typename T, int MAXD, bool CAUSAL, int MASK>
 __global__ __launch_bounds__(128) void attn_bwd_generic_dq_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
+    const uint8_t* __restrict__ kmask,
     T* __restrict__ dq, int64_t rows, int Hq, int Hkv, int S, int hd,
     int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
@@ -745,8 +757,10 @@ __global__ __launch_bounds__(128) void attn_bwd_generic_dq_kernel(
     acc[e] = 0.f;
   }
   const float l2 = lse2[r], dd = dvec[r];
-  const int tend = CAUSAL ? s + 1 : S;
+  const uint8_t* kmrow = MASK != 0 ? kmask + b * S : nullptr;
+  const int tend = CAUSAL && MASK != 2 ? s + 1 : S;
   for (int t = 0; t < tend; ++t) {
+    if (MASK != 0 && !bwd_visible<CAUSAL, MASK>(s, t, kmrow)) continue;
     const T* kr = k + b * ks0 + kvh * ks1 + t * ks2;
     const T* vr = v + b * vs0 + kvh * vs1 + t * vs2;
     float sc = 0.f, dpv = 0.f;
@@ -768,10 +782,11 @@ __global__ __launch_bounds__(128) void attn_bwd_generic_dq_kernel(
     if (e < hd) orow[e] = from_f32<T>(acc[e] * scale);
 }
 
-template <typename T, int MAXD, bool CAUSAL>
+template <typename T, int MAXD, bool CAUSAL, int MASK>
 __global__ __launch_bounds__(128) void attn_bwd_generic_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ dvec, const float* __restrict__ lse2,
+    const uint8_t* __restrict__ kmask,
     T* __restrict__ dk, T* __restrict__ dv, int64_t rows, int Hq, int Hkv, int S, int hd,
     int64_t qs0, int64_t qs1, int64_t qs2, int64_t ks0, int64_t ks1, int64_t ks2,
     int64_t vs0, int64_t vs1, int64_t vs2, int64_t ds0, int64_t ds1, int64_t ds2,
@@ -795,10 +810,12 @@ __global__ __launch_bounds__(128) void attn_bwd_generic_dkdv_kernel(
     ak[e] = 0.f;
     av[e] = 0.f;
   }
+  const uint8_t* kmrow = MASK != 0 ? kmask + b * S : nullptr;
   for (int g = 0; g < G; ++g) {
     const int h = kvh * G + g;
     const int64_t rb = (b * Hq + h) * S;
-    for (int s = CAUSAL ? t : 0; s < S; ++s) {
+    for (int s = CAUSAL && MASK != 2 ? t : 0; s < S; ++s) {
+      if (MASK != 0 && !bwd_visible<CAUSAL, MASK>(s, t, kmrow)) continue;
       const T* qr = q + b * qs0 + h * qs1 + s * qs2;
       const T* dr = dout + b * ds0 + h * ds1 + s * ds2;
       float sc = 0.f, dpv = 0.f;
@@ -837,6 +854,8 @@ struct BwdArgs {
   bool causal;
   float scale;
   hipStream_t st;
+  const uint8_t* kmask;  // [B, S], nonzero = keep (mask_mode != 0)
+  int mask_mode;
 };
 
 template <typename T>
@@ -936,7 +955,7 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* p
   return check_launch("attn_bwd: dq");
 }
 
-template <typename T, int MAXD, bool CAUSAL>
+template <typename T, int MAXD, bool CAUSAL, int MASK>
 int launch_generic(const BwdArgs& a, const float* dvec, const float* lse2) {
   const float sl2 = a.scale * kLog2e;
   const T* q = static_cast<const T*>(a.q);
@@ -945,34 +964,37 @@ int launch_generic(const BwdArgs& a, const float* dvec, const float* lse2) {
   const T* d = static_cast<const T*>(a.dout);
   const int64_t qrows = static_cast<int64_t>(a.B) * a.Hq * a.S;
   const int64_t krows = static_cast<int64_t>(a.B) * a.Hkv * a.S;
-  attn_bwd_generic_dkdv_kernel<T, MAXD, CAUSAL>
+  attn_bwd_generic_dkdv_kernel<T, MAXD, CAUSAL, MASK>
       <<<dim3(static_cast<unsigned>((krows + 127) / 128)), 128, 0, a.st>>>(
-          q, k, v, d, dvec, lse2, static_cast<T*>(a.dk), static_cast<T*>(a.dv), krows, a.Hq,
+          q, k, v, d, dvec, lse2, a.kmask, static_cast<T*>(a.dk), static_cast<T*>(a.dv), krows, a.Hq,
           a.Hkv, a.S, a.hd, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0],
           a.vs[1], a.vs[2], a.dos[0], a.dos[1], a.dos[2], a.dks[0], a.dks[1], a.dks[2],
           a.dvs[0], a.dvs[1], a.dvs[2], sl2, a.scale);
   if (int rc = check_launch("attn_bwd: generic dkdv")) return rc;
-  attn_bwd_generic_dq_kernel<T, MAXD, CAUSAL>
+  attn_bwd_generic_dq_kernel<T, MAXD, CAUSAL, MASK>
       <<<dim3(static_cast<unsigned>((qrows + 127) / 128)), 128, 0, a.st>>>(
-          q, k, v, d, dvec, lse2, static_cast<T*>(a.dq), qrows, a.Hq, a.Hkv, a.S, a.hd,
+          q, k, v, d, dvec, lse2, a.kmask, static_cast<T*>(a.dq), qrows, a.Hq, a.Hkv, a.S, a.hd,
           a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2],
           a.dos[0], a.dos[1], a.dos[2], a.dqs[0], a.dqs[1], a.dqs[2], sl2, a.scale);
   return check_launch("attn_bwd: generic dq");
 }
 
-template <typename T, bool CAUSAL>
+template <typename T, bool CAUSAL, int MASK>
 int launch_generic_d(const BwdArgs& a, const float* dvec, const float* lse2) {
-  if (a.hd <= 32) return launch_generic<T, 32, CAUSAL>(a, dvec, lse2);
-  if (a.hd <= 64) return launch_generic<T, 64, CAUSAL>(a, dvec, lse2);
-  if (a.hd <= 128) return launch_generic<T, 128, CAUSAL>(a, dvec, lse2);
-  return launch_generic<T, 256, CAUSAL>(a, dvec, lse2);
+  if (a.hd <= 32) return launch_generic<T, 32, CAUSAL, MASK>(a, dvec, lse2);
+  if (a.hd <= 64) return launch_generic<T, 64, CAUSAL, MASK>(a, dvec, lse2);
+  if (a.hd <= 128) return launch_generic<T, 128, CAUSAL, MASK>(a, dvec, lse2);
+  return launch_generic<T, 256, CAUSAL, MASK>(a, dvec, lse2);
 }
 
 template <typename T>
 int run_generic(const BwdArgs& a, float* dvec, float* lse2) {
   if (int rc = launch_rowdot<T>(a, dvec, lse2)) return rc;
-  return a.causal ? launch_generic_d<T, true>(a, dvec, lse2)
-                  : launch_generic_d<T, false>(a, dvec, lse2);
+  if (a.mask_mode == HYDRA_MASK_REFERENCE_SDPA) return launch_generic_d<T, true, 2>(a, dvec, lse2);
+  if (a.mask_mode == HYDRA_MASK_KEY_PADDING)
+    return a.causal ? launch_generic_d<T, true, 1>(a, dvec, lse2) : launch_generic_d<T, false, 1>(a, dvec, lse2);
+  return a.causal ? launch_generic_d<T, true, 0>(a, dvec, lse2)
+                  : launch_generic_d<T, false, 0>(a, dvec, lse2);
 }
 
 template <int HD>
@@ -987,13 +1009,26 @@ int run_mfma(const BwdArgs& a, float* dvec, float* lse2, float* part) {
 
 using namespace hydra;
 
-extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
-                              const void* grad_o, const float* lse, void* grad_q, void* grad_k,
-                              void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
-                              int64_t hd, const int64_t* qs, const int64_t* ks,
-                              const int64_t* vs, const int64_t* os, const int64_t* gos,
-                              const int64_t* gqs, const int64_t* gks, const int64_t* gvs,
-                              int causal, float scale, int dtype, void* stream) {
+// hydra_attn_bwd, or with need != nullptr the scratch bytes it would take
+// (no pointers needed; assumed 16-byte aligned, so the answer covers the
+// MFMA path whenever the shapes allow it).
+static int attn_bwd_impl(const void* q, const void* k, const void* v, const void* o,
+                         const void* grad_o, const float* lse, void* grad_q, void* grad_k,
+                         void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                         int64_t hd, const int64_t* qs, const int64_t* ks,
+                         const int64_t* vs, const int64_t* os, const int64_t* gos,
+                         const int64_t* gqs, const int64_t* gks, const int64_t* gvs,
+                         const uint8_t* key_mask, int mask_mode, int causal, float scale,
+                         int dtype, void* workspace, int64_t workspace_bytes, size_t* need,
+                         void* stream) {
+  if (need) *need = 0;
+  HYDRA_REQUIRE(workspace_bytes >= 0, "attn_bwd: negative workspace size");
+  HYDRA_REQUIRE(mask_mode >= HYDRA_MASK_NONE && mask_mode <= HYDRA_MASK_REFERENCE_SDPA,
+                "attn_bwd: unknown mask mode");
+  HYDRA_REQUIRE(mask_mode == HYDRA_MASK_NONE || key_mask != nullptr || need,
+                "attn_bwd: mask mode needs key_mask");
+  HYDRA_REQUIRE(mask_mode != HYDRA_MASK_REFERENCE_SDPA || causal,
+                "attn_bwd: the reference-SDPA mask mode is defined with causal=1");
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_bwd: bad size");
   HYDRA_REQUIRE(Hq % Hkv == 0, "attn_bwd: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(qs && ks && vs && os && gos && gqs && gks && gvs, "attn_bwd: null stride array");
@@ -1004,7 +1039,7 @@ extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const
   HYDRA_REQUIRE(dtype == HYDRA_F32 || dtype == HYDRA_BF16 || dtype == HYDRA_F16,
                 "attn_bwd: unknown dtype");
   if (B * S == 0) return HYDRA_OK;
-  HYDRA_REQUIRE(q && k && v && o && grad_o && lse && grad_q && grad_k && grad_v,
+  HYDRA_REQUIRE(need || (q && k && v && o && grad_o && lse && grad_q && grad_k && grad_v),
                 "attn_bwd: null pointer");
   HYDRA_REQUIRE(S < (int64_t(1) << 30) && B * Hq * S < (int64_t(1) << 31),
                 "attn_bwd: problem too large");
@@ -1013,24 +1048,32 @@ extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const
   const BwdArgs a{q, k, v, o, grad_o, lse, grad_q, grad_k, grad_v, static_cast<int>(B),
                   static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(S),
                   static_cast<int>(hd), qs, ks, vs, os, gos, gqs, gks, gvs, causal != 0, scale,
-                  st};
-  bool mfma_ok = dtype == HYDRA_BF16 && (hd == 32 || hd == 64 || hd == 128);
+                  st, mask_mode != HYDRA_MASK_NONE ? key_mask : nullptr, mask_mode};
+  // a key mask takes the VALU kernels
+  bool mfma_ok = dtype == HYDRA_BF16 && (hd == 32 || hd == 64 || hd == 128) && mask_mode == HYDRA_MASK_NONE;
   // Tiles are addressed with 32-bit byte offsets within one head's rows
   // (up to 64 rows past S).
   for (const int64_t* s : {qs, ks, vs, gos, gqs, gks, gvs})
     mfma_ok = mfma_ok && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= hd &&
               (S + 64) * s[2] * 2 < (int64_t(1) << 31);
-  for (const void* p : {q, k, v, grad_o, static_cast<const void*>(grad_q),
-                        static_cast<const void*>(grad_k), static_cast<const void*>(grad_v)})
-    mfma_ok = mfma_ok && aligned16(p);
+  if (!need)
+    for (const void* p : {q, k, v, grad_o, static_cast<const void*>(grad_q),
+                          static_cast<const void*>(grad_k), static_cast<const void*>(grad_v)})
+      mfma_ok = mfma_ok && aligned16(p);
   // Workspace: D and lse2 per query row, then the dK/dV chunk partials.
   const size_t rows_bytes = (static_cast<size_t>(rows) * 2 * sizeof(float) + 255) & ~size_t(255);
   const size_t part_bytes =
       mfma_ok ? plan_dkdv(static_cast<int>(hd), static_cast<int>(S), static_cast<int>(Hq / Hkv),
                           static_cast<int>(B * Hkv), causal != 0).part_bytes
               : 0;
-  void* ws = nullptr;
-  if (int rc = device_workspace(kWsAttnBwd, rows_bytes + part_bytes, st, &ws)) return rc;
+  if (need) {
+    *need = rows_bytes + part_bytes;
+    return HYDRA_OK;
+  }
+  if (workspace == nullptr || static_cast<size_t>(workspace_bytes) < rows_bytes + part_bytes)
+    return fail(HYDRA_ERR_ARG, "attn_bwd: workspace of " + std::to_string(rows_bytes + part_bytes) +
+                                   " bytes required (hydra_attn_bwd_workspace)");
+  void* ws = workspace;
   float* dvec = static_cast<float*>(ws);
   float* lse2 = dvec + rows;
   float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + rows_bytes);
@@ -1046,4 +1089,31 @@ extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const
     case HYDRA_BF16: return run_generic<bf16>(a, dvec, lse2);
     default: return run_generic<f16>(a, dvec, lse2);
   }
+}
+
+extern "C" int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                              const void* grad_o, const float* lse, void* grad_q, void* grad_k,
+                              void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                              int64_t hd, const int64_t* qs, const int64_t* ks,
+                              const int64_t* vs, const int64_t* os, const int64_t* gos,
+                              const int64_t* gqs, const int64_t* gks, const int64_t* gvs,
+                              const uint8_t* key_mask, int mask_mode, int causal, float scale,
+                              int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  return attn_bwd_impl(q, k, v, o, grad_o, lse, grad_q, grad_k, grad_v, B, Hq, Hkv, S, hd, qs, ks, vs, os,
+                       gos, gqs, gks, gvs, key_mask, mask_mode, causal, scale, dtype, workspace,
+                       workspace_bytes, nullptr, stream);
+}
+
+extern "C" int hydra_attn_bwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                                        const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                                        const int64_t* os, const int64_t* gos, const int64_t* gqs,
+                                        const int64_t* gks, const int64_t* gvs, int mask_mode,
+                                        int causal, int dtype, int64_t* bytes) {
+  HYDRA_REQUIRE(bytes != nullptr, "attn_bwd_workspace: null result pointer");
+  size_t need = 0;
+  const int rc = attn_bwd_impl(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, B,
+                               Hq, Hkv, S, hd, qs, ks, vs, os, gos, gqs, gks, gvs, nullptr, mask_mode, causal,
+                               1.f, dtype, nullptr, 0, &need, nullptr);
+  *bytes = static_cast<int64_t>(need);
+  return rc;
 }

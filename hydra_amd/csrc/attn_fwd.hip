@@ -646,7 +646,7 @@ __device__ __forceinline__ void attn_fwd_mfma_body(
       }
     }
   }
-  if (!started && tid == 0) desc[blockIdx.x] = make_int4(0, 0, 0, 0);
+  if (!per_item && !started && tid == 0) desc[blockIdx.x] = make_int4(0, 0, 0, 0);
 }
 
 // FXM: 0 running row max, 1 fixed reference (the host has bounded |q.k|),
@@ -1195,12 +1195,16 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_kernel(
 static unsigned long long* g_clock_stamps = nullptr;
 static int64_t g_clock_stamp_cap = 0;
 
+// With need != nullptr: only the plan -- *need = device scratch bytes the
+// launch takes (stream-K partials and merge descriptors; 0 otherwise), no
+// launch.  Otherwise the launch, with scratch from (ws, ws_bytes).
 template <int HD>
 static int launch_mfma(const void* q, const void* k, const void* v, void* o, float* lse,
                        const uint8_t* kmask, int mask_mode, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t S, const int64_t* qs, const int64_t* ks,
                        const int64_t* vs, const int64_t* os, bool causal, float scale,
-                       float score_bound, const void* tau, int tau_bf16, hipStream_t st) {
+                       float score_bound, const void* tau, int tau_bf16, void* ws_ptr,
+                       size_t ws_bytes, size_t* need, hipStream_t st) {
   constexpr int NW = 4;  // waves per workgroup; GQA heads share each staged K/V tile
   constexpr int DT = (HD + 31) / 32;
   // V with unit stride along the keys is read as V^T rows (vs[3] apart).
@@ -1260,6 +1264,10 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     if (sched && strcmp(sched, "kp") == 0) kp = vt && s32;
     if (getenv("HYDRA_ATTN_WGS")) kp = false;
     if (kp) {
+      if (need) {
+        *need = 0;
+        return HYDRA_OK;
+      }
       constexpr int KP = HD == 128 ? 2 : 3;  // key groups (LDS: KP double-buffered K/V^T tiles)
       auto kkern = attn_fwd_kp_kernel<HD, C, M, NW, KP, FX>;
       // one resident wave of workgroups, each taking two items (more
@@ -1301,13 +1309,21 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     }
     float* part = nullptr;
     int4* desc = nullptr;
-    // partial slots (stream-K only), then the merge descriptors
+    // stream-K: partial slots, then the merge descriptors (one workgroup
+    // per item takes none)
     const size_t pb = per_item ? 0 : static_cast<size_t>(2 * P) * NW * 64 * (DT * 8 + 2) * sizeof(float);
-    void* w = nullptr;
-    const int rc = device_workspace(kWsAttention, pb + static_cast<size_t>(P) * sizeof(int4), st, &w);
-    if (rc != HYDRA_OK) return rc;
-    part = static_cast<float*>(w);
-    desc = reinterpret_cast<int4*>(static_cast<char*>(w) + pb);
+    const size_t wb = per_item ? 0 : pb + static_cast<size_t>(P) * sizeof(int4);
+    if (need) {
+      *need = wb;
+      return HYDRA_OK;
+    }
+    if (wb > 0) {
+      if (ws_ptr == nullptr || ws_bytes < wb)
+        return fail(HYDRA_ERR_ARG, "attn_fwd: workspace of " + std::to_string(wb) +
+                                       " bytes required (hydra_attn_fwd_workspace)");
+      part = static_cast<float*>(ws_ptr);
+      desc = reinterpret_cast<int4*>(static_cast<char*>(ws_ptr) + pb);
+    }
     kern<<<dim3(static_cast<unsigned>(P)), 64 * NW, 0, st>>>(
         Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, T, per_item ? 1 : 0, part, desc,
         qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vt ? vs[3] : vs[2], os[0], os[1], os[2], sl2,
@@ -1561,13 +1577,18 @@ extern "C" int hydra_attn_clock_stamps(void* stamps, int64_t max_workgroups) {
   return HYDRA_OK;
 }
 
-extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
-                              float* lse, const uint8_t* key_mask, int mask_mode,
-                              int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
-                              const int64_t* qs, const int64_t* ks, const int64_t* vs,
-                              const int64_t* os, int causal, float scale,
-                              float score_bound, const void* bound_temperature,
-                              int bound_temperature_dtype, int dtype, void* stream) {
+// hydra_attn_fwd, or with need != nullptr the scratch bytes it would take
+// (pointers not needed then; they are assumed 16-byte aligned, so the
+// answer covers the MFMA path whenever the shapes allow it).
+static int attn_fwd_impl(const void* q, const void* k, const void* v, void* o,
+                         float* lse, const uint8_t* key_mask, int mask_mode,
+                         int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                         const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                         const int64_t* os, int causal, float scale,
+                         float score_bound, const void* bound_temperature,
+                         int bound_temperature_dtype, int dtype, void* workspace,
+                         int64_t workspace_bytes, size_t* need, void* stream) {
+  if (need) *need = 0;
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 1, "attn_fwd: bad size");
   HYDRA_REQUIRE(bound_temperature == nullptr || bound_temperature_dtype == HYDRA_BF16 ||
                     bound_temperature_dtype == HYDRA_F32,
@@ -1581,12 +1602,13 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
   HYDRA_REQUIRE(hd <= 256, "attn_fwd: head_dim must be <= 256");
   HYDRA_REQUIRE(mask_mode >= HYDRA_MASK_NONE && mask_mode <= HYDRA_MASK_REFERENCE_SDPA,
                 "attn_fwd: unknown mask mode");
-  HYDRA_REQUIRE(mask_mode == HYDRA_MASK_NONE || key_mask != nullptr,
+  HYDRA_REQUIRE(mask_mode == HYDRA_MASK_NONE || key_mask != nullptr || need,
                 "attn_fwd: mask mode needs key_mask");
+  HYDRA_REQUIRE(workspace_bytes >= 0, "attn_fwd: negative workspace size");
   HYDRA_REQUIRE(mask_mode != HYDRA_MASK_REFERENCE_SDPA || causal,
                 "attn_fwd: the reference-SDPA mask mode is defined with causal=1");
   if (B * S == 0) return HYDRA_OK;
-  HYDRA_REQUIRE(q && k && v && o, "attn_fwd: null pointer");
+  HYDRA_REQUIRE(need || (q && k && v && o), "attn_fwd: null pointer");
   HYDRA_REQUIRE(S < (int64_t(1) << 30), "attn_fwd: sequence too long");
   const uint8_t* km = mask_mode == HYDRA_MASK_NONE ? nullptr : key_mask;
   auto st = static_cast<hipStream_t>(stream);
@@ -1605,16 +1627,17 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
     strides8 = strides8 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && vs[3] % 8 == 0 && S % 8 == 0 &&
                vs[3] >= S && hd * vs[3] * 2 < lim;
   }
-  if (dtype == HYDRA_BF16 && mfma_shape && strides8 && aligned16(q) && aligned16(k) &&
-      aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0) {
+  if (dtype == HYDRA_BF16 && mfma_shape && strides8 &&
+      (need || (aligned16(q) && aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0))) {
     switch (hd) {
-      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
-      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
-      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
-      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, st);
+      case 16: return launch_mfma<16>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, workspace, static_cast<size_t>(workspace_bytes), need, st);
+      case 32: return launch_mfma<32>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, workspace, static_cast<size_t>(workspace_bytes), need, st);
+      case 64: return launch_mfma<64>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, workspace, static_cast<size_t>(workspace_bytes), need, st);
+      default: return launch_mfma<128>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, qs, ks, vs, os, causal != 0, scale, score_bound, bound_temperature, bound_temperature_dtype == HYDRA_BF16 ? 1 : 0, workspace, static_cast<size_t>(workspace_bytes), need, st);
     }
   }
   HYDRA_REQUIRE(B * Hq * S / 256 < (int64_t(1) << 31), "attn_fwd: too many rows");
+  if (need) return HYDRA_OK;  // the VALU kernels take no scratch
   const bool split_shape = hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128;
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     if (split_shape && getenv("HYDRA_ATTN_GENERIC") == nullptr)
@@ -1623,4 +1646,30 @@ extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void*
     return launch_generic<T>(q, k, v, o, lse, km, mask_mode, B, Hq, Hkv, S, hd, qs, ks, vs,
                              os, causal != 0, scale, st);
   });
+}
+
+extern "C" int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                              float* lse, const uint8_t* key_mask, int mask_mode,
+                              int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                              const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                              const int64_t* os, int causal, float scale,
+                              float score_bound, const void* bound_temperature,
+                              int bound_temperature_dtype, int dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  return attn_fwd_impl(q, k, v, o, lse, key_mask, mask_mode, B, Hq, Hkv, S, hd, qs, ks, vs, os, causal,
+                       scale, score_bound, bound_temperature, bound_temperature_dtype, dtype, workspace,
+                       workspace_bytes, nullptr, stream);
+}
+
+extern "C" int hydra_attn_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                                        const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                                        const int64_t* os, int causal, int mask_mode, int dtype,
+                                        int64_t* bytes) {
+  HYDRA_REQUIRE(bytes != nullptr, "attn_fwd_workspace: null result pointer");
+  size_t need = 0;
+  const int rc = attn_fwd_impl(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, mask_mode, B, Hq, Hkv, S,
+                               hd, qs, ks, vs, os, causal, 1.f, 0.f, nullptr, HYDRA_F32, dtype, nullptr, 0,
+                               &need, nullptr);
+  *bytes = static_cast<int64_t>(need);
+  return rc;
 }

@@ -441,12 +441,28 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
 // 3*CS steps are unrolled and the A fragments run through a ring of D
 // registers, so D L2 loads stay in flight behind the MFMAs; otherwise a
 // plain loop.
+template <int CS>
+struct ConvRing {
+  static constexpr int NSTEP = 3 * CS;
+  static constexpr int D = NSTEP < 12 ? NSTEP : 12;  // A steps in flight
+};
+
+// The first ConvRing<CS>::D A fragments of a conv task (see below), issued
+// ahead of the task (e.g. before the barrier that ends the staging).
+template <int CS>
+__device__ __forceinline__ void conv_ring_fill(const bf16* wbase, int64_t wtap, int wstep,
+                                               bf16x8_p (&ring)[ConvRing<CS>::D]) {
+#pragma unroll
+  for (int i = 0; i < ConvRing<CS>::D; ++i) ring[i] = ld_bf16x8(wbase + (i / CS) * wtap + wstep * (i % CS));
+}
+
 template <int NT, int CS, typename BRow>
 __device__ __forceinline__ void conv_task_fixed(const bf16* wbase, int64_t wtap, int wstep,
                                                 const uint16_t* bbase, BRow brow,
-                                                f32x16_p (&acc)[NT]) {
-  constexpr int NSTEP = 3 * CS;
-  constexpr int D = NSTEP < 12 ? NSTEP : 12;  // A steps in flight
+                                                f32x16_p (&acc)[NT],
+                                                const bf16x8_p* pre = nullptr) {
+  constexpr int NSTEP = ConvRing<CS>::NSTEP;
+  constexpr int D = ConvRing<CS>::D;  // A steps in flight
   bf16x8_p ring[D];
   bf16x8_p bq[2][NT];  // B fragments of this step and the next
   auto aptr = [&](int st) { return wbase + (st / CS) * wtap + wstep * (st % CS); };
@@ -455,7 +471,7 @@ __device__ __forceinline__ void conv_task_fixed(const bf16* wbase, int64_t wtap,
     for (int j = 0; j < NT; ++j) dst[j] = ld_bf16x8(bbase + brow(j, st / CS) + 16 * (st % CS));
   };
 #pragma unroll
-  for (int i = 0; i < D; ++i) ring[i] = ld_bf16x8(aptr(i));
+  for (int i = 0; i < D; ++i) ring[i] = pre ? pre[i] : ld_bf16x8(aptr(i));
   bload(0, bq[0]);
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) {
@@ -645,6 +661,22 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
   const bool tiled = flags & HYDRA_CCGQA_W_TILED;
   const int wstep = tiled ? 512 : 16;  // elements between k-steps
   const bf16* xb = qkv + static_cast<int64_t>(b) * S * qkv_rs;
+
+  // conv1 m-tile mt (32 output channels): its weight rows and input columns
+  const int nm1 = CW / 32;
+  auto conv1_w = [&](int mt) {
+    const int o0 = 32 * mt;
+    const bool is_q = o0 < L;
+    const int oo0 = is_q ? o0 : o0 - L;
+    return (is_q ? wq1 : wk1) + static_cast<int64_t>(oo0) * HD + (tiled ? 8 * lane : n * HD + 8 * hf);
+  };
+  auto conv1_wtap = [&](int mt) { return static_cast<int64_t>(32 * mt < L ? L : K) * HD; };
+  // The first m-tile's weight fragments go out before the staging, so
+  // their L2 latency overlaps the staging's HBM reads.
+  constexpr int CS1 = HD / 16;
+  bf16x8_p ring1[ConvRing<CS1>::D];
+  const bool pre1 = convs && HD != 16 && wave < nm1;
+  if (pre1) conv_ring_fill<CS1>(conv1_w(wave), conv1_wtap(wave), wstep, ring1);
 
   // ---- stage q0|k0 rows, v rows, RoPE angles --------------------------------
   if (tid == 0) *qa_done = 0;
@@ -886,15 +918,12 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
   // tokens < 0 come out 0 (their X rows are 0): conv2's causal padding.
   {
     constexpr int NT1 = NT + 1;
-    const int nm1 = CW / 32;
     for (int mt = wave; mt < nm1; mt += kPrepThreads / 64) {
       const int o0 = 32 * mt;
       const bool is_q = o0 < L;
       const int oo0 = is_q ? o0 : o0 - L;
-      const int O = is_q ? L : K;
       const int cbase = (is_q ? 0 : L) + (oo0 / HD) * HD;
-      const bf16* wbase = (is_q ? wq1 : wk1) + static_cast<int64_t>(oo0) * HD +
-                          (tiled ? 8 * lane : n * HD + 8 * hf);
+      const bf16* wbase = conv1_w(mt);
       f32x16_p acc[NT1];
 #pragma unroll
       for (int j = 0; j < NT1; ++j)
@@ -902,9 +931,11 @@ __global__ __launch_bounds__(kPrepThreads) void ccgqa_prep_mfma_kernel(
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
       auto brow1 = [&](int j, int t) { return min(32 * j + n + t, TT + 3) * RS; };
       if constexpr (HD == 16)
-        conv1_task_hd16<NT1>(wbase, static_cast<int64_t>(O) * HD, X + cbase + 8 * hf, brow1, n, acc);
+        conv1_task_hd16<NT1>(wbase, conv1_wtap(mt), X + cbase + 8 * hf, brow1, n, acc);
+      else if (mt == wave)  // the prefetched first m-tile
+        conv_task_fixed<NT1, CS1>(wbase, conv1_wtap(mt), wstep, X + cbase + 8 * hf, brow1, acc, ring1);
       else
-        conv_task<NT1>(wbase, static_cast<int64_t>(O) * HD, wstep, HD / 16, X + cbase + 8 * hf, brow1, acc);
+        conv_task<NT1>(wbase, conv1_wtap(mt), wstep, HD / 16, X + cbase + 8 * hf, brow1, acc);
 #pragma unroll
       for (int j = 0; j < NT1; ++j) {
         const int i = 32 * j + n;

@@ -160,12 +160,6 @@ int dtype_size(int dtype);
 int device_cus();
 // Workgroups of `kernel` (launched with `threads`) resident on one CU.
 int blocks_per_cu(const void* kernel, int threads);
-// Grow-only device scratch owned by the library, per device and slot.
-constexpr int kWorkspaceSlots = 4;
-constexpr int kWsAttention = 0;   // attention split partials + merge descriptors
-constexpr int kWsRmsNormBwd = 1;  // RMSNorm backward: per-block weight-gradient partials
-constexpr int kWsAttnBwd = 2;     // attention backward: per-row D and log2-domain lse
-int device_workspace(int slot, size_t bytes, hipStream_t st, void** out);
 
 }  // namespace hydra
 

@@ -987,7 +987,7 @@ static int rms_norm_bwd_check(const void* x, const void* w, const void* grad_y, 
 
 // ---- allocation-free variant ----------------------------------------------
 // hydra_rms_norm_bwd_noalloc keeps the weight-gradient partial rows in this
-// file-scope device array instead of the library's growable workspace, so
+// file-scope device array instead of caller-provided scratch, so
 // the call allocates nothing.  12 MiB per device (kRmsBwdParts rows of up to
 // kNoAllocMaxDim fp32), held until the process ends.  Every partial row the
 // reduction reads is written earlier in the same call, so nothing has to be
@@ -1037,21 +1037,24 @@ extern "C" int hydra_rms_norm_bwd_noalloc(const void* x, const void* w, const vo
                            w_dtype, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int64_t hydra_rms_norm_bwd_workspace(int64_t rows, int64_t dim) {
+  if (rows <= 0 || dim <= 0) return 0;
+  return static_cast<int64_t>(kRmsBwdParts) * dim * static_cast<int64_t>(sizeof(float));
+}
+
 extern "C" int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
                                   void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
-                                  int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream) {
+                                  int64_t gx_rs, float eps, int dtype, int w_dtype, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
   const int rc = rms_norm_bwd_check(x, w, grad_y, grad_x, grad_w, rows, dim, x_rs, gy_rs, gx_rs, dtype,
                                     w_dtype);
   if (rc != HYDRA_OK) return rc;
-  auto st = static_cast<hipStream_t>(stream);
-  void* ws = nullptr;
-  if (rows > 0) {
-    const int wrc = device_workspace(kWsRmsNormBwd, static_cast<size_t>(kRmsBwdParts) * dim * sizeof(float),
-                                     st, &ws);
-    if (wrc != HYDRA_OK) return wrc;
-  }
-  return rms_norm_bwd_body(x, w, grad_y, grad_x, grad_w, static_cast<float*>(ws), rows, dim, x_rs, gy_rs,
-                           gx_rs, eps, dtype, w_dtype, st);
+  const int64_t need = hydra_rms_norm_bwd_workspace(rows, dim);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(HYDRA_ERR_ARG, "rms_norm_bwd: workspace of " + std::to_string(need) +
+                                   " bytes required (hydra_rms_norm_bwd_workspace)");
+  return rms_norm_bwd_body(x, w, grad_y, grad_x, grad_w, static_cast<float*>(workspace), rows, dim, x_rs,
+                           gy_rs, gx_rs, eps, dtype, w_dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int hydra_rope_bwd(const void* grad_y, const void* cos, const void* sin, void* grad_x,

@@ -332,9 +332,11 @@ class _RMSNormFunction(torch.autograd.Function):
         gx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
         gw = torch.empty((dim,), dtype=w.dtype, device=x.device)
         with torch.cuda.device(x.device):
+            need = _lib.query("hydra_rms_norm_bwd_workspace", xv[0], dim)
+            ws = _lib.scratch(need, x)
             _lib.call("hydra_rms_norm_bwd", x.data_ptr(), w.data_ptr(), go.data_ptr(), gx.data_ptr(),
                       gw.data_ptr(), xv[0], dim, xv[1], ov[1], dim, ctx.eps, _lib.dtype_code(x),
-                      _lib.dtype_code(w), _lib.stream(x))
+                      _lib.dtype_code(w), ws.data_ptr(), need, _lib.stream(x))
         return gx, gw.to(ctx.w_dtype), None
 
 

@@ -98,17 +98,24 @@ int hydra_qk_norm_fwd(const void* q, const void* k, void* q_out, void* k_out,
  * w_dtype (`dtype`, or HYDRA_F32 for an fp32 master weight, read and
  * written in fp32 as the reference's kernel loads it,
  * fused_ops.py:1072, and casts its fp32 sum, :1244-1246).  The weight
- * gradient is summed in a fixed order (deterministic); uses a library-owned
- * scratch buffer of 2 KiB * dim per stream (grown on first use, so run a
- * shape once before capturing it in a graph). */
+ * gradient is summed in a fixed order (deterministic) through per-block
+ * partial rows in caller-provided device scratch `workspace` of
+ * workspace_bytes >= hydra_rms_norm_bwd_workspace(rows, dim) bytes (an
+ * error when smaller); the library keeps no memory between calls. */
 int hydra_rms_norm_bwd(const void* x, const void* w, const void* grad_y, void* grad_x,
                        void* grad_w, int64_t rows, int64_t dim, int64_t x_rs, int64_t gy_rs,
-                       int64_t gx_rs, float eps, int dtype, int w_dtype, void* stream);
+                       int64_t gx_rs, float eps, int dtype, int w_dtype, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* Device scratch bytes hydra_rms_norm_bwd needs for rows x dim (768 fp32
+ * partial rows of dim; 0 when rows or dim is 0).  Host-only, no device
+ * call.  No counterpart in the reference (its scratch is torch's). */
+int64_t hydra_rms_norm_bwd_workspace(int64_t rows, int64_t dim);
 
 /* hydra_rms_norm_bwd without any allocation: the same kernels and results
  * (bit for bit), with the weight-gradient partials in a fixed 12 MiB device
  * array of the library (one per device, held until the process ends) instead
- * of the growable workspace.  No counterpart in the reference: it is for
+ * of caller-provided scratch.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc).  Limit: dim <= 4096
  * (HYDRA_ERR_ARG beyond).  Calls that overlap on one device share the array
@@ -287,14 +294,28 @@ int hydra_causal_col2im(const void* in, void* out, int64_t out_rs, int64_t B, in
  *   key mask.  (No counterpart in the reference: its Triton kernel always
  *   keeps a running max.)
  * A query row with no visible key gets o = 0 (as CPU SDPA) and lse = -inf.
- * bf16 with hd in {16,32,64,128} runs on MFMA; other cases on the VALU. */
+ * bf16 with hd in {16,32,64,128} runs on MFMA; other cases on the VALU.
+ * workspace / workspace_bytes: caller-provided device scratch, at least
+ * hydra_attn_fwd_workspace(...) bytes for the same shapes and strides (the
+ * stream-K schedule's partials; 0 bytes, and NULL allowed, for every other
+ * schedule); the library keeps no memory between calls. */
 int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
                    float* lse, const uint8_t* key_mask, int mask_mode,
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
                    const int64_t* qs, const int64_t* ks, const int64_t* vs,
                    const int64_t* os, int causal, float scale,
                    float score_bound, const void* bound_temperature,
-                   int bound_temperature_dtype, int dtype, void* stream);
+                   int bound_temperature_dtype, int dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/* *bytes = device scratch hydra_attn_fwd needs for these shapes, strides,
+ * mask mode and dtype on the current device (pointers 16-byte aligned
+ * assumed; an upper bound otherwise).  Host-only, no device call.  No
+ * counterpart in the reference. */
+int hydra_attn_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                             const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                             const int64_t* os, int causal, int mask_mode, int dtype,
+                             int64_t* bytes);
 
 /* Causal / full GQA attention backward: given the forward's q, k, v, its
  * output o and lse (hydra_attn_fwd's fp32 [B,Hq,S] natural-log sum-exp of
@@ -302,22 +323,41 @@ int hydra_attn_fwd(const void* q, const void* k, const void* v, void* o,
  *   grad_v[b,j] = sum_g P^T grad_o,  grad_k[b,j] = sum_g dS^T q * scale,
  *   grad_q = dS k * scale,  dS = P (grad_o v^T - rowsum(grad_o * o)),
  * with P recomputed from lse, summing the G = Hq/Hkv query heads of K/V
- * head j.  No key mask.  fp32 accumulation, outputs rounded once; no
- * atomics (repeat calls are bit-identical).
+ * head j.  key_mask / mask_mode: the forward's ([B,S] uint8, nonzero =
+ * keep; HYDRA_MASK_KEY_PADDING or HYDRA_MASK_REFERENCE_SDPA, the latter
+ * with causal = 1), so P is zero exactly where the forward's was -- the
+ * backward of the padding-mask SDPA call (attention.py:268-299), which
+ * the reference trains through autograd.  fp32 accumulation, outputs
+ * rounded once; no atomics (repeat calls are bit-identical).
  * Replaces CCGQAAttentionFused.backward (kernels/fused_attention.py:706-823)
  * and its kernels _bwd_gqa_kv_kernel / _bwd_gqa_dq_kernel (:113-338) and
  * _bwd_kernel / _bwd_dq_kernel (:432-635).
  * q, o, grad_o, grad_q: [B,Hq,S,hd]; k, v, grad_k, grad_v: [B,Hkv,S,hd];
  * element strides *s[4], unit stride along hd for all.  bf16 with hd in
  * {32, 64, 128}, 16-byte aligned pointers and strides that are multiples of
- * 8 run on MFMA; every other case on the VALU path (hd <= 256).  Uses a
- * library-owned workspace of 8 * B * Hq * S bytes (grown on first use). */
+ * 8 and no key mask run on MFMA; every other case on the VALU path
+ * (hd <= 256).  Scratch
+ * (8 * B * Hq * S bytes of row statistics, plus the dK/dV chunk partials
+ * of long causal walks) comes from the caller: workspace_bytes >=
+ * hydra_attn_bwd_workspace(...) for the same shapes; the library keeps no
+ * memory between calls. */
 int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                    const void* grad_o, const float* lse, void* grad_q, void* grad_k,
                    void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
                    const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os,
                    const int64_t* gos, const int64_t* gqs, const int64_t* gks,
-                   const int64_t* gvs, int causal, float scale, int dtype, void* stream);
+                   const int64_t* gvs, const uint8_t* key_mask, int mask_mode, int causal,
+                   float scale, int dtype, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+/* *bytes = device scratch hydra_attn_bwd needs for these shapes and strides
+ * (pointers 16-byte aligned assumed; an upper bound otherwise).  Host-only,
+ * no device call.  No counterpart in the reference. */
+int hydra_attn_bwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
+                             const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                             const int64_t* os, const int64_t* gos, const int64_t* gqs,
+                             const int64_t* gks, const int64_t* gvs, int mask_mode, int causal,
+                             int dtype, int64_t* bytes);
 
 #define HYDRA_LINEAR_W_TILED 1 /* W in MFMA-fragment order (below)             */
 

@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "hydra_amd.h"
 
 def declared_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hydra_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(hydra_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -43,7 +43,7 @@ def test_abi_version_and_error_path():
     from hydra_amd import _lib
 
     lib = _lib.load()
-    assert lib.hydra_abi_version() == 110
+    assert lib.hydra_abi_version() == 111
     # dim = 0 is rejected before any HIP call
     rc = lib.hydra_rms_norm_fwd(None, None, None, 4, 0, 0, 0, ctypes.c_float(1e-6), 1, None)
     assert rc == _lib.ERR_ARG
@@ -60,11 +60,11 @@ def test_abi_version_and_error_path():
     with pytest.raises(ValueError, match="multiple of n_kv_heads"):
         st = (ctypes.c_int64 * 4)(0, 0, 0, 1)
         _lib.call("hydra_attn_fwd", None, None, None, None, None, None, 0, 1, 3, 2, 8, 16,
-                  st, st, st, st, 1, ctypes.c_float(0.25), ctypes.c_float(0.0), None, 0, 1, None)
+                  st, st, st, st, 1, ctypes.c_float(0.25), ctypes.c_float(0.0), None, 0, 1, None, 0, None)
     with pytest.raises(ValueError, match="mask mode needs key_mask"):
         st = (ctypes.c_int64 * 4)(0, 0, 0, 1)
         _lib.call("hydra_attn_fwd", None, None, None, None, None, None, 1, 1, 2, 2, 8, 16,
-                  st, st, st, st, 1, ctypes.c_float(0.25), ctypes.c_float(0.0), None, 0, 1, None)
+                  st, st, st, st, 1, ctypes.c_float(0.25), ctypes.c_float(0.0), None, 0, 1, None, 0, None)
     with pytest.raises(ValueError, match="unknown flag"):
         _lib.call("hydra_ccgqa_prep_fwd", None, 48, None, None, None, None, None, None, None, 0,
                   None, None, None, 1, 4, 2, 1, 16, 128, 1, None)

@@ -166,3 +166,47 @@ def test_attention_backward_in_hip_graph(cuda):
         torch.cuda.synchronize()
         for a, b in zip(got, want):
             assert torch.equal(a, b)
+
+
+MASK_CASES = [
+    # B, Hq, Hkv, S, hd, dtype
+    (2, 4, 2, 70, 32, torch.float32),
+    (2, 4, 1, 96, 64, torch.bfloat16),
+    (1, 6, 3, 40, 16, torch.float32),
+]
+
+
+@pytest.mark.parametrize("mode", ["key_padding", "reference"])
+@pytest.mark.parametrize("case", MASK_CASES, ids=[str(c[:5]) for c in MASK_CASES])
+def test_attention_backward_key_mask(cuda, case, mode):
+    """hydra_attn_bwd with the forward's key mask: both mask modes against
+    fp64 autograd through the oracle's masked forward (key padding: the
+    explicit masked softmax attention_key_padding; reference: the SDPA call
+    with the reference's combined attn_mask, attention.py:268-299).  Every
+    row sees at least one key (key 0 kept; in the reference mode a padded
+    key is visible to every row)."""
+    from hydra_amd.attention.backends.ccgqa.ops import (MASK_KEY_PADDING, MASK_REFERENCE_SDPA,
+                                                        attention_backward, attention_forward)
+
+    B, Hq, Hkv, S, hd, dtype = case
+    q, k, v, go = _inputs(B, Hq, Hkv, S, hd, dtype, seed=S + hd)
+    g = torch.Generator().manual_seed(S)
+    mask = (torch.rand(B, S, generator=g) > 0.3).long()
+    mask[:, 0] = 1
+    mask[:, S // 2] = 0
+    mm = MASK_KEY_PADDING if mode == "key_padding" else MASK_REFERENCE_SDPA
+    dev = lambda t: t.to(cuda)
+    out, lse = attention_forward(dev(q), dev(k), dev(v), causal=True, key_mask=dev(mask), mask_mode=mm,
+                                 want_lse=True)
+    got = attention_backward(dev(q), dev(k), dev(v), out, lse, dev(go), causal=True, key_mask=dev(mask),
+                             mask_mode=mm)
+    q64, k64, v64 = (t.detach().double().requires_grad_(True) for t in (q, k, v))
+    if mode == "key_padding":
+        ref_out = occ.attention_key_padding(q64, k64, v64, causal=True, mask=mask)
+    else:
+        ref_out = occ.attention(q64, k64, v64, causal=True, mask=mask)
+    assert max_rel_err(out.cpu(), ref_out.detach()) < TOL[dtype]
+    ref_out.backward(go.double())
+    for name, a, r in zip(("dq", "dk", "dv"), got, (q64.grad, k64.grad, v64.grad)):
+        err = max_rel_err(a.cpu(), r)
+        assert err < (1e-4 if dtype == torch.float32 else 5e-2), f"{name}: {err:.3g}"

@@ -149,16 +149,46 @@ def test_module_train_step_reduces_loss(cuda):
     assert losses[-1] < losses[0]
 
 
-def test_module_backward_with_mask_raises(cuda):
-    """A padding mask has no backward in this build: recording a graph
-    through it raises at backward instead of dropping gradients."""
+@pytest.mark.parametrize("semantics", ["reference", "key_padding"])
+def test_module_backward_with_mask(cuda, monkeypatch, semantics):
+    """CCGQAAttention with a padding mask trains: forward + backward against
+    fp64 autograd through oracle.ccgqa.forward with the same mask, in the
+    reference's literal semantics (attention.py:268-299) and the key-padding
+    reading."""
     from hydra_amd.attention import CCGQAAttention
 
-    m = CCGQAAttention(dim=256, n_heads=4, n_kv_heads=2, compression_factor=4, max_seq_len=64).to(cuda)
-    x = torch.randn(1, 16, 256, device=cuda, requires_grad=True)
-    out = m(x, mask=torch.ones(1, 16, dtype=torch.long, device=cuda))
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+    monkeypatch.setenv("HYDRA_CCGQA_MASK_SEMANTICS", semantics)
+    case = dict(dim=256, n_heads=4, n_kv_heads=2, compression_factor=4, B=2, S=48)
+    cfg, B, S, g, params = _setup(case, torch.float32, seed=44)
+    x = torch.randn(B, S, cfg.dim, generator=g)
+    gout = torch.randn(B, S, cfg.dim, generator=g)
+    mask = (torch.rand(B, S, generator=g) > 0.3).long()
+    mask[:, 0] = 1
+    mask[:, S // 2] = 0
+    p64 = {k: _leaf64(v) for k, v in params.items()}
+    x64 = _leaf64(x)
+    if semantics == "reference":
+        out = occ.forward(p64, x64, cfg, mask=mask)
+    else:
+        qkv = torch.nn.functional.linear(x64, p64["qkv_proj.weight"])
+        q, k, v = occ.prep(p64, qkv, cfg)
+        o = occ.attention_key_padding(q, k, v, causal=True, mask=mask)
+        o = o.transpose(1, 2).reshape(B, S, cfg.latent_dim)
+        out = torch.nn.functional.linear(o, p64["o_proj.weight"])
+    (out * gout.double()).sum().backward()
+
+    m = CCGQAAttention(dim=cfg.dim, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+                       compression_factor=cfg.compression_factor, max_seq_len=cfg.max_seq_len)
+    m.load_state_dict(params)
+    m = m.to(cuda).train()
+    xd = x.to(cuda).requires_grad_(True)
+    od = m(xd, mask=mask.to(cuda))
+    assert max_rel_err(od.detach().cpu(), out) < 1e-5
+    od.backward(gout.to(cuda))
+    assert max_rel_err(xd.grad.cpu(), x64.grad) < 1e-4
+    for n, prm in m.named_parameters():
+        assert prm.grad is not None, n
+        assert max_rel_err(prm.grad.cpu(), p64[n].grad) < 1e-4, n
 
 
 def test_module_eval_under_grad_uses_inference_kernels(cuda):

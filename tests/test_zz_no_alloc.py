@@ -20,8 +20,14 @@ def _bwd(name, x, w, gy):
     rows, dim = x.shape
     gx = torch.empty_like(x)
     gw = torch.empty_like(w)
-    _lib.call(name, x.data_ptr(), w.data_ptr(), gy.data_ptr(), gx.data_ptr(), gw.data_ptr(), rows, dim,
-              dim, dim, dim, 1e-6, _lib.dtype_code(x), _lib.dtype_code(w), _lib.stream(x))
+    args = (x.data_ptr(), w.data_ptr(), gy.data_ptr(), gx.data_ptr(), gw.data_ptr(), rows, dim,
+            dim, dim, dim, 1e-6, _lib.dtype_code(x), _lib.dtype_code(w))
+    if name == "hydra_rms_norm_bwd":  # the allocating form takes torch-provided scratch
+        need = _lib.query("hydra_rms_norm_bwd_workspace", rows, dim)
+        ws = _lib.scratch(need, x)
+        _lib.call(name, *args, ws.data_ptr(), need, _lib.stream(x))
+    else:
+        _lib.call(name, *args, _lib.stream(x))
     return gx, gw
 
 
