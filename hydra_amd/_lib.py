@@ -49,7 +49,7 @@ SIGNATURES = {
     "hydra_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "hydra_qk_norm_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _P],
     "hydra_ccgqa_prep_fwd": [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P,
-                             _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
+                             _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_attn_fwd": [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64,
                        _I64P, _I64P, _I64P, _I64P, _I, _F, _F, _P, _I, _I, _P, _I64, _P],
     "hydra_attn_fwd_workspace": [_I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _I64P, _I, _I, _I,
@@ -65,8 +65,8 @@ SIGNATURES = {
     "hydra_ccgqa_prep_faults": [_P],
     "hydra_ccgqa_prep_bwd": [_P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P,
                              _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
-    "hydra_causal_im2col": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P],
-    "hydra_causal_col2im": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
+    "hydra_causal_im2col": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I, _P],
+    "hydra_causal_col2im": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _P],
     "hydra_embedding_fwd": [_P, _I64, _P, _I64, _I64, _I64, _F, _P, _I64, _I, _P],
     "hydra_residual_norm_fwd": [_P, _I64, _P, _I64, _F, _P, _P, _P, _F, _I, _P, _I64, _P, _I64,
                                 _I64, _I64, _I, _I, _P],

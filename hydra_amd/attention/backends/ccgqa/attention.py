@@ -145,8 +145,6 @@ class CCGQAAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         B, S, _ = x.shape
-        if self.use_convs and self.conv_kernel_size != 3:
-            raise NotImplementedError("CCGQAAttention: the HIP prep kernel implements conv_kernel_size=3")
         if self.use_rope and S > self.cos_cached.shape[2]:
             raise ValueError(f"CCGQAAttention: sequence length {S} exceeds the RoPE cache "
                              f"({self.cos_cached.shape[2]})")
@@ -181,7 +179,8 @@ class CCGQAAttention(nn.Module):
         B, S, _ = x.shape
         if x.dtype == torch.bfloat16 and S % 8 == 0 and self.head_dim in (16, 32, 64, 128):
             flags |= CCGQA_V_TRANSPOSED  # V^T feeds the MFMA attention without a transpose
-        tiled = self.use_convs and tiled_weights_ok(self.n_heads, self.n_kv_heads, self.head_dim, x.dtype)
+        tiled = (self.use_convs and self.conv_kernel_size == 3 and
+                 tiled_weights_ok(self.n_heads, self.n_kv_heads, self.head_dim, x.dtype))
         if tiled:
             flags |= CCGQA_W_TILED  # conv weights in MFMA-fragment order
         with torch.no_grad():
@@ -190,7 +189,8 @@ class CCGQAAttention(nn.Module):
                 qkv.detach(), self.n_heads, self.n_kv_heads, self.head_dim, flags, *packed,
                 temperature=self.key_temperature if self.use_qk_norm else None,
                 cos=self.cos_cached if self.use_rope else None,
-                sin=self.sin_cached if self.use_rope else None, packed=True)
+                sin=self.sin_cached if self.use_rope else None, packed=True,
+                conv_ks=self.conv_kernel_size)
             out = torch.empty((B, S, self.latent_dim), dtype=x.dtype, device=x.device)
             o_view = out.view(B, S, self.n_heads, self.head_dim).transpose(1, 2)
             attention_forward(q, k, v, causal=True, scale=self.scale,

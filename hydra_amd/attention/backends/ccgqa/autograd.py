@@ -15,7 +15,8 @@ backward: 1. the conv outputs y2 recomputed by the same kernel with the
              dy1 = col2im(dY2 W2r); conv1 (grouped, batched over groups) --
              dW1 = dY1^T im2col(q0), grad(q0) += col2im(dY1 W1r); y1 itself
              is recomputed as im2col(q0) W1r^T, rounded to the working dtype
-             as the forward kernel rounds it.
+             as the forward kernel rounds it.  Any conv kernel size (the
+             taps of the im2col columns follow the weights).
 """
 from __future__ import annotations
 
@@ -34,23 +35,24 @@ def _conv_pair_backward(x0: torch.Tensor, dy2: torch.Tensor, w1: torch.Tensor, w
     (dW1, dW2) in the weights' layouts [C, C/groups, 3] and [C, C, 3]."""
     B, S, C = x0.shape
     N, cg = B * S, C // groups
+    ks = w1.shape[-1]  # conv taps
     dt = x0.dtype
     w1d, w2d = w1.detach().to(dt), w2.detach().to(dt)
     # Wr[g][o][t*cg + c] = W[g*cg + o, c, t]
-    w1r = w1d.view(groups, cg, cg, 3).permute(0, 1, 3, 2).reshape(groups, cg, 3 * cg).contiguous()
-    w2r = w2d.permute(0, 2, 1).reshape(C, 3 * C).contiguous()
-    x0s = causal_im2col(x0, groups)                                # [G, N, 3cg]
+    w1r = w1d.view(groups, cg, cg, ks).permute(0, 1, 3, 2).reshape(groups, cg, ks * cg).contiguous()
+    w2r = w2d.permute(0, 2, 1).reshape(C, ks * C).contiguous()
+    x0s = causal_im2col(x0, groups, ks)                            # [G, N, ks*cg]
     y1 = torch.bmm(x0s, w1r.transpose(1, 2).contiguous())         # [G, N, cg]
     y1 = y1.permute(1, 0, 2).reshape(B, S, C)
-    y1s = causal_im2col(y1, 1)[0]                                  # [N, 3C]
+    y1s = causal_im2col(y1, 1, ks)[0]                              # [N, ks*C]
     dy2f = dy2.reshape(N, C)
-    dw2 = (dy2f.t().contiguous() @ y1s).view(C, 3, C).permute(0, 2, 1)
+    dw2 = (dy2f.t().contiguous() @ y1s).view(C, ks, C).permute(0, 2, 1)
     dy1 = torch.empty((B, S, C), dtype=dt, device=x0.device)
-    causal_col2im((dy2f @ w2r).view(1, N, 3 * C), dy1)
+    causal_col2im((dy2f @ w2r).view(1, N, ks * C), dy1, taps=ks)
     dy1g = dy1.view(N, groups, cg).permute(1, 0, 2).contiguous()  # [G, N, cg]
-    dw1 = torch.bmm(dy1g.transpose(1, 2).contiguous(), x0s)       # [G, cg, 3cg]
-    dw1 = dw1.view(groups, cg, 3, cg).permute(0, 1, 3, 2).reshape(C, cg, 3)
-    causal_col2im(torch.bmm(dy1g, w1r), dx0, accumulate=True)
+    dw1 = torch.bmm(dy1g.transpose(1, 2).contiguous(), x0s)       # [G, cg, ks*cg]
+    dw1 = dw1.view(groups, cg, ks, cg).permute(0, 1, 3, 2).reshape(C, cg, ks)
+    causal_col2im(torch.bmm(dy1g, w1r), dx0, accumulate=True, taps=ks)
     return dw1.to(w1.dtype), dw2.to(w2.dtype)
 
 
@@ -63,10 +65,11 @@ class CCGQAPrepFunction(torch.autograd.Function):
     def forward(ctx, qkv, wq1, wq2, wk1, wk2, temperature, cos, sin, n_heads, n_kv_heads,
                 head_dim, flags):
         convs = bool(flags & CCGQA_CONVS)
-        tiled = convs and tiled_weights_ok(n_heads, n_kv_heads, head_dim, qkv.dtype)
+        ks = wq1.shape[-1] if convs else 3
+        tiled = convs and ks == 3 and tiled_weights_ok(n_heads, n_kv_heads, head_dim, qkv.dtype)
         fl = flags | (CCGQA_W_TILED if tiled else 0)
         q, k, v = ccgqa_prep(qkv, n_heads, n_kv_heads, head_dim, fl, wq1, wq2, wk1, wk2,
-                             temperature=temperature, cos=cos, sin=sin)
+                             temperature=temperature, cos=cos, sin=sin, conv_ks=ks)
         ctx.save_for_backward(qkv, wq1, wq2, wk1, wk2, temperature)
         ctx.rope = (cos, sin)
         ctx.meta = (n_heads, n_kv_heads, head_dim, flags, tiled)
@@ -87,7 +90,7 @@ class CCGQAPrepFunction(torch.autograd.Function):
         y2q = y2k = None
         if convs:
             fl = CCGQA_CONVS | (CCGQA_W_TILED if tiled else 0)
-            y2q, y2k, _ = ccgqa_prep(qkv, Hq, Hkv, hd, fl, wq1, wq2, wk1, wk2)
+            y2q, y2k, _ = ccgqa_prep(qkv, Hq, Hkv, hd, fl, wq1, wq2, wk1, wk2, conv_ks=wq1.shape[-1])
         dy, dqkv, dtemp_tok = ccgqa_prep_backward(qkv, Hq, Hkv, hd, flags, gq, gk, gv, y2q, y2k,
                                                   temperature=temp, cos=cos, sin=sin)
         dw = [None] * 4

@@ -46,7 +46,7 @@ def tiled_weights_ok(n_heads: int, n_kv_heads: int, head_dim: int, dtype: torch.
 
 def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, flags: int,
                wq1=None, wq2=None, wk1=None, wk2=None, temperature=None, cos=None, sin=None,
-               packed: bool = False):
+               packed: bool = False, conv_ks: int = 3):
     """q [B,Hq,S,hd], k/v [B,Hkv,S,hd] from the fused projection qkv [B,S,L+2K]
     (CCGQAAttention.forward, attention.py:205-266).  Conv weights are in
     PyTorch Conv1d layout, or already packed (pack_conv_weight, tiled when
@@ -68,9 +68,10 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
             ws = tuple(w.to(dt).contiguous() for w in ws)
         else:
             ws = tuple(pack_conv_weight(w, dt, tiled) for w in ws)
-        exp = [(3, L, head_dim), (3, L, L), (3, K, head_dim), (3, K, K)]
+        ks = conv_ks
+        exp = [(ks, L, head_dim), (ks, L, L), (ks, K, head_dim), (ks, K, K)]
         if tiled:
-            exp = [(3, o // 32, i // 16, 2, 32, 8) for _, o, i in exp]
+            exp = [(ks, o // 32, i // 16, 2, 32, 8) for _, o, i in exp]
         for w, e in zip(ws, exp):
             if tuple(w.shape) != e:
                 raise ValueError(f"ccgqa_prep: packed conv weight shape {tuple(w.shape)} != {e}")
@@ -95,7 +96,7 @@ def ccgqa_prep(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int, 
                   _lib.ptr(wq2), _lib.ptr(wk1), _lib.ptr(wk2), _lib.ptr(temp), _lib.ptr(cos),
                   _lib.ptr(sin), head_dim // 2 if cos is None else cos.stride(0),
                   q.data_ptr(), k.data_ptr(), v.data_ptr(), B, S, n_heads, n_kv_heads,
-                  head_dim, flags, _lib.dtype_code(qkv), _lib.stream(qkv))
+                  head_dim, conv_ks, flags, _lib.dtype_code(qkv), _lib.stream(qkv))
     return q, k, (v.transpose(2, 3) if vt else v)
 
 
@@ -265,15 +266,14 @@ def conv_sequence(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, groups1: 
     buffer whose k block is zero, with every other prep feature off."""
     if groups2 != 1:
         raise NotImplementedError("conv_sequence: the HIP conv stage implements a dense conv2 (groups2 == 1)")
-    if w1.shape[-1] != 3:
-        raise NotImplementedError("conv_sequence: the HIP conv stage implements kernel_size 3")
     _lib.require_gpu("conv_sequence", x, w1, w2)
     B, N, C = x.shape
     hd = C // groups1
+    ks = w1.shape[-1]
     qkv = torch.zeros((B, N, C + 2 * hd), dtype=x.dtype, device=x.device)
     qkv[..., :C] = x
-    zk = torch.zeros((hd, hd, 3), dtype=x.dtype, device=x.device)
-    q, _, _ = ccgqa_prep(qkv, groups1, 1, hd, CCGQA_CONVS, w1, w2, zk, zk)
+    zk = torch.zeros((hd, hd, ks), dtype=x.dtype, device=x.device)
+    q, _, _ = ccgqa_prep(qkv, groups1, 1, hd, CCGQA_CONVS, w1, w2, zk, zk, conv_ks=ks)
     return q.transpose(1, 2).reshape(B, N, C)
 
 
@@ -281,11 +281,11 @@ __all__ = ["prep_flags", "pack_conv_weight", "ccgqa_prep", "attention_forward", 
            "qk_norm_score_bound", "MASK_NONE", "MASK_KEY_PADDING", "MASK_REFERENCE_SDPA"]
 
 
-def causal_im2col(x: torch.Tensor, groups: int) -> torch.Tensor:
-    """[B,S,G*cg] (unit channel stride, any row stride) -> [G, B*S, 3*cg]:
-    row b*S+s of group g holds x[b, s+t-2, g*cg:(g+1)*cg] for taps t = 0..2
-    (zero before the row start), the operand of the k=3 causal conv as a
-    GEMM (hydra_causal_im2col)."""
+def causal_im2col(x: torch.Tensor, groups: int, taps: int = 3) -> torch.Tensor:
+    """[B,S,G*cg] (unit channel stride, any row stride) -> [G, B*S, taps*cg]:
+    row b*S+s of group g holds x[b, s+t-(taps-1), g*cg:(g+1)*cg] for taps
+    t = 0..taps-1 (zero before the row start), the operand of the causal
+    conv as a GEMM (hydra_causal_im2col)."""
     _lib.require_gpu("causal_im2col", x)
     B, S, C = x.shape
     if C % groups != 0:
@@ -293,28 +293,29 @@ def causal_im2col(x: torch.Tensor, groups: int) -> torch.Tensor:
     if x.stride(-1) != 1 or (B > 1 and x.stride(0) != S * x.stride(1)):
         x = x.contiguous()
     cg = C // groups
-    out = torch.empty((groups, B * S, 3 * cg), dtype=x.dtype, device=x.device)
+    out = torch.empty((groups, B * S, taps * cg), dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
         _lib.call("hydra_causal_im2col", x.data_ptr(), x.stride(1), out.data_ptr(), B, S, groups, cg,
-                  _lib.dtype_code(x), _lib.stream(x))
+                  taps, _lib.dtype_code(x), _lib.stream(x))
     return out
 
 
-def causal_col2im(cols: torch.Tensor, out: torch.Tensor, accumulate: bool = False) -> torch.Tensor:
-    """The transpose of causal_im2col: cols [G, B*S, 3*cg] summed over taps
-    into out [B,S,G*cg] (unit channel stride; added to its contents with
-    `accumulate`).  Returns out."""
+def causal_col2im(cols: torch.Tensor, out: torch.Tensor, accumulate: bool = False,
+                  taps: int = 3) -> torch.Tensor:
+    """The transpose of causal_im2col: cols [G, B*S, taps*cg] summed over
+    taps into out [B,S,G*cg] (unit channel stride; added to its contents
+    with `accumulate`).  Returns out."""
     _lib.require_gpu("causal_col2im", cols, out)
     B, S, C = out.shape
     G = cols.shape[0]
-    if C % G != 0 or cols.shape != (G, B * S, 3 * (C // G)) or cols.dtype != out.dtype:
+    if C % G != 0 or cols.shape != (G, B * S, taps * (C // G)) or cols.dtype != out.dtype:
         raise ValueError(f"causal_col2im: cols {tuple(cols.shape)} do not match out {tuple(out.shape)}")
     if out.stride(-1) != 1 or (B > 1 and out.stride(0) != S * out.stride(1)):
         raise ValueError("causal_col2im: out needs unit channel stride and uniform row stride")
     cols = cols.contiguous()
     with torch.cuda.device(out.device):
         _lib.call("hydra_causal_col2im", cols.data_ptr(), out.data_ptr(), out.stride(1), B, S, G,
-                  C // G, 1 if accumulate else 0, _lib.dtype_code(out), _lib.stream(out))
+                  C // G, taps, 1 if accumulate else 0, _lib.dtype_code(out), _lib.stream(out))
     return out
 
 

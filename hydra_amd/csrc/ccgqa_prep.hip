@@ -61,13 +61,14 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
     const T* __restrict__ wq2, const T* __restrict__ wk1, const T* __restrict__ wk2,
     const T* __restrict__ temp, const float* __restrict__ cs, const float* __restrict__ sn,
     int64_t cs_rs, T* __restrict__ qo, T* __restrict__ ko, T* __restrict__ vo, int S,
-    int Hq, int Hkv, int hd, int TT, int flags) {
+    int Hq, int Hkv, int hd, int TT, int ks, int flags) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   T* sm = reinterpret_cast<T*>(smem_raw);
   const int L = Hq * hd, K = Hkv * hd, CW = L + K;
-  T* xs = sm;                        // rows: tokens s0-4 .. s0+TT-1
-  T* y1 = xs + (TT + 4) * CW;        // rows: tokens s0-2 .. s0+TT-1
-  T* y2 = y1 + (TT + 2) * CW;        // rows: tokens s0   .. s0+TT-1
+  const int hw = ks - 1;               // each causal conv reaches ks-1 tokens back
+  T* xs = sm;                          // rows: tokens s0-2hw .. s0+TT-1
+  T* y1 = xs + (TT + 2 * hw) * CW;     // rows: tokens s0-hw .. s0+TT-1
+  T* y2 = y1 + (TT + hw) * CW;         // rows: tokens s0   .. s0+TT-1
   const int tid = threadIdx.x;
   const int b = blockIdx.y;
   const int s0 = blockIdx.x * TT;
@@ -78,25 +79,25 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
   const bool rope = flags & HYDRA_CCGQA_ROPE;
   const T* xb = qkv + static_cast<int64_t>(b) * S * qkv_rs;
 
-  for (int i = tid; i < (TT + 4) * CW; i += 256) {
+  for (int i = tid; i < (TT + 2 * hw) * CW; i += 256) {
     const int r = i / CW, c = i - r * CW;
-    const int s = s0 - 4 + r;
+    const int s = s0 - 2 * hw + r;
     xs[i] = (s >= 0 && s < S) ? xb[static_cast<int64_t>(s) * qkv_rs + c] : from_f32<T>(0.f);
   }
   __syncthreads();
 
   if (convs) {
     // conv1 (grouped): output channel o of group g reads channels g*hd..g*hd+hd-1.
-    for (int i = tid; i < (TT + 2) * CW; i += 256) {
+    for (int i = tid; i < (TT + hw) * CW; i += 256) {
       const int r = i / CW, o = i - r * CW;
-      const int s = s0 - 2 + r;
+      const int s = s0 - hw + r;
       float acc = 0.f;
       if (s >= 0 && s < S) {
         const bool is_q = o < L;
         const int oo = is_q ? o : o - L;
         const int col0 = (is_q ? 0 : L) + (oo / hd) * hd;
         const int O = is_q ? L : K;
-        for (int t = 0; t < 3; ++t) {
+        for (int t = 0; t < ks; ++t) {
           const T* w = (is_q ? wq1 : wk1) + (static_cast<int64_t>(t) * O + oo) * hd;
           const T* xr = xs + (r + t) * CW + col0;
           for (int c = 0; c < hd; ++c) acc = fmaf(to_f32(w[c]), to_f32(xr[c]), acc);
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
       const int C = is_q ? L : K;
       const int col0 = is_q ? 0 : L;
       float acc = 0.f;
-      for (int t = 0; t < 3; ++t) {
+      for (int t = 0; t < ks; ++t) {
         const T* w = (is_q ? wq2 : wk2) + (static_cast<int64_t>(t) * C + oo) * C;
         const T* yr = y1 + (r + t) * CW + col0;
         for (int c = 0; c < C; ++c) acc = fmaf(to_f32(w[c]), to_f32(yr[c]), acc);
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
       y2[i] = from_f32<T>(acc);
     }
   } else {
-    for (int i = tid; i < TT * CW; i += 256) y2[i] = xs[4 * CW + i];
+    for (int i = tid; i < TT * CW; i += 256) y2[i] = xs[2 * hw * CW + i];
   }
   __syncthreads();
 
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(256) void ccgqa_prep_generic_kernel(
     const int head = is_k ? hh - Hq : hh;
     const int col0 = (is_k ? L : 0) + head * hd;
     T* row = y2 + r * CW + col0;
-    const T* x0 = xs + (r + 4) * CW;  // pre-conv q0 | k0 of this token
+    const T* x0 = xs + (r + 2 * hw) * CW;  // pre-conv q0 | k0 of this token
     if (qk_mean) {
       for (int d = 0; d < hd; ++d) {
         float add;
@@ -1230,12 +1231,14 @@ static int launch_prep_generic(const void* qkv, int64_t qkv_rs, const void* wq1,
                                const void* wq2, const void* wk1, const void* wk2,
                                const void* temp, const float* cs, const float* sn,
                                int64_t cs_rs, void* qo, void* ko, void* vo, int64_t B,
-                               int64_t S, int64_t Hq, int64_t Hkv, int64_t hd, int flags,
-                               hipStream_t st) {
+                               int64_t S, int64_t Hq, int64_t Hkv, int64_t hd, int64_t ks,
+                               int flags, hipStream_t st) {
   const int64_t CW = (Hq + Hkv) * hd;
+  const int64_t hw = ks - 1;  // token rows each causal conv reaches back
+  auto lds_of = [&](int tt) { return static_cast<size_t>(3 * tt + 3 * hw) * CW * sizeof(T); };
   int TT = 32;
-  while (TT > 1 && static_cast<int64_t>(3 * TT + 6) * CW * sizeof(T) > 64 * 1024) TT >>= 1;
-  const size_t lds = static_cast<size_t>(3 * TT + 6) * CW * sizeof(T);
+  while (TT > 1 && lds_of(TT) > 64 * 1024) TT >>= 1;
+  const size_t lds = lds_of(TT);
   if (lds > 64 * 1024)
     return fail(HYDRA_ERR_UNSUPPORTED, "ccgqa_prep: latent too wide for the LDS tile");
   const dim3 grid(static_cast<unsigned>((S + TT - 1) / TT), static_cast<unsigned>(B));
@@ -1243,7 +1246,7 @@ static int launch_prep_generic(const void* qkv, int64_t qkv_rs, const void* wq1,
       static_cast<const T*>(qkv), qkv_rs, static_cast<const T*>(wq1),
       static_cast<const T*>(wq2), static_cast<const T*>(wk1), static_cast<const T*>(wk2),
       static_cast<const T*>(temp), cs, sn, cs_rs, static_cast<T*>(qo), static_cast<T*>(ko),
-      static_cast<T*>(vo), (int)S, (int)Hq, (int)Hkv, (int)hd, TT, flags);
+      static_cast<T*>(vo), (int)S, (int)Hq, (int)Hkv, (int)hd, TT, (int)ks, flags);
   return check_launch("ccgqa_prep_generic_kernel");
 }
 
@@ -1274,8 +1277,10 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
                                     const void* temp, const float* cos, const float* sin,
                                     int64_t cs_rs, void* q_out, void* k_out, void* v_out,
                                     int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
-                                    int64_t hd, int flags, int dtype, void* stream) {
+                                    int64_t hd, int64_t conv_ks, int flags, int dtype,
+                                    void* stream) {
   HYDRA_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && hd >= 2, "ccgqa_prep: bad size");
+  HYDRA_REQUIRE(conv_ks >= 1 && conv_ks <= 16, "ccgqa_prep: conv kernel size must be in [1, 16]");
   HYDRA_REQUIRE(Hq % Hkv == 0, "ccgqa_prep: n_heads must be a multiple of n_kv_heads");
   HYDRA_REQUIRE(hd % 2 == 0, "ccgqa_prep: head_dim must be even");
   HYDRA_REQUIRE((flags & ~127) == 0, "ccgqa_prep: unknown flag bits");
@@ -1294,8 +1299,11 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
   HYDRA_REQUIRE(S * (L + 2 * K) < (int64_t(1) << 40), "ccgqa_prep: too large");
   auto st = static_cast<hipStream_t>(stream);
   const bool rope = flags & HYDRA_CCGQA_ROPE;
+  // the MFMA and vector kernels are written for the reference's default
+  // k = 3 (or no convs); other sizes take the generic kernel
+  const bool k3 = conv_ks == 3 || !(flags & HYDRA_CCGQA_CONVS);
   const bool mfma_ok =
-      dtype == HYDRA_BF16 && (hd == 16 || hd == 32 || hd == 64 || hd == 128) && K % 32 == 0 &&
+      k3 && dtype == HYDRA_BF16 && (hd == 16 || hd == 32 || hd == 64 || hd == 128) && K % 32 == 0 &&
       L % 32 == 0 &&
       qkv_rs % 8 == 0 && aligned16(qkv) && aligned16(q_out) && aligned16(k_out) &&
       aligned16(v_out) &&
@@ -1327,7 +1335,7 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
     max_lds = 65536;
   // 4-element weight and LDS steps: every channel count a multiple of 4.
   const int esz = dtype_size(dtype);
-  const bool vec_ok = hd % 4 == 0 && aligned16(qkv) &&
+  const bool vec_ok = k3 && hd % 4 == 0 && aligned16(qkv) &&
                       (!(flags & HYDRA_CCGQA_CONVS) ||
                        ((reinterpret_cast<uintptr_t>(wq1) | reinterpret_cast<uintptr_t>(wq2) |
                          reinterpret_cast<uintptr_t>(wk1) | reinterpret_cast<uintptr_t>(wk2)) %
@@ -1341,6 +1349,6 @@ extern "C" int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs, const void*
       if (rc >= 0) return rc;
     }
     return launch_prep_generic<T>(qkv, qkv_rs, wq1, wq2, wk1, wk2, temp, cos, sin, cs_rs,
-                                  q_out, k_out, v_out, B, S, Hq, Hkv, hd, flags, st);
+                                  q_out, k_out, v_out, B, S, Hq, Hkv, hd, conv_ks, flags, st);
   });
 }

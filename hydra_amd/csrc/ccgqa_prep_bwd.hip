@@ -12,7 +12,7 @@
 //     pre-conv q0/k0 from qkv, and writes the gradient of the conv outputs,
 //     the QK-mean and v parts of grad(qkv) and a per-token partial of
 //     grad(temperature).
-//   * hydra_causal_im2col / hydra_causal_col2im: the k=3 causal conv as a
+//   * hydra_causal_im2col / hydra_causal_col2im: the k-tap causal conv as a
 //     GEMM over [tap, channel] columns (per group), so the conv backward is
 //     plain library GEMMs: dX = col2im(dY W), dW = dY^T im2col(X).
 //   * the GEMMs themselves (hipBLASLt through the caller).
@@ -222,26 +222,26 @@ __global__ __launch_bounds__(kPbThreads) void ccgqa_prep_bwd_kernel(
 template <typename T>
 __global__ __launch_bounds__(256) void causal_im2col_kernel(const T* __restrict__ x, int64_t x_rs,
                                                            T* __restrict__ out, int64_t N, int S,
-                                                           int G, int cg, int64_t total) {
+                                                           int G, int cg, int taps, int64_t total) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
-  const int w = 3 * cg;
+  const int w = taps * cg;
   const int64_t gn = i / w;
   const int col = static_cast<int>(i - gn * w);
   const int g = static_cast<int>(gn / N);
   const int64_t n = gn - static_cast<int64_t>(g) * N;
   const int t = col / cg, c = col - t * cg;
   const int s = static_cast<int>(n % S);
-  const int src = s + t - 2;
-  out[i] = src >= 0 ? x[(n + t - 2) * x_rs + g * cg + c] : from_f32<T>(0.f);
+  const int back = taps - 1 - t;  // tap t reads the token taps-1-t back
+  out[i] = s >= back ? x[(n - back) * x_rs + g * cg + c] : from_f32<T>(0.f);
 }
 
-// out[b, s, g*cg + c] (+)= sum_t in[g][b*S + s - t + 2][t*cg + c] over the
-// taps whose output token s - t + 2 lies in the row.
+// out[b, s, g*cg + c] (+)= sum_t in[g][b*S + s + taps-1-t][t*cg + c] over
+// the taps whose output token s + taps-1-t lies in the row.
 template <typename T>
 __global__ __launch_bounds__(256) void causal_col2im_kernel(const T* __restrict__ in,
                                                            T* __restrict__ out, int64_t out_rs,
-                                                           int64_t N, int S, int G, int cg,
+                                                           int64_t N, int S, int G, int cg, int taps,
                                                            int accumulate, int64_t total) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
@@ -250,13 +250,12 @@ __global__ __launch_bounds__(256) void causal_col2im_kernel(const T* __restrict_
   const int ch = static_cast<int>(i - n * C);
   const int g = ch / cg, c = ch - g * cg;
   const int s = static_cast<int>(n % S);
-  const int w = 3 * cg;
+  const int w = taps * cg;
   const T* base = in + static_cast<int64_t>(g) * N * w;
   float acc = 0.f;
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    const int so = s - t + 2;  // output token that read this input at tap t
-    if (so < S) acc += to_f32(base[(n - t + 2) * w + t * cg + c]);
+  for (int t = 0; t < taps; ++t) {
+    const int fwd = taps - 1 - t;  // output token s + fwd read this input at tap t
+    if (s + fwd < S) acc += to_f32(base[(n + fwd) * w + t * cg + c]);
   }
   T* o = out + n * out_rs + ch;
   if (accumulate) acc += to_f32(*o);
@@ -309,24 +308,28 @@ extern "C" int hydra_ccgqa_prep_bwd(const void* qkv, int64_t qkv_rs, const void*
 }
 
 extern "C" int hydra_causal_im2col(const void* x, int64_t x_rs, void* out, int64_t B, int64_t S,
-                                   int64_t G, int64_t cg, int dtype, void* stream) {
+                                   int64_t G, int64_t cg, int64_t taps, int dtype, void* stream) {
   HYDRA_REQUIRE(B >= 0 && S >= 0 && G >= 1 && cg >= 1, "causal_im2col: bad size");
+  HYDRA_REQUIRE(taps >= 1 && taps <= 16, "causal_im2col: taps must be in [1, 16]");
   HYDRA_REQUIRE(x_rs >= G * cg, "causal_im2col: row stride smaller than G * cg");
-  const int64_t total = G * B * S * 3 * cg;
+  const int64_t total = G * B * S * taps * cg;
   if (total == 0) return HYDRA_OK;
   HYDRA_REQUIRE(x && out, "causal_im2col: null pointer");
   HYDRA_REQUIRE(S < (int64_t(1) << 31) && G * cg < (int64_t(1) << 31), "causal_im2col: too large");
   auto st = static_cast<hipStream_t>(stream);
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     causal_im2col_kernel<T><<<static_cast<unsigned>((total + 255) / 256), 256, 0, st>>>(
-        static_cast<const T*>(x), x_rs, static_cast<T*>(out), B * S, (int)S, (int)G, (int)cg, total);
+        static_cast<const T*>(x), x_rs, static_cast<T*>(out), B * S, (int)S, (int)G, (int)cg, (int)taps,
+        total);
     return check_launch("causal_im2col_kernel");
   });
 }
 
 extern "C" int hydra_causal_col2im(const void* in, void* out, int64_t out_rs, int64_t B, int64_t S,
-                                   int64_t G, int64_t cg, int accumulate, int dtype, void* stream) {
+                                   int64_t G, int64_t cg, int64_t taps, int accumulate, int dtype,
+                                   void* stream) {
   HYDRA_REQUIRE(B >= 0 && S >= 0 && G >= 1 && cg >= 1, "causal_col2im: bad size");
+  HYDRA_REQUIRE(taps >= 1 && taps <= 16, "causal_col2im: taps must be in [1, 16]");
   HYDRA_REQUIRE(out_rs >= G * cg, "causal_col2im: row stride smaller than G * cg");
   const int64_t total = B * S * G * cg;
   if (total == 0) return HYDRA_OK;
@@ -336,7 +339,7 @@ extern "C" int hydra_causal_col2im(const void* in, void* out, int64_t out_rs, in
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
     causal_col2im_kernel<T><<<static_cast<unsigned>((total + 255) / 256), 256, 0, st>>>(
         static_cast<const T*>(in), static_cast<T*>(out), out_rs, B * S, (int)S, (int)G, (int)cg,
-        accumulate, total);
+        (int)taps, accumulate, total);
     return check_launch("causal_col2im_kernel");
   });
 }

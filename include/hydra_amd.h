@@ -168,17 +168,19 @@ int hydra_qk_norm_bwd(const void* q, const void* k, const void* grad_qo, const v
 
 /* Everything of CCGQAAttention.forward between the qkv GEMM and the attention
  * core, in one pass over token tiles: split of the fused projection, value
- * shift, causal grouped conv1 + dense conv2 (k=3, each left-padded by 2) on q
- * and k, QK-mean coupling from the pre-conv q/k, L2-norm of q and of k times
- * the key temperature, and RoPE.  Replaces attention.py:205-266 with
- * OptimizedConvSequence.forward (kernels/fused_conv.py:39-62).
+ * shift, causal grouped conv1 + dense conv2 (conv_ks taps, each left-padded
+ * by conv_ks - 1; the reference's default is 3) on q and k, QK-mean
+ * coupling from the pre-conv q/k, L2-norm of q and of k times the key
+ * temperature, and RoPE.  Replaces attention.py:205-266 with
+ * OptimizedConvSequence.forward (kernels/fused_conv.py:39-62; the conv
+ * sequences are built with conv_kernel_size at attention.py:132-145).
  *
  * qkv:  [B, S, L + 2K] (row stride qkv_rs), L = Hq*hd, K = Hkv*hd; column
  *       order q | k | v_curr | v_prev (v: | v when no value shift).
  * wq1/wq2/wk1/wk2: the four Conv1d weights (q_conv.conv1/conv2,
- *       k_conv.conv1/conv2) in tap-major layout [3][out][in/groups], i.e.
- *       PyTorch's [out, in/groups, 3] permuted (2, 0, 1):
- *       wq1 [3][L][hd], wq2 [3][L][L], wk1 [3][K][hd], wk2 [3][K][K]
+ *       k_conv.conv1/conv2) in tap-major layout [ks][out][in/groups], i.e.
+ *       PyTorch's [out, in/groups, ks] permuted (2, 0, 1), ks = conv_ks:
+ *       wq1 [ks][L][hd], wq2 [ks][L][L], wk1 [ks][K][hd], wk2 [ks][K][K]
  *       (unused and may be NULL without HYDRA_CCGQA_CONVS).
  *       With HYDRA_CCGQA_W_TILED each tap-major weight [3][O][I] is instead
  *       given as [3][O/32][I/16][2][32][8]: element (t, o/32, i/16, (i/8)%2,
@@ -189,8 +191,9 @@ int hydra_qk_norm_bwd(const void* q, const void* k, const void* grad_qo, const v
  * q_out: [B, Hq, S, hd]; k_out: [B, Hkv, S, hd]; v_out: [B, Hkv, S, hd], or
  * [B, Hkv, hd, S] with HYDRA_CCGQA_V_TRANSPOSED (the layout hydra_attn_fwd
  * stages without a transpose); all contiguous.
- * bf16 with hd in {32, 64, 128} runs both convs on MFMA (up to ~100 KB of LDS
- * per workgroup at L+K = 320); other cases run on the VALU. */
+ * bf16 with hd in {16, 32, 64, 128} and conv_ks = 3 runs both convs on MFMA
+ * (up to ~140 KB of LDS per workgroup at L+K = 320); other cases (any
+ * conv_ks in [1, 16]) run on the VALU. */
 int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
                          const void* wq1, const void* wq2,
                          const void* wk1, const void* wk2,
@@ -198,7 +201,7 @@ int hydra_ccgqa_prep_fwd(const void* qkv, int64_t qkv_rs,
                          int64_t cs_rs,
                          void* q_out, void* k_out, void* v_out,
                          int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
-                         int64_t hd, int flags, int dtype, void* stream);
+                         int64_t hd, int64_t conv_ks, int flags, int dtype, void* stream);
 
 /* 1 when hydra_ccgqa_prep_fwd takes its MFMA path for these heads and
  * dtype on the current device (given 16-byte aligned pointers and, with
@@ -235,20 +238,22 @@ int hydra_ccgqa_prep_bwd(const void* qkv, int64_t qkv_rs, const void* y2q,
                          int64_t Hq, int64_t Hkv, int64_t hd, int flags, int dtype,
                          void* stream);
 
-/* The k = 3 causal conv of OptimizedConvSequence (kernels/fused_conv.py:52-57,
- * left padding 2 per batch row) as a GEMM operand: x [B,S,G*cg] (row stride
- * x_rs) -> out [G][B*S][3*cg] contiguous, out[g][b*S+s][t*cg+c] =
- * x[b, s+t-2, g*cg+c] (0 before the row start).  A conv with weight
- * W[o, c, t] (groups G) is then out[g] @ Wr[g]^T with Wr[g][o][t*cg+c]. */
+/* The `taps`-tap causal conv of OptimizedConvSequence (kernels/fused_conv.py:
+ * 52-57, left padding taps-1 per batch row) as a GEMM operand: x [B,S,G*cg]
+ * (row stride x_rs) -> out [G][B*S][taps*cg] contiguous,
+ * out[g][b*S+s][t*cg+c] = x[b, s+t-(taps-1), g*cg+c] (0 before the row
+ * start).  A conv with weight W[o, c, t] (groups G) is then out[g] @
+ * Wr[g]^T with Wr[g][o][t*cg+c].  taps in [1, 16]. */
 int hydra_causal_im2col(const void* x, int64_t x_rs, void* out, int64_t B, int64_t S,
-                        int64_t G, int64_t cg, int dtype, void* stream);
+                        int64_t G, int64_t cg, int64_t taps, int dtype, void* stream);
 
 /* The transpose of hydra_causal_im2col: out[b,s,g*cg+c] (row stride out_rs)
- * = sum over taps t of in[g][b*S+s-t+2][t*cg+c] for s-t+2 < S, added to
- * out's contents when accumulate != 0 (the conv's input gradient from the
- * GEMM dY @ Wr). */
+ * = sum over taps t of in[g][b*S+s+(taps-1)-t][t*cg+c] for
+ * s+(taps-1)-t < S, added to out's contents when accumulate != 0 (the
+ * conv's input gradient from the GEMM dY @ Wr). */
 int hydra_causal_col2im(const void* in, void* out, int64_t out_rs, int64_t B, int64_t S,
-                        int64_t G, int64_t cg, int accumulate, int dtype, void* stream);
+                        int64_t G, int64_t cg, int64_t taps, int accumulate, int dtype,
+                        void* stream);
 
 /* Key-mask modes of hydra_attn_fwd (key_mask: uint8 [B,S], nonzero = keep).
  * KEY_PADDING: key t is visible to query s iff key_mask[b,t] != 0 (and t <= s

@@ -67,7 +67,7 @@ def test_abi_version_and_error_path():
                   st, st, st, st, 1, ctypes.c_float(0.25), ctypes.c_float(0.0), None, 0, 1, None, 0, None)
     with pytest.raises(ValueError, match="unknown flag"):
         _lib.call("hydra_ccgqa_prep_fwd", None, 48, None, None, None, None, None, None, None, 0,
-                  None, None, None, 1, 4, 2, 1, 16, 128, 1, None)
+                  None, None, None, 1, 4, 2, 1, 16, 3, 128, 1, None)
     # the tiled conv-weight layout is offered for bf16 MFMA head dims only
     # (a layout small enough for the 64 KB LDS assumed without a device)
     assert _lib.query("hydra_ccgqa_prep_tiled_ok", 4, 1, 32, _lib.BF16) == 1

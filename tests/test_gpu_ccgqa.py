@@ -173,3 +173,36 @@ def test_prep_generic_kernel_fallback(cuda, monkeypatch):
                          temperature=params["key_temperature"].to(cuda), cos=cos.to(cuda), sin=sin.to(cuda))
     for got, want in zip((q, k, v), ref):
         assert max_rel_err(got.cpu(), want) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ks", [1, 2, 5])
+def test_module_conv_kernel_sizes(cuda, dtype, ks):
+    """conv_kernel_size other than 3 (attention.py:132-145 builds both conv
+    sequences with it; fused_conv.py:52-57 pads by k-1): the module against
+    the oracle's forward, in fp32 and bf16, and the standalone conv
+    sequence against oracle.causal_conv_seq."""
+    from hydra_amd.attention import CCGQAAttention
+    from hydra_amd.attention.backends.ccgqa.kernels.fused_conv import OptimizedConvSequence
+
+    cfg = occ.CCGQAConfig(dim=512, n_heads=4, n_kv_heads=2, compression_factor=4, max_seq_len=128,
+                          conv_kernel_size=ks)
+    g = torch.Generator().manual_seed(50 + ks)
+    params = {k: v.to(dtype) for k, v in occ.init_params(cfg, g, std=0.05, temperature=2.0).items()}
+    x = torch.randn(2, 96, 512, generator=g).to(dtype)
+    want = occ.forward({k: v.float() for k, v in params.items()}, x.float(), cfg)
+    m = CCGQAAttention(dim=512, n_heads=4, n_kv_heads=2, compression_factor=4, max_seq_len=128,
+                       conv_kernel_size=ks)
+    m.load_state_dict(params)
+    with torch.no_grad():
+        got = m.to(cuda, dtype)(x.to(cuda)).float().cpu()
+    assert max_rel_err(got, want) < (1e-5 if dtype == torch.float32 else 2e-2)
+    seq = OptimizedConvSequence(128, 4, 1, ks).to(cuda, dtype)
+    seq.load_state_dict({"conv1.weight": params["q_conv.conv1.weight"],
+                         "conv2.weight": params["q_conv.conv2.weight"]})
+    xs = torch.randn(2, 70, 128, generator=g).to(dtype)
+    with torch.no_grad():
+        ys = seq(xs.to(cuda)).float().cpu()
+    ref = occ.causal_conv_seq(xs.float(), params["q_conv.conv1.weight"].float(),
+                              params["q_conv.conv2.weight"].float(), 4)
+    assert max_rel_err(ys, ref) < (1e-5 if dtype == torch.float32 else 2e-2)

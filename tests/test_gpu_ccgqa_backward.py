@@ -219,3 +219,33 @@ def test_module_eval_under_grad_uses_inference_kernels(cuda):
     out.backward(gout)
     for n, p in m.named_parameters():
         assert torch.equal(p.grad, eval_grads[n]), n
+
+
+@pytest.mark.parametrize("ks", [2, 5])
+def test_module_backward_conv_kernel_sizes(cuda, ks):
+    """The training path with conv_kernel_size != 3 (the im2col columns take
+    ks taps): forward + backward against fp64 autograd through
+    oracle.ccgqa.forward."""
+    from hydra_amd.attention import CCGQAAttention
+
+    case = dict(dim=256, n_heads=4, n_kv_heads=2, compression_factor=4, B=2, S=40,
+                conv_kernel_size=ks)
+    cfg, B, S, g, params = _setup(case, torch.float32, seed=45 + ks)
+    x = torch.randn(B, S, cfg.dim, generator=g)
+    gout = torch.randn(B, S, cfg.dim, generator=g)
+    p64 = {k: _leaf64(v) for k, v in params.items()}
+    x64 = _leaf64(x)
+    out = occ.forward(p64, x64, cfg)
+    (out * gout.double()).sum().backward()
+    m = CCGQAAttention(dim=cfg.dim, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+                       compression_factor=cfg.compression_factor, max_seq_len=cfg.max_seq_len,
+                       conv_kernel_size=ks)
+    m.load_state_dict(params)
+    m = m.to(cuda).train()
+    xd = x.to(cuda).requires_grad_(True)
+    od = m(xd)
+    assert max_rel_err(od.detach().cpu(), out) < 1e-5
+    od.backward(gout.to(cuda))
+    assert max_rel_err(xd.grad.cpu(), x64.grad) < 1e-4
+    for n, prm in m.named_parameters():
+        assert max_rel_err(prm.grad.cpu(), p64[n].grad) < 1e-4, n
