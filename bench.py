@@ -35,7 +35,7 @@ Also reported on the same line:
                 cpu_baselines adds configs 1, 2 and 4 the same way.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                      [--only-c3] [--no-c5]
+                      [--only-c3] [--only-attn-bwd] [--no-c5]
 """
 from __future__ import annotations
 
@@ -883,6 +883,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-c3", action="store_true", help="skip every section but config 3")
+    ap.add_argument("--only-attn-bwd", action="store_true",
+                    help="run only the attention backward section and print its figures "
+                         "(for counter runs of its kernels)")
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 model forward")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 512 MiB device copy (traffic-counter calibration)")
@@ -907,6 +910,9 @@ def main():
 
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.only_attn_bwd:
+        print(json.dumps({"attention_backward": bench_attention_backward(dev)}))
+        return
     step, ms_step, eager_ms, stages, attn_ms = bench_c3(dev, args.steps, args.warmup)
     probe_mhz, wall_khz = shader_clock_mhz(dev)
     clock, span_ms = attention_clock(step, wall_khz)
