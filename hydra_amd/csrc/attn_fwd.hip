@@ -709,7 +709,10 @@ struct KpLds {
   static constexpr int XF = DT * 16 + 2;             // exchanged floats per lane: O, m, l
   static constexpr int XCH = (KP - 1) * NW * 64 * XF * 2;  // exchange size in elements
   static constexpr int XOFF = KP * TILE;             // exchange start: the buffer-1 region
-  static constexpr int SIZE = XOFF + (XCH > KP * TILE ? XCH : KP * TILE);
+  // At hd 64 the output rows leave through a per-wave LDS tile (group 0's
+  // NW waves x 32 rows x HD), outside the buffers and the exchange.
+  static constexpr int SOFF = XOFF + (XCH > KP * TILE ? XCH : KP * TILE);
+  static constexpr int SIZE = SOFF + (HD == 64 ? NW * 32 * HD : 0);
 };
 
 template <int HD, bool CAUSAL, int MASK, int NW, int KP, bool FIXED>
@@ -987,10 +990,42 @@ __device__ __forceinline__ void attn_fwd_kp_body(
     // rows are stored after that barrier, so the stores overlap the next
     // item's first step instead of holding the barrier.
     if (nxt_pos < nitems) land();
-    if (store)
+    if constexpr (HD == 64) {
+      // The wave's 32 rows go to its LDS tile (16-byte chunks XOR-swizzled
+      // by row, so the column writes of 32 rows spread over the banks) and
+      // come back row-contiguous: each store instruction then writes 8
+      // whole 128-byte rows, instead of 8-byte pieces of 32 rows (the host
+      // takes this kernel only for 16-byte aligned rows).
+      if (grp == 0 && cur.active) {
+        uint16_t* sw = smem + Lay::SOFF + wq * 32 * HD;
+        const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int ch = 4 * dt + g4;
+            uint2 w;
+            w.x = pack2<bf16>(acc[dt][4 * g4 + 0] * inv, acc[dt][4 * g4 + 1] * inv);
+            w.y = pack2<bf16>(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
+            *reinterpret_cast<uint2*>(sw + n * HD + ((ch ^ (n & 7)) << 3) + 4 * hf) = w;
+          }
+        if (lse && hf == 0 && cur.qi < S)
+          lse[(static_cast<int64_t>(cur.b) * Hq + cur.h) * S + cur.qi] =
+              l_i > 0.f ? (m_i + __log2f(l_i)) * kLn2 : -INFINITY;
+        bf16* ob = o + static_cast<int64_t>(cur.b) * os0 + static_cast<int64_t>(cur.h) * os1;
+        const int c = lane & 7;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 8 * i + (lane >> 3);
+          const uint4 val = *reinterpret_cast<const uint4*>(sw + r * HD + ((c ^ (r & 7)) << 3));
+          if (cur.q0 + r < S) *reinterpret_cast<uint4*>(ob + static_cast<int64_t>(cur.q0 + r) * os2 + 8 * c) = val;
+        }
+      }
+    } else if (store) {
       attn_store_row<HD>(o + static_cast<int64_t>(cur.b) * os0 + static_cast<int64_t>(cur.h) * os1 +
                              static_cast<int64_t>(cur.qi) * os2, acc, m_i, l_i, hf,
                          lse ? lse + (static_cast<int64_t>(cur.b) * Hq + cur.h) * S + cur.qi : nullptr);
+    }
   };
 
   // At most two items per workgroup (the launch makes P >= items / 2): the
@@ -1259,9 +1294,12 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
       return true;
     };
     const bool s32 = fits32(qs, 3) && fits32(ks, 3) && fits32(vs, 4) && fits32(os, 3);
-    bool kp = vt && s32 && items < 2 * slots;
+    // at hd 64 it stores 16-byte row chunks
+    const bool o16 = HD != 64 || ((reinterpret_cast<uintptr_t>(O) & 15) == 0 && os[0] % 8 == 0 &&
+                                  os[1] % 8 == 0 && os[2] % 8 == 0);
+    bool kp = vt && s32 && o16 && items < 2 * slots;
     if (sched && strcmp(sched, "streamk") == 0) kp = false;
-    if (sched && strcmp(sched, "kp") == 0) kp = vt && s32;
+    if (sched && strcmp(sched, "kp") == 0) kp = vt && s32 && o16;
     if (getenv("HYDRA_ATTN_WGS")) kp = false;
     if (kp) {
       if (need) {
