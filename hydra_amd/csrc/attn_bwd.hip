@@ -192,15 +192,54 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
   const int b = bk / Hkv, kvh = bk - b * Hkv;
   const int nkg = (S + 32 * KB - 1) / (32 * KB);
   const int nqt = (S + 31) / 32;
-  // Workgroup -> (key group kg, chunk): key groups in order (the longest
-  // causal walks first), each split into ceil(nq / ch) chunks of ch query
-  // tiles.  Scalar loop over at most nkg groups.
-  int kg = 0, nch = 1, chunk = static_cast<int>(blockIdx.x) / BHkv;
-  for (;; ++kg) {
-    nch = ((CAUSAL ? nqt - KB * kg : nqt) + ch - 1) / ch;
-    if (chunk < nch || kg + 1 >= nkg) break;
-    chunk -= nch;
+  // Workgroup -> (key group kg, chunk): each key group's nq query tiles
+  // are cut into ceil(nq / ch) chunks of ch tiles.  Without chunking
+  // (ch >= nqt) the key groups come in order, the longest causal walks
+  // first.  With chunking the order is longest first over all chunks, so
+  // that the dispatcher's next-free-CU assignment is a longest-processing-
+  // time schedule: every full chunk (key groups in order), then the partial
+  // chunks by decreasing length.  Their lengths nq mod ch repeat with
+  // period T = ch / gcd(ch, KB) in kg (causal; 1 otherwise), so the partial
+  // chunks are taken class by class (kg = j, j + T, ...), classes by
+  // decreasing remainder.  Scalar loops: nkg, then (ch - 1) x T <= 240
+  // iterations (the host chunks with ch <= 16).
+  auto nq_of = [&](int g) { return CAUSAL ? nqt - KB * g : nqt; };
+  int kg = -1, chunk = static_cast<int>(blockIdx.x) / BHkv;
+  if (ch >= nqt) {
+    for (kg = 0; kg + 1 < nkg; ++kg) {
+      const int c = (nq_of(kg) + ch - 1) / ch;
+      if (chunk < c) break;
+      chunk -= c;
+    }
+  } else {
+    for (int g = 0; g < nkg; ++g) {
+      const int f = nq_of(g) / ch;
+      if (chunk < f) {
+        kg = g;
+        break;
+      }
+      chunk -= f;
+    }
+    if (kg < 0) {
+      int a = ch, c = KB;  // gcd(ch, KB)
+      while (c) {
+        const int t = a % c;
+        a = c;
+        c = t;
+      }
+      const int T = CAUSAL ? ch / a : 1;
+      for (int r = ch - 1; r >= 1 && kg < 0; --r)
+        for (int j = 0; j < T && j < nkg && kg < 0; ++j) {
+          if (nq_of(j) % ch != r) continue;
+          const int cnt = (nkg - j + T - 1) / T;
+          if (chunk < cnt) kg = j + chunk * T;
+          else chunk -= cnt;
+        }
+      kg = max(kg, 0);  // not reached: the host launches exactly the chunk count
+      chunk = nq_of(kg) / ch;
+    }
   }
+  const int nch = (nq_of(kg) + ch - 1) / ch;
   const int kg0 = 32 * KB * kg;           // first key of the workgroup
   const int kw0 = kg0 + 32 * kbl;         // first key of this wave
   const int key = kw0 + n;
@@ -900,7 +939,7 @@ DkdvPlan plan_dkdv(int hd, int S, int G, int BHkv, bool causal) {
   p.ch = nqt;
   if (static_cast<int64_t>(nkg) * BHkv < 2 * static_cast<int64_t>(device_cus())) {
     const char* e = std::getenv("HYDRA_ATTN_BWD_CHUNK");
-    p.ch = std::max(1, std::min(nqt, e ? std::atoi(e) : 16));
+    p.ch = std::max(1, std::min({nqt, 16, e ? std::atoi(e) : 16}));
   }
   p.nwg = 0;
   for (int kg = 0; kg < nkg; ++kg) p.nwg += ((causal ? nqt - p.KB * kg : nqt) + p.ch - 1) / p.ch;
