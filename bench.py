@@ -311,7 +311,10 @@ def _time_rotating(fn, sets, iters, warmup=3):
 
     The calls are captured once into a HIP graph (torch.cuda.graph) and the
     graph is replayed, so the figure is kernel time on the GPU timeline and
-    not the Python/ctypes launch cost, which exceeds a ~10 us kernel."""
+    not the Python/ctypes launch cost, which exceeds a ~10 us kernel.  The
+    graph holds at least 96 calls, so the gap at each replay boundary is
+    spread over as many calls (with 12 calls per graph a ~9 us kernel read
+    ~0.3 us longer)."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -320,7 +323,7 @@ def _time_rotating(fn, sets, iters, warmup=3):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    n_per = max(len(sets), 8)
+    n_per = max(len(sets), 96)
     with torch.cuda.graph(graph):
         for i in range(n_per):
             fn(*sets[i % len(sets)])
