@@ -37,6 +37,20 @@ def test_factory_whitelist_and_env(monkeypatch):
                                       compression_factor=4, attention_kwargs={})
 
 
+def test_build_ccqa_attention_both_import_paths():
+    """build_ccqa_attention from the package (backends/ccgqa/__init__.py:12-15,
+    a lazy alias) and from backend.py (:8-17) build the same module."""
+    from hydra_amd.attention import CCGQAAttention
+    from hydra_amd.attention.backends.ccgqa import build_ccqa_attention as from_pkg
+    from hydra_amd.attention.backends.ccgqa.backend import build_ccqa_attention as from_backend
+
+    kw = dict(dim=256, n_heads=4, n_kv_heads=1, compression_factor=4, max_seq_len=64, conv_kernel_size=5)
+    a, b = from_pkg(**kw), from_backend(**kw)
+    assert type(a) is CCGQAAttention and type(b) is CCGQAAttention
+    assert a.conv_kernel_size == 5 and a.q_conv.kernel_size == 5
+    assert a.state_dict().keys() == b.state_dict().keys()
+
+
 def test_module_structure_matches_reference():
     """Paper-compliance structure of the debug shape (tests/test_paper_compliance.py:185-272)."""
     from hydra_amd.attention import CCGQAAttention
