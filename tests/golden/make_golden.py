@@ -230,7 +230,7 @@ def _bf16_init_(module: torch.nn.Module, g: torch.Generator, std: float = 0.02) 
 
 
 def make_hydra_block() -> None:
-    """Config-1 composition (SURVEY a15): _safe_embedding_lookup
+    """Config-1 composition: _safe_embedding_lookup
     (hydra/model/framework/model.py:51-73, scale sqrt(dim), ids clamped) then
     HydraBlock.forward (blocks.py:68-70) with its MLP replaced by
     SwiGLUMLPFused(dim, int(dim * 8/3)) (the unrounded hidden of config 1),
