@@ -721,7 +721,7 @@ __device__ __forceinline__ void attn_fwd_kp_body(
     bf16* __restrict__ o, float* __restrict__ lse, const uint8_t* __restrict__ kmask,
     int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int P,
     int qs0, int qs1, int qs2, int ks0, int ks1, int ks2,
-    int vs0, int vs1, int vs2, int os0, int os1, int os2, float scale_log2) {
+    int vs0, int vs1, int vs2, int os0, int os1, int os2, float scale_log2, bool o16) {
   constexpr int BN = kAttnBN;
   constexpr int KSTEPS = HD / 16;
   constexpr int DT = (HD + 31) / 32;
@@ -990,12 +990,14 @@ __device__ __forceinline__ void attn_fwd_kp_body(
     // rows are stored after that barrier, so the stores overlap the next
     // item's first step instead of holding the barrier.
     if (nxt_pos < nitems) land();
-    if constexpr (HD == 64) {
+    bool staged = false;
+    if constexpr (HD == 64) staged = o16;
+    if (staged) {
       // The wave's 32 rows go to its LDS tile (16-byte chunks XOR-swizzled
       // by row, so the column writes of 32 rows spread over the banks) and
       // come back row-contiguous: each store instruction then writes 8
-      // whole 128-byte rows, instead of 8-byte pieces of 32 rows (the host
-      // takes this kernel only for 16-byte aligned rows).
+      // whole 128-byte rows, instead of 8-byte pieces of 32 rows (o16: the
+      // host found the rows 16-byte aligned; otherwise the 8-byte stores).
       if (grp == 0 && cur.active) {
         uint16_t* sw = smem + Lay::SOFF + wq * 32 * HD;
         const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
@@ -1052,7 +1054,7 @@ __global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
     int S, int Hq, int Hkv, int G, int ntasks, int nwg, int BH, int P,
     int qs0, int qs1, int qs2, int ks0, int ks1, int ks2,
     int vs0, int vs1, int vs2, int os0, int os1, int os2, float scale_log2, const void* tau, int tau_bf16,
-    unsigned long long* __restrict__ clk) {
+    int o16, unsigned long long* __restrict__ clk) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[KpLds<HD, NW, KP>::SIZE];
   // Clock stamps (measurement aid, off unless the host installed a buffer):
   // thread 0 records the shader-clock and wall-clock counters when the
@@ -1065,7 +1067,7 @@ __global__ __launch_bounds__(64 * NW * KP) void attn_fwd_kp_kernel(
 #define HYDRA_KP_BODY(FX)                                                                       \
   attn_fwd_kp_body<HD, CAUSAL, MASK, NW, KP, FX>(smem, q, k, v, o, lse, kmask, S, Hq, Hkv, G,    \
                                                  ntasks, nwg, BH, P, qs0, qs1, qs2, ks0, ks1, ks2, \
-                                                 vs0, vs1, vs2, os0, os1, os2, scale_log2)
+                                                 vs0, vs1, vs2, os0, os1, os2, scale_log2, o16 != 0)
   if constexpr (FXM == 2) {
     if (attn_fixed_from_temperature(tau, tau_bf16, scale_log2)) HYDRA_KP_BODY(true);
     else HYDRA_KP_BODY(false);
@@ -1294,12 +1296,9 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
       return true;
     };
     const bool s32 = fits32(qs, 3) && fits32(ks, 3) && fits32(vs, 4) && fits32(os, 3);
-    // at hd 64 it stores 16-byte row chunks
-    const bool o16 = HD != 64 || ((reinterpret_cast<uintptr_t>(O) & 15) == 0 && os[0] % 8 == 0 &&
-                                  os[1] % 8 == 0 && os[2] % 8 == 0);
-    bool kp = vt && s32 && o16 && items < 2 * slots;
+    bool kp = vt && s32 && items < 2 * slots;
     if (sched && strcmp(sched, "streamk") == 0) kp = false;
-    if (sched && strcmp(sched, "kp") == 0) kp = vt && s32 && o16;
+    if (sched && strcmp(sched, "kp") == 0) kp = vt && s32;
     if (getenv("HYDRA_ATTN_WGS")) kp = false;
     if (kp) {
       if (need) {
@@ -1317,10 +1316,15 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
       const int32_t ks32[3] = {(int32_t)ks[0], (int32_t)ks[1], (int32_t)ks[2]};
       const int32_t vs32[3] = {(int32_t)vs[0], (int32_t)vs[1], (int32_t)vs[3]};
       const int32_t os32[3] = {(int32_t)os[0], (int32_t)os[1], (int32_t)os[2]};
+      // 16-byte aligned output rows take whole-row stores through LDS (hd
+      // 64); others the 8-byte stores (the workspace query cannot see the
+      // pointer, so the choice does not change the schedule)
+      const bool o16 = (reinterpret_cast<uintptr_t>(O) & 15) == 0 && os[0] % 8 == 0 && os[1] % 8 == 0 &&
+                       os[2] % 8 == 0;
       kkern<<<dim3(static_cast<unsigned>(Pk)), 64 * NW * KP, 0, st>>>(
           Q, K, V, O, lse, kmask, iS, (int)Hq, (int)Hkv, G, ntasks, nwg, BH, Pk, qs32[0], qs32[1], qs32[2],
           ks32[0], ks32[1], ks32[2], vs32[0], vs32[1], vs32[2], os32[0], os32[1], os32[2], sl2, tau, tau_bf16,
-          Pk <= g_clock_stamp_cap ? g_clock_stamps : nullptr);
+          o16 ? 1 : 0, Pk <= g_clock_stamp_cap ? g_clock_stamps : nullptr);
       return check_launch("attn_fwd_kp_kernel");
     }
     auto kern = vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX> : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>;

@@ -408,6 +408,31 @@ def test_attention_vt_rows_schedules(cuda, monkeypatch, case, mode, sched):
         assert (lse.cpu() - torch.logsumexp(logits, -1)).abs().max().item() < 2e-2
 
 
+@pytest.mark.parametrize("pad,shift", [(68, 0), (64, 4), (72, 0)])
+def test_attention_vt_rows_output_views(cuda, monkeypatch, pad, shift):
+    """The key-split kernel at hd 64 stores whole 16-byte row chunks, so it
+    takes an output view only with 16-byte aligned rows; other views (row
+    stride 68, or a base 8 bytes past alignment) run the stream-K kernel.
+    Every view gets the oracle's result, and the padding around it is not
+    written."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_forward
+
+    monkeypatch.setenv("HYDRA_ATTN_SCHED", "kp")
+    B, Hq, Hkv, S, hd = 2, 4, 1, 264, 64
+    q, k, v = _qkv(B, Hq, Hkv, S, hd, seed=77)
+    dev = lambda t: t.to(cuda, torch.bfloat16)
+    buf = torch.full((B * S * Hq * pad + shift,), 7.0, device=cuda, dtype=torch.bfloat16)
+    view = buf[shift:].view(B, S, Hq, pad)[..., :hd].transpose(1, 2)
+    out, _ = attention_forward(dev(q), dev(k), _vt_rows(dev(v)), causal=True, out=view)
+    ref = occ.attention(q, k, v, causal=True)
+    assert max_rel_err(view.float().cpu(), ref) < 2e-2
+    full = buf[shift:].view(B, S, Hq, pad)
+    if pad > hd:
+        assert bool((full[..., hd:] == 7.0).all())
+    if shift:
+        assert bool((buf[:shift] == 7.0).all())
+
+
 FIXED_VT_CASES = [
     # B, Hq, Hkv, S, hd, temperature, causal
     (4, 4, 1, 512, 64, 1.0, True),
