@@ -114,39 +114,74 @@ __device__ __forceinline__ uint4 ld16_or0(const bf16* p, bool ok) {
 
 // ---------------------------------------------------------------------------
 // D[r] = sum_d dO[r,d] O[r,d] and lse2[r] = lse[r] * log2(e), r = (b*Hq+h)*S+s.
-// TPR threads per row, each a strided set of E-element chunks.
-template <typename T, int TPR, bool VEC>
+// blockIdx.y + 65535 blockIdx.z = b*Hq+h; TPR threads per row, each a
+// strided set of E-element chunks (ONE: the launch made hd <= TPR * E, one
+// chunk per thread); a thread group takes RPG consecutive rows, all of
+// their loads issued before the sums.
+template <typename T, int TPR, bool VEC, int RPG, bool ONE>
 __global__ __launch_bounds__(256) void attn_bwd_rowdot_kernel(
     const T* __restrict__ o, const T* __restrict__ dout, const float* __restrict__ lse,
-    float* __restrict__ dvec, float* __restrict__ lse2, int64_t rows, int Hq, int S, int hd,
+    float* __restrict__ dvec, float* __restrict__ lse2, int BH, int Hq, int S, int hd,
     int64_t os0, int64_t os1, int64_t os2, int64_t ds0, int64_t ds1, int64_t ds2) {
   constexpr int E = VEC ? 16 / int(sizeof(T)) : 1;
-  const int64_t r = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / TPR;
+  const int bh = blockIdx.y + 65535 * blockIdx.z;
+  if (bh >= BH) return;
+  const int b = bh / Hq, h = bh - b * Hq;
+  const int s0 = ((blockIdx.x * 256 + threadIdx.x) / TPR) * RPG;
   const int sub = threadIdx.x % TPR;
-  float acc = 0.f;
-  if (r < rows) {
-    const int s = static_cast<int>(r % S);
-    const int64_t bh = r / S;
-    const int h = static_cast<int>(bh % Hq);
-    const int64_t b = bh / Hq;
-    const T* orow = o + b * os0 + h * os1 + s * os2;
-    const T* drow = dout + b * ds0 + h * ds1 + s * ds2;
-    for (int e = sub * E; e < hd; e += TPR * E) {
-      if constexpr (VEC) {
-        float a[E], c[E];
-        load16<T>(orow + e, a);
-        load16<T>(drow + e, c);
+  const T* obase = o + b * os0 + h * os1;
+  const T* dbase = dout + b * ds0 + h * ds1;
+  float acc[RPG];
+  if constexpr (ONE && VEC) {
+    // hd <= TPR * E: one 16-byte chunk of each row per thread, all loaded first
+    float a[RPG][E], c[RPG][E];
 #pragma unroll
-        for (int i = 0; i < E; ++i) acc = fmaf(a[i], c[i], acc);
+    for (int j = 0; j < RPG; ++j) {
+      const int s = s0 + j, e = sub * E;
+      if (s < S && e < hd) {
+        load16<T>(obase + static_cast<int64_t>(s) * os2 + e, a[j]);
+        load16<T>(dbase + static_cast<int64_t>(s) * ds2 + e, c[j]);
       } else {
-        acc = fmaf(to_f32(orow[e]), to_f32(drow[e]), acc);
+#pragma unroll
+        for (int i = 0; i < E; ++i) a[j][i] = c[j][i] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+      acc[j] = 0.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc[j] = fmaf(a[j][i], c[j][i], acc[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+      acc[j] = 0.f;
+      const int s = s0 + j;
+      if (s >= S) continue;
+      const T* orow = obase + static_cast<int64_t>(s) * os2;
+      const T* drow = dbase + static_cast<int64_t>(s) * ds2;
+      for (int e = sub * E; e < hd; e += TPR * E) {
+        if constexpr (VEC) {
+          float a[E], c[E];
+          load16<T>(orow + e, a);
+          load16<T>(drow + e, c);
+#pragma unroll
+          for (int i = 0; i < E; ++i) acc[j] = fmaf(a[i], c[i], acc[j]);
+        } else {
+          acc[j] = fmaf(to_f32(orow[e]), to_f32(drow[e]), acc[j]);
+        }
       }
     }
   }
-  acc = wave_sum<TPR>(acc);
-  if (r < rows && sub == 0) {
-    dvec[r] = acc;
-    lse2[r] = lse[r] * kLog2e;
+#pragma unroll
+  for (int j = 0; j < RPG; ++j) {
+    const float v = wave_sum<TPR>(acc[j]);
+    const int s = s0 + j;
+    if (s < S && sub == 0) {
+      const int64_t r = static_cast<int64_t>(bh) * S + s;
+      dvec[r] = v;
+      lse2[r] = lse[r] * kLog2e;
+    }
   }
 }
 
@@ -899,23 +934,30 @@ struct BwdArgs {
 
 template <typename T>
 int launch_rowdot(const BwdArgs& a, float* dvec, float* lse2) {
-  const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.S;
   constexpr int E = 16 / int(sizeof(T));
   const bool vec = a.hd % E == 0 && aligned16(a.o) && aligned16(a.dout) && a.os[0] % E == 0 &&
                    a.os[1] % E == 0 && a.os[2] % E == 0 && a.dos[0] % E == 0 &&
                    a.dos[1] % E == 0 && a.dos[2] % E == 0;
-  constexpr int TPR = 16;
-  const dim3 grid(static_cast<unsigned>((rows * TPR + 255) / 256));
   const T* o = static_cast<const T*>(a.o);
   const T* d = static_cast<const T*>(a.dout);
-  if (vec)
-    attn_bwd_rowdot_kernel<T, TPR, true><<<grid, 256, 0, a.st>>>(
-        o, d, a.lse, dvec, lse2, rows, a.Hq, a.S, a.hd, a.os[0], a.os[1], a.os[2], a.dos[0],
-        a.dos[1], a.dos[2]);
-  else
-    attn_bwd_rowdot_kernel<T, TPR, false><<<grid, 256, 0, a.st>>>(
-        o, d, a.lse, dvec, lse2, rows, a.Hq, a.S, a.hd, a.os[0], a.os[1], a.os[2], a.dos[0],
-        a.dos[1], a.dos[2]);
+  constexpr int RPG = 2;
+  // rows per block: 256 / TPR thread groups x RPG rows
+  const int BH = a.B * a.Hq;
+  auto grid = [&](int tpr) {
+    return dim3(static_cast<unsigned>((a.S + 256 / tpr * RPG - 1) / (256 / tpr * RPG)),
+                static_cast<unsigned>(std::min(BH, 65535)), static_cast<unsigned>((BH + 65534) / 65535));
+  };
+#define HYDRA_ROWDOT(TPRV, VECV, ONEV)                                                              \
+  attn_bwd_rowdot_kernel<T, TPRV, VECV, RPG, ONEV><<<grid(TPRV), 256, 0, a.st>>>(                   \
+      o, d, a.lse, dvec, lse2, BH, a.Hq, a.S, a.hd, a.os[0], a.os[1], a.os[2], a.dos[0], a.dos[1],  \
+      a.dos[2])
+  // vector path: one 16-byte chunk per thread and row when hd <= 16 E
+  if (vec && a.hd <= 4 * E) HYDRA_ROWDOT(4, true, true);
+  else if (vec && a.hd <= 8 * E) HYDRA_ROWDOT(8, true, true);
+  else if (vec && a.hd <= 16 * E) HYDRA_ROWDOT(16, true, true);
+  else if (vec) HYDRA_ROWDOT(16, true, false);
+  else HYDRA_ROWDOT(16, false, false);
+#undef HYDRA_ROWDOT
   return check_launch("attn_bwd: rowdot");
 }
 
