@@ -551,30 +551,42 @@ __global__ __launch_bounds__(64 * KB * HG) void attn_bwd_dkdv_kernel(
 }
 
 // Sums the chunk partials of key groups that were split (in chunk order),
-// scales dK and writes both gradients; one thread per 4 values of a row.
+// scales dK and writes both gradients; one thread per 4 values of a key
+// row, blockIdx.y + 65535 blockIdx.z = b * Hkv + kv head.  The loads of 8
+// chunks are issued before they are added (in order), so a thread waits
+// for one load latency per 8 chunks.
 template <int HD, bool CAUSAL, int KB>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_reduce_kernel(
-    const float* __restrict__ part, bf16* __restrict__ dk, bf16* __restrict__ dv, int Hkv, int S,
-    int ch, int maxch, int64_t total, int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0,
-    int64_t dvs1, int64_t dvs2, float scale) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int d = 4 * static_cast<int>(i % (HD / 4));
-  const int64_t row = i / (HD / 4);
-  const int key = static_cast<int>(row % S);
-  const int bk = static_cast<int>(row / S);
+    const float* __restrict__ part, bf16* __restrict__ dk, bf16* __restrict__ dv, int BHkv, int Hkv,
+    int S, int ch, int maxch, int64_t dks0, int64_t dks1, int64_t dks2, int64_t dvs0, int64_t dvs1,
+    int64_t dvs2, float scale) {
+  constexpr int CS = KB * 32 * HD * 2;  // floats per chunk partial (dK, then dV)
+  constexpr int U = 8;
+  const int bk = blockIdx.y + 65535 * blockIdx.z;
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < S * HD / 4
+  if (bk >= BHkv || i >= S * (HD / 4)) return;
+  const int d = 4 * (i % (HD / 4));
+  const int key = i / (HD / 4);
   const int nkg = (S + 32 * KB - 1) / (32 * KB), nqt = (S + 31) / 32;
   const int kg = key / (32 * KB);
   const int nch = ((CAUSAL ? nqt - KB * kg : nqt) + ch - 1) / ch;
   if (nch <= 1) return;
-  const float* pk = part + (static_cast<int64_t>(bk) * nkg + kg) * maxch * (KB * 32 * HD * 2) +
-                    (key - 32 * KB * kg) * HD + d;
+  const float* pk = part + (static_cast<int64_t>(bk) * nkg + kg) * maxch * CS + (key - 32 * KB * kg) * HD + d;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f), c = a;
-  for (int j = 0; j < nch; ++j) {
-    const float4 x = *reinterpret_cast<const float4*>(pk + static_cast<int64_t>(j) * (KB * 32 * HD * 2));
-    const float4 y = *reinterpret_cast<const float4*>(pk + static_cast<int64_t>(j) * (KB * 32 * HD * 2) + KB * 32 * HD);
-    a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
-    c.x += y.x; c.y += y.y; c.z += y.z; c.w += y.w;
+  for (int j0 = 0; j0 < nch; j0 += U) {
+    float4 x[U], y[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j0 + u < nch) {
+        x[u] = *reinterpret_cast<const float4*>(pk + static_cast<int64_t>(j0 + u) * CS);
+        y[u] = *reinterpret_cast<const float4*>(pk + static_cast<int64_t>(j0 + u) * CS + KB * 32 * HD);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j0 + u < nch) {
+        a.x += x[u].x; a.y += x[u].y; a.z += x[u].z; a.w += x[u].w;
+        c.x += y[u].x; c.y += y[u].y; c.z += y[u].z; c.w += y[u].w;
+      }
   }
   const int b = bk / Hkv, kvh = bk - b * Hkv;
   *reinterpret_cast<uint2*>(dk + b * dks0 + kvh * dks1 + key * dks2 + d) =
@@ -1009,12 +1021,12 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* p
       a.dks[2], a.dvs[0], a.dvs[1], a.dvs[2], sl2, a.scale);                                     \
   if (int rc = check_launch("attn_bwd: dkdv")) return rc;                                       \
   if (pl.maxch > 1) {                                                                            \
-    const int64_t total = static_cast<int64_t>(BHkv) * a.S * (HD / 4);                          \
     attn_bwd_dkdv_reduce_kernel<HD, CAUSAL, KBV>                                                 \
-        <<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, a.st>>>(                    \
-            part, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), a.Hkv, a.S, pl.ch,         \
-            pl.maxch, total, a.dks[0], a.dks[1], a.dks[2], a.dvs[0], a.dvs[1], a.dvs[2],         \
-            a.scale);                                                                            \
+        <<<dim3(static_cast<unsigned>((a.S * (HD / 4) + 255) / 256),                             \
+                static_cast<unsigned>(std::min(BHkv, 65535)),                                    \
+                static_cast<unsigned>((BHkv + 65534) / 65535)), 256, 0, a.st>>>(                 \
+            part, static_cast<bf16*>(a.dk), static_cast<bf16*>(a.dv), BHkv, a.Hkv, a.S, pl.ch,   \
+            pl.maxch, a.dks[0], a.dks[1], a.dks[2], a.dvs[0], a.dvs[1], a.dvs[2], a.scale);      \
     if (int rc = check_launch("attn_bwd: dkdv reduce")) return rc;                              \
   }
     if (pl.HG == 2) {
