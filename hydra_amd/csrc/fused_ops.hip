@@ -175,22 +175,24 @@ __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(
 template <typename C, int N>
 struct alignas(N * sizeof(C)) CsVec { C v[N]; };
 
+// Grid: x over (s, c) of one (b, head group), y + 65535 z = b * ng + hg, so
+// a thread finds its row with one 32-bit shift (or division) and no 64-bit
+// index arithmetic; csh = log2(D / E) when that is a power of two, else -1.
 template <typename T, typename C, int HB, int BS, bool CSV, bool BWD>
 __global__ __launch_bounds__(BS) void rope_hg_kernel(
     const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
     T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
-    int64_t cs_rs, int64_t nthr) {
+    int64_t cs_rs, int nbg, int csh) {
   constexpr int E = Vec<T>::N;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * BS + threadIdx.x;
-  if (t >= nthr) return;
+  const int bg = blockIdx.y + 65535 * blockIdx.z;
   const int cpr = D / E;
-  const int c = static_cast<int>(t % cpr);
-  int64_t r = t / cpr;
-  const int s = static_cast<int>(r % S);
-  r /= S;
+  const int t = blockIdx.x * BS + threadIdx.x;
+  if (bg >= nbg || t >= S * cpr) return;
+  const int s = csh >= 0 ? t >> csh : t / cpr;
+  const int c = t - s * cpr;
   const int ng = (H + HB - 1) / HB;
-  const int hg = static_cast<int>(r % ng);
-  const int64_t b = r / ng;
+  const int64_t b = bg / ng;
+  const int hg = bg - static_cast<int>(b) * ng;
   const int h0 = hg * HB;
   uint4 raw[HB];
   const T* xr = x + b * xb + static_cast<int64_t>(s) * xsr + c * E;
@@ -245,16 +247,21 @@ static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
                       aligned16(out);
   constexpr int kRopeBlock = 128;
   const int hb = H % 6 == 0 ? 6 : 4;
-  const int64_t nthr = B * ((H + hb - 1) / hb) * S * (D / E);
-  if (vec_ok && (nthr + kRopeBlock - 1) / kRopeBlock < (int64_t(1) << 31)) {
-    const dim3 grid(static_cast<unsigned>((nthr + kRopeBlock - 1) / kRopeBlock));
+  const int64_t nbg = B * ((H + hb - 1) / hb);
+  const int64_t per_bg = S * (D / E);
+  if (vec_ok && per_bg < (int64_t(1) << 31) - kRopeBlock && nbg <= 65535 * int64_t(65535)) {
+    const dim3 grid(static_cast<unsigned>((per_bg + kRopeBlock - 1) / kRopeBlock),
+                    static_cast<unsigned>(std::min<int64_t>(nbg, 65535)),
+                    static_cast<unsigned>((nbg + 65534) / 65535));
+    const int cpr = static_cast<int>(D / E);
+    const int csh = (cpr & (cpr - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(cpr)) : -1;
     constexpr size_t kCsBytes = (E / 2) * sizeof(C);
     const bool csv = cs_rs % (E / 2) == 0 && reinterpret_cast<uintptr_t>(cs) % kCsBytes == 0 &&
                      reinterpret_cast<uintptr_t>(sn) % kCsBytes == 0;
 #define HYDRA_ROPE_CASE(HB, CV)                                                            \
   if (hb == HB && csv == CV)                                                               \
     rope_hg_kernel<T, C, HB, kRopeBlock, CV, BWD><<<grid, kRopeBlock, 0, st>>>(            \
-        X, CS, SN, O, (int)H, (int)S, (int)D, xs[0], xs[1], xs[2], cs_rs, nthr);
+        X, CS, SN, O, (int)H, (int)S, (int)D, xs[0], xs[1], xs[2], cs_rs, (int)nbg, csh);
     HYDRA_ROPE_CASE(6, true) HYDRA_ROPE_CASE(6, false) HYDRA_ROPE_CASE(4, true) HYDRA_ROPE_CASE(4, false)
 #undef HYDRA_ROPE_CASE
     return check_launch("rope_hg_kernel");
