@@ -64,6 +64,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
 }
 
 constexpr int kAttnBN = 64;  // keys per tile of the bf16 kernel
+// At head_dim 16 the O^T tile has 16 unused rows; row 24 of the V^T tile
+// holds ones (no tile load writes rows past 21 there), so O^T row 24 -- the
+// first lane half's register 12 -- is the row sum of the bf16 P.
+constexpr int kAttnOnesRow = 24;
 
 // Key tiles item wg walks: all of them, or (causal) up to its last query.
 template <int NW>
@@ -171,8 +175,10 @@ __device__ __forceinline__ void attn_store_row(bf16* orow, const f32x16_t* acc, 
 // (m_i, l_i, acc) and O^T += V^T P^T from the staged V^T rows vt (pitch
 // VROW).  Lane (n, hf) owns query row qi; l_i is the lane's half of the row
 // sum.  FIXED: Q was pre-scaled by scale * log2(e) and bounded, P = exp2 of
-// the accumulator with no reference max.
-template <int HD, bool CAUSAL, int MASK, bool FIXED, bool MASKED, int KROW, int VROW>
+// the accumulator with no reference max.  RSM: the caller keeps a row of
+// ones in the V^T tile's padding (row kAttnOnesRow), so the PV MFMAs also
+// sum P into that row of O^T and the tile adds nothing to l_i.
+template <int HD, bool CAUSAL, int MASK, bool FIXED, bool MASKED, int KROW, int VROW, bool RSM = false>
 __device__ __forceinline__ void attn_tile(const uint16_t* kt, const uint16_t* vt, const bf16x8_t* qf,
                                           f32x16_t* acc, float& m_i, float& l_i, int key0, int qi,
                                           int S, int n, int hf, const uint8_t* kmrow, float scale_log2) {
@@ -251,12 +257,14 @@ __device__ __forceinline__ void attn_tile(const uint16_t* kt, const uint16_t* vt
     pk[s2].y = pack2<bf16>(p[2], p[3]);
     pk[s2].z = pack2<bf16>(p[4], p[5]);
     pk[s2].w = pack2<bf16>(p[6], p[7]);
-    rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
-    rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
-    rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
-    rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
+    if constexpr (!RSM) {
+      rs = dot2_bf16(pk[s2].x, kOnesBf16x2, rs);
+      rs = dot2_bf16(pk[s2].y, kOnesBf16x2, rs);
+      rs = dot2_bf16(pk[s2].z, kOnesBf16x2, rs);
+      rs = dot2_bf16(pk[s2].w, kOnesBf16x2, rs);
+    }
   }
-  l_i += rs;
+  if constexpr (!RSM) l_i += rs;
   // O^T += V^T P^T over PS k-steps of 16 keys.
 #pragma unroll
   for (int s2 = 0; s2 < PS; ++s2) {
@@ -370,10 +378,15 @@ __device__ __forceinline__ void attn_fwd_mfma_body(
     v_end = r.y;
   }
 
-  if (DT * 32 > HD) {  // zero the padding rows of both V^T buffers once
+  // HD 16: P's row sums come from the PV MFMAs (a row of ones in V^T)
+  constexpr bool RSM = HD == 16;
+  static_assert(!RSM || (VINS * 64 <= kAttnOnesRow * VSL && kAttnOnesRow < DT * 32),
+                "no V^T tile load reaches the row of ones");
+  if (DT * 32 > HD) {  // zero the padding rows of both V^T buffers once (ones in the sum row)
     for (int i = tid; i < (DT * 32 - HD) * VROW; i += NT) {
-      Vt[HD * VROW + i] = 0;
-      Vt[VBUF + HD * VROW + i] = 0;
+      const uint16_t f = RSM && HD + i / VROW == kAttnOnesRow ? 0x3f80 : 0;
+      Vt[HD * VROW + i] = f;
+      Vt[VBUF + HD * VROW + i] = f;
     }
   }
 
@@ -575,8 +588,8 @@ __device__ __forceinline__ void attn_fwd_mfma_body(
     auto tile = [&](int kb, auto masked_tag) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       const int buf = kb & 1;
-      attn_tile<HD, CAUSAL, MASK, FIXED, MASKED, KROW, VROW>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i, l_i,
-                                                            kb * BN, qi, S, n, hf, kmrow, scale_log2);
+      attn_tile<HD, CAUSAL, MASK, FIXED, MASKED, KROW, VROW, RSM>(Ks + buf * KBUF, Vt + buf * VBUF, qf, acc, m_i,
+                                                                 l_i, kb * BN, qi, S, n, hf, kmrow, scale_log2);
     };
 
 
@@ -616,7 +629,12 @@ __device__ __forceinline__ void attn_fwd_mfma_body(
       if (kb + 1 < kb1) zero_tail((kb + 1) * BN, (kb & 1) ^ 1);
     }
 
-    if (wave_active) l_i = halves_sum(l_i);
+    if constexpr (RSM) {
+      // O^T row 24: register 12 of the lanes with hf = 0 (rescaled with O)
+      if (wave_active) l_i = halves_sum(hf == 0 ? acc[0][12] : 0.f);
+    } else {
+      if (wave_active) l_i = halves_sum(l_i);
+    }
     if (kb0 == 0 && kb1 == nkb) {
       if (wave_active && qi < S)
         attn_store_row<HD>(o + b * os0 + h * os1 + static_cast<int64_t>(qi) * os2, acc, m_i, l_i, hf,
