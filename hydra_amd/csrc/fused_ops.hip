@@ -142,16 +142,17 @@ static int launch_rms_norm(const void* x, const void* w, void* y, int64_t rows,
 // BWD: the gradient with respect to x of the same rotation (its transpose:
 // sin negated), which the reference's CPU path gets from autograd.
 // 16-byte path (rope_hg_kernel): a thread rotates one chunk (E/2 pairs) of
-// HB heads of one row.  Otherwise (rope_scalar_kernel) blockIdx.y = b*H + h
-// and a thread rotates one pair.
+// HB heads of one row.  Otherwise (rope_scalar_kernel) blockIdx.y + 65535
+// blockIdx.z = b*H + h and a thread rotates one pair.
 // ===========================================================================
 template <typename T, typename C, bool BWD>
 __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(
     const T* __restrict__ x, const C* __restrict__ cs, const C* __restrict__ sn,
-    T* __restrict__ out, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
+    T* __restrict__ out, int BH, int H, int S, int D, int64_t xb, int64_t xh, int64_t xsr,
     int64_t xd, int64_t cs_rs) {
   const int half = D / 2;
-  const int bh = blockIdx.y;
+  const int bh = blockIdx.y + 65535 * blockIdx.z;
+  if (bh >= BH) return;
   const int b = bh / H, h = bh - b * H;
   const int t = blockIdx.x * kBlock + threadIdx.x;
   const int s = t / half;
@@ -268,8 +269,9 @@ static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
   }
   const int64_t threads = S * (D / 2);
   const dim3 grid(static_cast<unsigned>((threads + kBlock - 1) / kBlock),
-                  static_cast<unsigned>(B * H));
-  rope_scalar_kernel<T, C, BWD><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)H, (int)S,
+                  static_cast<unsigned>(std::min<int64_t>(B * H, 65535)),
+                  static_cast<unsigned>((B * H + 65534) / 65535));
+  rope_scalar_kernel<T, C, BWD><<<grid, kBlock, 0, st>>>(X, CS, SN, O, (int)(B * H), (int)H, (int)S,
                                                     (int)D, xs[0], xs[1], xs[2],
                                                     xs[3], cs_rs);
   return check_launch("rope_scalar_kernel");
@@ -909,7 +911,7 @@ extern "C" int hydra_rope_fwd(const void* x, const void* cos, const void* sin,
   if (B * H * S * D == 0) return HYDRA_OK;
   HYDRA_REQUIRE(x && cos && sin && out, "rope: null pointer");
   HYDRA_REQUIRE(cs_rs >= D / 2, "rope: cos/sin row stride smaller than head_dim/2");
-  HYDRA_REQUIRE(B * H <= 65535, "rope: B*H must be <= 65535");
+  HYDRA_REQUIRE(B * H <= int64_t(65535) * 65535, "rope: B*H too large");
   HYDRA_REQUIRE(S * D < (int64_t(1) << 31), "rope: S*D too large");
   auto st = static_cast<hipStream_t>(stream);
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
@@ -1073,7 +1075,7 @@ extern "C" int hydra_rope_bwd(const void* grad_y, const void* cos, const void* s
   if (B * H * S * D == 0) return HYDRA_OK;
   HYDRA_REQUIRE(grad_y && cos && sin && grad_x, "rope_bwd: null pointer");
   HYDRA_REQUIRE(cs_rs >= D / 2, "rope_bwd: cos/sin row stride smaller than head_dim/2");
-  HYDRA_REQUIRE(B * H <= 65535, "rope_bwd: B*H must be <= 65535");
+  HYDRA_REQUIRE(B * H <= int64_t(65535) * 65535, "rope_bwd: B*H too large");
   HYDRA_REQUIRE(S * D < (int64_t(1) << 31), "rope_bwd: S*D too large");
   auto st = static_cast<hipStream_t>(stream);
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {

@@ -54,6 +54,13 @@ MFMA_CASES = [(2, 4, 1, 256, 64), (1, 8, 2, 300, 64), (2, 2, 2, 128, 128), (1, 3
               (1, 6, 3, 97, 64), (1, 4, 1, 1000, 128), (1, 1, 1, 33, 64)]
 
 
+def test_attention_backward_many_heads(cuda):
+    """B x Hq past 65535: the row-dot launch spreads (batch, head) over grid y
+    and z."""
+    q, k, v, go = _inputs(16400, 4, 1, 16, 32, torch.bfloat16, seed=7)
+    _check(_run(q, k, v, go, True, cuda), q, k, v, go, True, TOL[torch.bfloat16])
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", MFMA_CASES)
 def test_attention_backward_mfma(cuda, shape, causal):

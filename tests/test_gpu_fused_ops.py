@@ -65,6 +65,17 @@ def test_rope(cuda, dtype, shape):
     assert max_rel_err(y, ref) < TOL[dtype]
 
 
+def test_rope_many_batch_head_groups(cuda):
+    """B x (head groups) past 65535: the launch spreads them over grid y and z."""
+    from hydra_amd.kernels import fused_rope
+
+    g = _gen(11)
+    x = torch.randn(65600, 6, 2, 64, generator=g).to(torch.bfloat16)
+    cos, sin = ofo.rope_cache(64, 2)
+    y = fused_rope(x.to(cuda), cos.to(cuda), sin.to(cuda)).cpu()
+    assert max_rel_err(y, ofo.rope(x.float(), cos, sin)) < TOL[torch.bfloat16]
+
+
 def test_rope_cache_row_stride_not_vector_aligned(cuda):
     """cos/sin rows 35 elements apart: the per-element cos/sin loads."""
     from hydra_amd.kernels import fused_rope
