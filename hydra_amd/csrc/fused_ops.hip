@@ -250,7 +250,7 @@ static int launch_rope(const void* x, const void* cs, const void* sn, void* out,
   const int hb = H % 6 == 0 ? 6 : 4;
   const int64_t nbg = B * ((H + hb - 1) / hb);
   const int64_t per_bg = S * (D / E);
-  if (vec_ok && per_bg < (int64_t(1) << 31) - kRopeBlock && nbg <= 65535 * int64_t(65535)) {
+  if (vec_ok && per_bg < (int64_t(1) << 31) - kRopeBlock) {  // nbg <= B * H < 2^31
     const dim3 grid(static_cast<unsigned>((per_bg + kRopeBlock - 1) / kRopeBlock),
                     static_cast<unsigned>(std::min<int64_t>(nbg, 65535)),
                     static_cast<unsigned>((nbg + 65534) / 65535));
@@ -911,7 +911,7 @@ extern "C" int hydra_rope_fwd(const void* x, const void* cos, const void* sin,
   if (B * H * S * D == 0) return HYDRA_OK;
   HYDRA_REQUIRE(x && cos && sin && out, "rope: null pointer");
   HYDRA_REQUIRE(cs_rs >= D / 2, "rope: cos/sin row stride smaller than head_dim/2");
-  HYDRA_REQUIRE(B * H <= int64_t(65535) * 65535, "rope: B*H too large");
+  HYDRA_REQUIRE(B * H < (int64_t(1) << 31), "rope: B*H too large");
   HYDRA_REQUIRE(S * D < (int64_t(1) << 31), "rope: S*D too large");
   auto st = static_cast<hipStream_t>(stream);
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
@@ -1075,7 +1075,7 @@ extern "C" int hydra_rope_bwd(const void* grad_y, const void* cos, const void* s
   if (B * H * S * D == 0) return HYDRA_OK;
   HYDRA_REQUIRE(grad_y && cos && sin && grad_x, "rope_bwd: null pointer");
   HYDRA_REQUIRE(cs_rs >= D / 2, "rope_bwd: cos/sin row stride smaller than head_dim/2");
-  HYDRA_REQUIRE(B * H <= int64_t(65535) * 65535, "rope_bwd: B*H too large");
+  HYDRA_REQUIRE(B * H < (int64_t(1) << 31), "rope_bwd: B*H too large");
   HYDRA_REQUIRE(S * D < (int64_t(1) << 31), "rope_bwd: S*D too large");
   auto st = static_cast<hipStream_t>(stream);
   return HYDRA_DISPATCH_DTYPE(dtype, T, [&] {
