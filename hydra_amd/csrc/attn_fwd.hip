@@ -202,7 +202,18 @@ __device__ __forceinline__ void attn_tile(const uint16_t* kt, const uint16_t* vt
       const uint4 a = *reinterpret_cast<const uint4*>(&kt[(32 * mt + n) * KROW + 16 * s + 8 * hf]);
       st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[s], st[mt], 0, 0, 0);
     }
-  if constexpr (MASKED) {
+  if constexpr (MASKED && MASK == 0) {
+    // key = key0 + 4 hf + off with off = 32 mt + 8 (r / 4) + r % 4 a constant
+    // per register: one compare against the lane's last visible key
+    const int lim = (CAUSAL ? min(qi, S - 1) : S - 1) - key0 - 4 * hf;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int off = 32 * mt + 8 * (r >> 2) + (r & 3);
+        st[mt][r] = off <= lim ? st[mt][r] : -INFINITY;
+      }
+  } else if constexpr (MASKED) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1300,10 +1311,13 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     // equal share of the key tiles, and a merge pass.  HYDRA_ATTN_SCHED=
     // streamk or kp forces the V^T choice; HYDRA_ATTN_WGS=n forces stream-K
     // on n workgroups, HYDRA_ATTN_WGS=0 one workgroup per item.
+    // Resident slots from the instantiation without a fixed reference max
+    // (FX 0) whichever runs: the workspace query sees no bound or
+    // temperature, so the schedule it sizes for must not depend on them.
     const int64_t slots = static_cast<int64_t>(device_cus()) *
                           blocks_per_cu(reinterpret_cast<const void*>(
-                                            vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FX>
-                                               : attn_fwd_mfma_kernel<HD, C, M, false, NW, FX>),
+                                            vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, 0>
+                                               : attn_fwd_mfma_kernel<HD, C, M, false, NW, 0>),
                                         64 * NW);
     const int64_t items = static_cast<int64_t>(nwg) * BH;
     const char* sched = getenv("HYDRA_ATTN_SCHED");
