@@ -715,6 +715,9 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_kernel(
       const uint16_t* Vs = Ks + L::ROWS;
       const uint16_t* Kt = Ks + 2 * L::ROWS;
       f32x16_t st[MT], dp[MT];
+      // MASKED: key = key0 + 4 hf + off, off = 32 mt + 8 (r / 4) + r % 4 a
+      // constant per register, visible iff off <= lim
+      const int lim = (CAUSAL ? min(qi, S - 1) : S - 1) - key0 - 4 * hf;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) { st[mt] = zero16(); dp[mt] = zero16(); }
 #pragma unroll
@@ -730,11 +733,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float p = __builtin_amdgcn_exp2f(fmaf(st[mt][r], scale_log2, -l2));
-          if constexpr (MASKED) {  // keys past S, and after the query when causal: P = 0
-            const int key = key0 + 32 * mt + 8 * (r >> 2) + 4 * hf + (r & 3);
-            const bool ok = key < S && (!CAUSAL || key <= qi);
-            p = ok ? p : 0.f;
-          }
+          if constexpr (MASKED)  // keys past S, and after the query when causal: P = 0
+            p = 32 * mt + 8 * (r >> 2) + (r & 3) <= lim ? p : 0.f;
           dp[mt][r] = p * (dp[mt][r] - dd);
         }
 #pragma unroll

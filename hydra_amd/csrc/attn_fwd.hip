@@ -1311,13 +1311,15 @@ static int launch_mfma(const void* q, const void* k, const void* v, void* o, flo
     // equal share of the key tiles, and a merge pass.  HYDRA_ATTN_SCHED=
     // streamk or kp forces the V^T choice; HYDRA_ATTN_WGS=n forces stream-K
     // on n workgroups, HYDRA_ATTN_WGS=0 one workgroup per item.
-    // Resident slots from the instantiation without a fixed reference max
-    // (FX 0) whichever runs: the workspace query sees no bound or
+    // Resident slots from one instantiation per (causal, mask mode) --
+    // without a key mask the one that picks its fixed-max path on the device
+    // (FX 2), whichever runs: the workspace query sees no bound or
     // temperature, so the schedule it sizes for must not depend on them.
+    constexpr int FXS = M == 0 ? 2 : 0;
     const int64_t slots = static_cast<int64_t>(device_cus()) *
                           blocks_per_cu(reinterpret_cast<const void*>(
-                                            vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, 0>
-                                               : attn_fwd_mfma_kernel<HD, C, M, false, NW, 0>),
+                                            vt ? attn_fwd_mfma_kernel<HD, C, M, true, NW, FXS>
+                                               : attn_fwd_mfma_kernel<HD, C, M, false, NW, FXS>),
                                         64 * NW);
     const int64_t items = static_cast<int64_t>(nwg) * BH;
     const char* sched = getenv("HYDRA_ATTN_SCHED");
