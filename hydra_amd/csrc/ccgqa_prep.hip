@@ -598,6 +598,19 @@ __device__ __forceinline__ void conv2_task(const bf16* wrow, int64_t wtap, int64
     case 16: return conv2_task_fixed<MT, NG, 16>(wrow, wtap, wmt, wstep, brow0, rs, acc);
     default: break;
   }
+  if constexpr (MT == 1) {
+    // head_dim <= 32 (one m-tile per task): the latent widths 192, 320,
+    // 384, 448 (the 1B preset: 28 heads of 16) and 512 get the pipelined
+    // weight stream too (at MT > 1 the longer unrolled bodies would spill)
+    switch (CS) {
+      case 12: return conv2_task_fixed<MT, NG, 12>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+      case 20: return conv2_task_fixed<MT, NG, 20>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+      case 24: return conv2_task_fixed<MT, NG, 24>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+      case 28: return conv2_task_fixed<MT, NG, 28>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+      case 32: return conv2_task_fixed<MT, NG, 32>(wrow, wtap, wmt, wstep, brow0, rs, acc);
+      default: break;
+    }
+  }
   for (int t = 0; t < 3; ++t)
     for (int c = 0; c < CS; ++c) {
 #pragma unroll
