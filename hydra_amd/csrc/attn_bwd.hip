@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 namespace hydra {
@@ -1002,6 +1003,60 @@ DkdvPlan plan_dkdv(int hd, int S, int G, int BHkv, bool causal) {
   return p;
 }
 
+// A side stream per device (default priority, non-blocking) with a fork and
+// a join event.  fork() makes the side stream wait for everything queued on
+// the caller's stream so far; finish() makes the caller's stream wait for
+// everything queued on the side stream since.  The lock, held from fork to
+// finish, serialises the sequences of concurrent callers on one device.
+// Inside a graph capture the pair is the usual cross-stream fork/join; the
+// stream and events are only created outside one (a capture's first call
+// runs on the caller's stream alone).
+struct SideStream {
+  std::unique_lock<std::mutex> lock;
+  hipStream_t stream = nullptr, main = nullptr;
+  hipEvent_t join = nullptr;
+
+  bool fork(hipStream_t st) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static hipStream_t streams[kMaxDevices] = {};
+    static hipEvent_t forks[kMaxDevices] = {}, joins[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    lock = std::unique_lock<std::mutex>(mu);
+    if (streams[dev] == nullptr) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+      hipStream_t s = nullptr;
+      hipEvent_t f = nullptr, j = nullptr;
+      if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return false;
+      if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+          hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+        if (f) (void)hipEventDestroy(f);
+        (void)hipStreamDestroy(s);
+        return false;
+      }
+      streams[dev] = s;
+      forks[dev] = f;
+      joins[dev] = j;
+    }
+    if (hipEventRecord(forks[dev], st) != hipSuccess ||
+        hipStreamWaitEvent(streams[dev], forks[dev], 0) != hipSuccess)
+      return false;
+    stream = streams[dev];
+    join = joins[dev];
+    main = st;
+    return true;
+  }
+  int finish() {
+    if (stream == nullptr) return HYDRA_OK;
+    if (hipEventRecord(join, stream) != hipSuccess || hipStreamWaitEvent(main, join, 0) != hipSuccess)
+      return fail(HYDRA_ERR_LAUNCH, "attn_bwd: joining the side stream failed");
+    stream = nullptr;
+    return HYDRA_OK;
+  }
+};
+
 template <int HD, bool CAUSAL>
 int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* part) {
   const float sl2 = a.scale * kLog2e;
@@ -1010,7 +1065,25 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* p
   const bf16* k = static_cast<const bf16*>(a.k);
   const bf16* v = static_cast<const bf16*>(a.v);
   const bf16* d = static_cast<const bf16*>(a.dout);
-  {
+  // dQ needs only the row-dot's outputs, so it runs on a side stream,
+  // concurrently with dK/dV: the two launches' causal tails (CUs whose
+  // workgroups are done while others still walk the longest key ranges)
+  // take each other's workgroups.
+  SideStream side;
+  const hipStream_t dq_st = side.fork(a.st) ? side.stream : a.st;
+  auto launch_dq = [&]() {
+    // An item is NW query tasks (32 query rows of one head) sharing each
+    // staged K/V tile.
+    constexpr int NW = kDqWaves;
+    const int ntasks = ((a.S + 31) / 32) * G;
+    const int items = (ntasks + NW - 1) / NW;
+    attn_bwd_dq_kernel<HD, CAUSAL, NW><<<dim3(static_cast<unsigned>(items * BHkv)), 64 * NW, 0, dq_st>>>(
+        q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dq), a.Hq, a.Hkv, a.S, G, ntasks, items,
+        a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2], a.dos[0],
+        a.dos[1], a.dos[2], a.dqs[0], a.dqs[1], a.dqs[2], sl2, a.scale);
+    return check_launch("attn_bwd: dq");
+  };
+  auto launch_dkdv = [&]() -> int {
     const DkdvPlan pl = plan_dkdv(HD, a.S, G, BHkv, CAUSAL);
     const dim3 grid(static_cast<unsigned>(pl.nwg * BHkv));
 #define HYDRA_DKDV(KBV, HGV)                                                                     \
@@ -1035,17 +1108,13 @@ int launch_mfma(const BwdArgs& a, const float* dvec, const float* lse2, float* p
       HYDRA_DKDV(4, 1)
     }
 #undef HYDRA_DKDV
-  }
-  // dQ: an item is NW query tasks (32 query rows of one head) sharing each
-  // staged K/V tile.
-  constexpr int NW = kDqWaves;
-  const int ntasks = ((a.S + 31) / 32) * G;
-  const int items = (ntasks + NW - 1) / NW;
-  attn_bwd_dq_kernel<HD, CAUSAL, NW><<<dim3(static_cast<unsigned>(items * BHkv)), 64 * NW, 0, a.st>>>(
-      q, k, v, d, dvec, lse2, static_cast<bf16*>(a.dq), a.Hq, a.Hkv, a.S, G, ntasks, items,
-      a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2], a.dos[0],
-      a.dos[1], a.dos[2], a.dqs[0], a.dqs[1], a.dqs[2], sl2, a.scale);
-  return check_launch("attn_bwd: dq");
+    return HYDRA_OK;
+  };
+  // every path joins the side stream back before returning
+  int rc = launch_dkdv();
+  if (rc == HYDRA_OK) rc = launch_dq();
+  const int rj = side.finish();
+  return rc != HYDRA_OK ? rc : rj;
 }
 
 template <typename T, int MAXD, bool CAUSAL, int MASK>
