@@ -1021,8 +1021,12 @@ struct SideStream {
     static std::mutex mu;
     static hipStream_t streams[kMaxDevices] = {};
     static hipEvent_t forks[kMaxDevices] = {}, joins[kMaxDevices] = {};
+    // Only for a stream of the current device (the side stream lives there).
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    hipDevice_t sdev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices ||
+        hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev)
+      return false;
     lock = std::unique_lock<std::mutex>(mu);
     if (streams[dev] == nullptr) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
