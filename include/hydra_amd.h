@@ -345,7 +345,11 @@ int hydra_attn_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int6
  * (8 * B * Hq * S bytes of row statistics, plus the dK/dV chunk partials
  * of long causal walks) comes from the caller: workspace_bytes >=
  * hydra_attn_bwd_workspace(...) for the same shapes; the library keeps no
- * memory between calls. */
+ * memory between calls.  On the MFMA path the dQ launch runs on a side
+ * stream of the library's (one per device, default priority), forked from
+ * `stream` after the row statistics and joined back before the call
+ * returns, so everything queued on `stream` afterwards (and a graph
+ * captured from it) sees all three gradients. */
 int hydra_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                    const void* grad_o, const float* lse, void* grad_q, void* grad_k,
                    void* grad_v, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hd,
