@@ -25,6 +25,7 @@
 //  * attn_bwd_dq_kernel: lanes own queries, as in the forward: S^T = K Q^T,
 //    dP^T = V dO^T, dQ^T += K^T dS^T; a step stages 64 keys of K and V
 //    (row-major) and K^T in LDS, shared by the 4 query tasks of an item.
+//    It runs on a side stream, concurrently with dK/dV (see SideStream).
 // The MFMA B operand of the PV-type products is taken straight from the
 // score accumulator registers; the A operand is read from the transposed
 // LDS tile in the same (register-order) permutation of the summed index.
