@@ -145,6 +145,31 @@ def test_attention_backward_query_chunks(cuda, monkeypatch, shape, causal):
     _check(first, q, k, v, go, causal, TOL[torch.bfloat16])
 
 
+def test_attention_backward_two_streams(cuda):
+    """Two backward calls queued on two user streams at once (both fork
+    their dQ launch onto the library's one side stream per device): each
+    equals the same call on the default stream, bit for bit."""
+    from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+
+    calls = []
+    for seed in (21, 22):
+        q, k, v, go = (t.to(cuda) for t in _inputs(2, 4, 1, 768, 64, torch.bfloat16, seed=seed))
+        out, lse = attention_forward(q, k, v, causal=True, want_lse=True)
+        calls.append((q, k, v, out, lse, go))
+    want = [attention_backward(*c[:5], c[5], causal=True) for c in calls]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    got = []
+    for st, c in zip(streams, calls):
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            got.append(attention_backward(*c[:5], c[5], causal=True))
+    torch.cuda.synchronize()
+    for g, w in zip(got, want):
+        for a, b in zip(g, w):
+            assert torch.equal(a, b)
+
+
 def test_attention_backward_in_hip_graph(cuda):
     """After one eager call (which sizes the library workspace), the backward
     captures into a HIP graph; three replays, with eager work and
