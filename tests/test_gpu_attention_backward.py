@@ -170,6 +170,49 @@ def test_attention_backward_two_streams(cuda):
             assert torch.equal(a, b)
 
 
+_CAPTURE_FIRST = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from hydra_amd.attention.backends.ccgqa.ops import attention_backward, attention_forward
+g = torch.Generator().manual_seed(31)
+q, k, v, go = (torch.randn(*sh, generator=g).to(torch.bfloat16).cuda()
+               for sh in ((2, 4, 512, 64), (2, 1, 512, 64), (2, 1, 512, 64), (2, 4, 512, 64)))
+out, lse = attention_forward(q, k, v, causal=True, want_lse=True)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph):  # the process's first backward call
+        got = attention_backward(q, k, v, out, lse, go, causal=True)
+torch.cuda.current_stream().wait_stream(side)
+torch.cuda.synchronize()
+want = attention_backward(q, k, v, out, lse, go, causal=True)
+for _ in range(3):
+    for t in got:
+        t.zero_()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(got, want))
+print("capture-first ok")
+"""
+
+
+def test_attention_backward_captured_as_first_call(cuda):
+    """A process whose first backward call is inside a graph capture (the
+    library creates its side stream only outside one, so that call runs on
+    the caller's stream alone): three replays equal the eager gradients."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST, root], capture_output=True, text=True,
+                         timeout=180)
+    assert res.returncode == 0 and "capture-first ok" in res.stdout, res.stdout[-2000:] + res.stderr[-2000:]
+
+
 def test_attention_backward_in_hip_graph(cuda):
     """After one eager call (which sizes the library workspace), the backward
     captures into a HIP graph; three replays, with eager work and
