@@ -1469,14 +1469,22 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(
   const int b = bh / Hq, h = bh - b * Hq;
   const int j = h / (Hq / Hkv);
   const int tid = threadIdx.x, row = tid / KL, kl = tid % KL;
+  // Above head_dim 64 a row's lanes also split the head dimension: lane
+  // pair (2i, 2i+1) takes keys i, i + KL/2, .. and the two halves of d, and
+  // adds its partial dot products with one shuffle (the whole q row and
+  // output accumulator per lane would not fit in registers).
+  constexpr int DS = HD > 64 ? 2 : 1;   // d-slices per row
+  constexpr int DH = HD / DS;           // dims per lane
+  constexpr int KLK = KL / DS;          // key lanes per row
+  const int dh = kl % DS, kln = kl / DS;
   const int s = sb * RW + row;
   const bool live = s < S;
   const float qscale = scale * kLog2e;
-  float qv[HD], acc[HD];
+  float qv[DH], acc[DH];
   {
-    const T* qr = q + b * qs0 + h * qs1 + static_cast<int64_t>(live ? s : 0) * qs2;
+    const T* qr = q + b * qs0 + h * qs1 + static_cast<int64_t>(live ? s : 0) * qs2 + dh * DH;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) {
+    for (int d = 0; d < DH; ++d) {
       qv[d] = to_f32(qr[d]) * qscale;
       acc[d] = 0.f;
     }
@@ -1532,11 +1540,11 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(
     if constexpr (PF) {
       if (t0 + TK < kend) prefetch(t0 + TK);
     }
-    float x[KPT];
+    float x[KPT * DS];
     float mt = m;
 #pragma unroll
-    for (int u = 0; u < KPT; ++u) {
-      const int kk = kl + KL * u;
+    for (int u = 0; u < KPT * DS; ++u) {
+      const int kk = kln + KLK * u;
       const int t = t0 + kk;
       bool vis = live && t < S;
       if (mask_mode == HYDRA_MASK_REFERENCE_SDPA) vis = vis && (t > s || Vis[kk] == 0);
@@ -1545,9 +1553,10 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(
         if (mask_mode == HYDRA_MASK_KEY_PADDING) vis = vis && Vis[kk] != 0;
       }
       float dot = 0.f;
-      const float* kr = Ks + kk * KP;
+      const float* kr = Ks + kk * KP + dh * DH;
 #pragma unroll
-      for (int d = 0; d < HD; ++d) dot = fmaf(qv[d], kr[d], dot);
+      for (int d = 0; d < DH; ++d) dot = fmaf(qv[d], kr[d], dot);
+      if constexpr (DS == 2) dot += __shfl_xor(dot, 1, KL);
       x[u] = vis ? dot : -INFINITY;
       mt = fmaxf(mt, x[u]);
     }
@@ -1556,39 +1565,39 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(
       const float alpha = __builtin_amdgcn_exp2f(m - mt);  // m = -inf -> 0
       l *= alpha;
 #pragma unroll
-      for (int d = 0; d < HD; ++d) acc[d] *= alpha;
+      for (int d = 0; d < DH; ++d) acc[d] *= alpha;
       m = mt;
     }
 #pragma unroll
-    for (int u = 0; u < KPT; ++u) {
+    for (int u = 0; u < KPT * DS; ++u) {
       const float pu = __builtin_amdgcn_exp2f(x[u] - m);  // -inf -> 0
       l += pu;
-      const float* vr = Vs + (kl + KL * u) * KP;
+      const float* vr = Vs + (kln + KLK * u) * KP + dh * DH;
 #pragma unroll
-      for (int d = 0; d < HD; ++d) acc[d] = fmaf(pu, vr[d], acc[d]);
+      for (int d = 0; d < DH; ++d) acc[d] = fmaf(pu, vr[d], acc[d]);
     }
   }
-  // merge the KL lanes of the row
+  // merge the key lanes of the row (lanes of one d-slice: offsets >= DS)
   float mg = m;
 #pragma unroll
-  for (int off = KL / 2; off > 0; off >>= 1) mg = fmaxf(mg, __shfl_xor(mg, off, KL));
+  for (int off = KL / 2; off >= DS; off >>= 1) mg = fmaxf(mg, __shfl_xor(mg, off, KL));
   const float f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mg);
   l *= f;
 #pragma unroll
-  for (int off = KL / 2; off > 0; off >>= 1) l += __shfl_xor(l, off, KL);
+  for (int off = KL / 2; off >= DS; off >>= 1) l += __shfl_xor(l, off, KL);
 #pragma unroll
-  for (int d = 0; d < HD; ++d) {
+  for (int d = 0; d < DH; ++d) {
     float a = acc[d] * f;
 #pragma unroll
-    for (int off = KL / 2; off > 0; off >>= 1) a += __shfl_xor(a, off, KL);
+    for (int off = KL / 2; off >= DS; off >>= 1) a += __shfl_xor(a, off, KL);
     acc[d] = a;
   }
   if (!live) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  T* orow = o + b * os0 + h * os1 + static_cast<int64_t>(s) * os2;
+  T* orow = o + b * os0 + h * os1 + static_cast<int64_t>(s) * os2 + dh * DH;
 #pragma unroll
-  for (int d = 0; d < HD; ++d)
-    if (d % KL == kl) orow[d] = from_f32<T>(acc[d] * inv);
+  for (int d = 0; d < DH; ++d)
+    if (d % KLK == kln) orow[d] = from_f32<T>(acc[d] * inv);
   if (lse && kl == 0)
     lse[(static_cast<int64_t>(b) * Hq + h) * S + s] = l > 0.f ? (mg + __log2f(l)) * kLn2 : -INFINITY;
 }
