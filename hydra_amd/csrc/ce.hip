@@ -112,27 +112,36 @@ __global__ __launch_bounds__(256) void ce_rows_reg_kernel(
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const T* x = logits + row * rs;
-  float v[NCH][E];
+  // The row's chunks stay in registers as loaded (16-bit types packed: 128
+  // VGPRs at 32 chunks, where unpacked floats would spill) and are widened
+  // where used.
+  uint4 raw[NCH];
+  auto chunk = [&](int c, float (&f)[E]) {
+    const int e = (c * 256 + tid) * E;
+    if (e < V) {
+      load16<T>(reinterpret_cast<const T*>(&raw[c]), f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) f[i] = -INFINITY;
+    }
+  };
   float m = -INFINITY, s = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int e = (c * 256 + tid) * E;
-    if (e < V) {
-      load16<T, true>(x + e, v[c]);  // read once: non-temporal
-    } else {
-#pragma unroll
-      for (int i = 0; i < E; ++i) v[c][i] = -INFINITY;
-    }
+    raw[c] = e < V ? ld16raw<true>(x + e) : make_uint4(0, 0, 0, 0);  // read once: non-temporal
   }
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    float cm = v[c][0] * kLog2e;
+    float v[E];
+    chunk(c, v);
+    float cm = v[0] * kLog2e;
 #pragma unroll
-    for (int i = 1; i < E; ++i) cm = fmaxf(cm, v[c][i] * kLog2e);
+    for (int i = 1; i < E; ++i) cm = fmaxf(cm, v[i] * kLog2e);
     if (cm == -INFINITY) continue;
     float cs = 0.f;
 #pragma unroll
-    for (int i = 0; i < E; ++i) cs += __builtin_amdgcn_exp2f(fmaf(v[c][i], kLog2e, -cm));
+    for (int i = 0; i < E; ++i) cs += __builtin_amdgcn_exp2f(fmaf(v[i], kLog2e, -cm));
     lse_merge(m, s, cm, cs);
   }
 #pragma unroll
@@ -163,10 +172,11 @@ __global__ __launch_bounds__(256) void ce_rows_reg_kernel(
   for (int c = 0; c < NCH; ++c) {
     const int e = (c * 256 + tid) * E;
     if (e < V) {
-      float o[E];
+      float v[E], o[E];
+      chunk(c, v);
 #pragma unroll
       for (int i = 0; i < E; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(v[c][i], kLog2e, -lse2));
+        const float p = __builtin_amdgcn_exp2f(fmaf(v[i], kLog2e, -lse2));
         o[i] = (p - (e + i == t ? 1.f : 0.f)) * sc;
       }
       store16<T, true>(g + e, o);
